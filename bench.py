@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""MoE layer benchmark on one MI355X.
+
+A step is one pass of the hot path over one batch of synthetic input: router (fp16 logits -> top-k), dispatch, fused
+gate/up GEMV + epilogue, down GEMV + combine, for the GLM-shaped layer (288 routed experts, top-8 sigmoid + bias, one
+shared expert, H 4096, I 1536, EXL3 3 bpw; decode batch of 1 token by default). Inputs and all 289 experts are resident
+in HBM before the timed region. Prints one JSON line.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "big-moe-small-box_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE layer µs/token (decode) + prefill tok/s; HBM GB/s & MFMA util vs peak"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def physical_cpus(limit):
+    """CPUs of this process, one per physical core first (the reference's lane rule: one lane thread per core)."""
+    allowed = sorted(os.sched_getaffinity(0))
+    first, sib, seen = [], [], set()
+    for c in allowed:
+        try:
+            core = open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id").read().strip()
+            pkg = open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id").read().strip()
+        except OSError:
+            core, pkg = str(c), "0"
+        if (pkg, core) in seen:
+            sib.append(c)
+        else:
+            seen.add((pkg, core))
+            first.append(c)
+    return (first + sib)[:limit], len(first)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
+    """The reference's CPU lane (ft_n135.h moe_forward4, built from the reference sources into oracle/_ref) on the same
+    routes, driven as the reference's cpu_forward drives it (nv2_host.cpp:1974-2003): experts in RAM, routes given (no
+    router), mode auto, the shared expert as a weight-1 job. Median of warm calls, whole-call wall time."""
+    import numpy as np
+    from oracle import oracle as O
+    R = O.ref_lane()
+    if R is None:
+        return None
+    cpus, ncores = physical_cpus(max_threads)
+    E1 = tab.E + (1 if tab.has_shared else 0)
+    sel = sel.cpu().numpy()
+    w = w.float().cpu().numpy()
+    T, k = sel.shape
+    if tab.has_shared:
+        sel = np.concatenate([sel, np.full((T, 1), tab.E, np.int64)], 1)
+        w = np.concatenate([w, np.ones((T, 1), np.float32)], 1)
+        k += 1
+    arr = (ctypes.c_int * len(cpus))(*cpus)
+    if R.ref_lane_create(tab.H, tab.I, E1, len(cpus), arr, 0.0) != 0:
+        return None
+    keep = []
+    tf = {0: 0, 1: 1, 2: 2}
+    try:
+        for e in sorted(set(sel.ravel().tolist())):
+            ex = tab.host_expert(e)
+            if any(f not in tf for f in ex["fmt"]):
+                return None
+            sc = [ex["suh"][0], ex["svh"][0], ex["suh"][1], ex["svh"][1], ex["suh"][2], ex["svh"][2]]
+            sc = [np.ascontiguousarray(a.view(np.uint16)) for a in sc]
+            keep += ex["tr"] + sc
+            R.ref_lane_set_expert(e, *[t.ctypes.data for t in ex["tr"]], *[a.ctypes.data for a in sc], *ex["fmt"])
+        x = np.random.default_rng(0).standard_normal((T, tab.H)).astype(np.float16).astype(np.float32)
+        si = np.ascontiguousarray(sel.astype(np.int32))
+        wf = np.ascontiguousarray(w)
+        out = np.zeros((T, tab.H), np.float32)
+        times = []
+        t_end = time.perf_counter() + budget_s
+        for i in range(10000):
+            t0 = time.perf_counter()
+            R.ref_lane_forward(x.ctypes.data, T, si.ctypes.data, wf.ctypes.data, k, out.ctypes.data, -1)
+            times.append(time.perf_counter() - t0)
+            if (i >= 60 and time.perf_counter() > t_end) or time.perf_counter() > t_end + budget_s:
+                break
+        med = statistics.median(times[10:] if len(times) > 20 else times)
+    finally:
+        R.ref_lane_destroy()
+    return {"value": T / med, "unit": "tokens/s", "cores": len(cpus), "kind": "reference",
+            "sample": f"{len(times)} calls of the same {T}-token layer call ({k} jobs per token incl. the shared "
+                      f"expert), median wall time {med * 1e6:.0f} us; moe_forward4 mode auto, {len(cpus)} threads "
+                      f"pinned one per physical core ({ncores} physical cores available), {cpu_model()}",
+            "us_per_layer": med * 1e6}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the layer shards by experts "
+              f"across GPUs only in design, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import bmx
+    from bmx import synth
+
+    dev = torch.device("cuda:0")
+    c = synth.CONFIGS[args.config]
+    T = args.tokens
+    log(f"bench: building {args.config} table (E={c['E']}, H={c['H']}, I={c['I']})")
+    tab = synth.table(args.config, seed=0, device=dev)
+    x, lg, bias = synth.inputs(args.config, T=T, seed=0, device=dev)
+    layer = bmx.MoELayer(tab, c["topk"], score=c["score"], bias=bias, n_group=c["n_group"],
+                         topk_group=c["topk_group"], renorm=c["renorm"], scale=c["scale"])
+    torch.cuda.synchronize()
+
+    def step():
+        return layer.forward(x, lg)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"bench: timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # per-stage timing with events on the launch stream (torch's current stream): gate/up (dominant) and down+combine
+    sel, w = layer.routing_fn(T, None, x, {"logits": lg})
+    rpg = bmx.lib().bmx_rows_per_group(T, 0)
+    routes = bmx.ops.dispatch(sel, tab.E, 0, tab.has_shared, rpg)
+    desc = layer.desc
+    need = bmx.lib().bmx_experts_workspace(ctypes.byref(desc), T, 0)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    y = torch.empty((routes.R, tab.H), dtype=torch.float32, device=dev)
+    out = torch.empty((T, tab.H), dtype=torch.float32, device=dev)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    L = bmx.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for i in range(args.steps + args.warmup):
+        e = evs[i - args.warmup] if i >= args.warmup else None
+        if e: e[0].record()
+        bmx._lib.check(L.bmx_moe_gate_up(ctypes.byref(desc), P(x), T, ctypes.byref(routes.struct), None, P(ws), need, 0, s))
+        if e: e[1].record()
+        bmx._lib.check(L.bmx_moe_down(ctypes.byref(desc), T, ctypes.byref(routes.struct), None, P(y), P(w), P(out), P(ws),
+                                      need, 0, s))
+        if e: e[2].record()
+    torch.cuda.synchronize()
+    gu_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    dn_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    experts = set(sel.cpu().numpy().ravel().tolist())
+    if tab.has_shared:
+        experts.add(tab.E)
+    gu_bytes = sum(tab.mat_bytes(e, 0) + tab.mat_bytes(e, 1) for e in experts)
+    dn_bytes = sum(tab.mat_bytes(e, 2) for e in experts)
+    q_bytes = gu_bytes + dn_bytes
+    gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
+    layer_gbps = q_bytes / (ms * 1e-3) / 1e9
+
+    cpu = None if args.no_cpu else cpu_baseline(tab, sel, w)
+    res = {
+        "metric": METRIC,
+        "value": round(T * 1e3 / ms, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: random EXL3 trellis codes, suh ~ U(0.5,1.5), svh ~ U(0.5,1.5)/sqrt(k), x ~ N(0,1) fp16, "
+                "router logits ~ N(0,1) fp16, bias ~ N(0,0.1); seed 0",
+        "config": {"workload": f"{args.config} decode layer: {c['E']} routed experts top-{c['topk']} "
+                               f"{'sigmoid+bias' if c['bias'] else 'softmax' if c['score'] == 0 else 'sigmoid'}"
+                               f"{' + 1 shared' if c['shared'] else ''}, H {c['H']}, I {c['I']}, EXL3 "
+                               f"{ {'c1': '4', 'c2': '3', 'c4': '3'}.get(args.config, 'mixed') } bpw",
+                   "tokens": T, "step": "router + dispatch + gate/up + down + combine"},
+        "us_per_token": round(ms * 1e3 / T, 3),
+        "us_per_layer": round(ms * 1e3, 3),
+        "quantized_bytes_per_layer": q_bytes,
+        "layer_hbm_gbps": round(layer_gbps, 1),
+        "stage_us": {"gate_up": round(gu_ms * 1e3, 3), "down_combine": round(dn_ms * 1e3, 3)},
+        "roofline": {"kernel": "k_gu (gate/up GEMV + epilogue)", "bound": "hbm", "achieved": round(gu_gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "algorithmic_bytes": gu_bytes},
+        "cpu_baseline": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()} if cpu else None),
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,83 @@
+"""ctypes binding of libbmx.so (include/bmx.h). The library is required: nothing here has a fallback."""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbmx.so")
+
+BMX_OK, BMX_ERR_ARG, BMX_ERR_HIP, BMX_ERR_WORKSPACE, BMX_ERR_UNSUPPORTED = 0, 1, 2, 3, 4
+TF_K2, TF_K25, TF_K3, TF_K4 = 0, 1, 2, 3
+TILE_BYTES = {TF_K2: 64, TF_K25: 80, TF_K3: 96, TF_K4: 128}
+SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
+PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+_I64 = ctypes.c_int64
+
+
+class Expert(ctypes.Structure):
+    _fields_ = [("tr", ctypes.c_uint64 * 3), ("suh", ctypes.c_uint64 * 3), ("svh", ctypes.c_uint64 * 3),
+                ("fmt", ctypes.c_int32 * 3), ("reserved", ctypes.c_int32)]
+
+
+class MoeDesc(ctypes.Structure):
+    _fields_ = [("H", ctypes.c_int32), ("I", ctypes.c_int32), ("E", ctypes.c_int32), ("topk", ctypes.c_int32),
+                ("first", ctypes.c_int64), ("act", ctypes.c_int32), ("gated", ctypes.c_int32),
+                ("act_limit", ctypes.c_float), ("experts", _P), ("shared", _P)]
+
+
+class Routes(ctypes.Structure):
+    _fields_ = [(n, _P) for n in ("counts", "offsets", "row_token", "row_slot", "inv", "uexp", "nuniq", "groups",
+                                  "ngroups")]
+
+
+# name -> (restype, argtypes): every symbol include/bmx.h declares
+SIGNATURES = {
+    "bmx_last_error": (ctypes.c_char_p, []),
+    "bmx_abi_version": (_I, []),
+    "bmx_tile_bytes": (_I, [_I]),
+    "bmx_exl3_dequant": (_I, [_P, _I, _I, _I, _P, _P]),
+    "bmx_router_topk": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _I64, _P, _P, _P]),
+    "bmx_groups_max": (_I, [_I, _I, _I, _I, _I]),
+    "bmx_dispatch_workspace": (_SZ, [_I, _I, _I]),
+    "bmx_dispatch": (_I, [_P, _I, _I, _I, _I64, _I, _I, ctypes.POINTER(Routes), _P, _SZ, _P]),
+    "bmx_moe_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
+    "bmx_moe_forward": (_I, [ctypes.POINTER(MoeDesc), _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
+    "bmx_rows_per_group": (_I, [_I, _I]),
+    "bmx_experts_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
+    "bmx_moe_experts": (_I, [ctypes.POINTER(MoeDesc), _P, _I, ctypes.POINTER(Routes), _P, _P, _P, _SZ, _I, _P]),
+    "bmx_moe_gate_up": (_I, [ctypes.POINTER(MoeDesc), _P, _I, ctypes.POINTER(Routes), _P, _P, _SZ, _I, _P]),
+    "bmx_moe_down": (_I, [ctypes.POINTER(MoeDesc), _I, ctypes.POINTER(Routes), _P, _P, _P, _P, _P, _SZ, _I, _P]),
+    "bmx_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libbmx.so. Raises if it is missing: the HIP library is the only implementation."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libbmx.so not built ({LIB_PATH}); run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+class BmxError(RuntimeError):
+    pass
+
+
+def check(rc, what=""):
+    if rc != BMX_OK:
+        msg = lib().bmx_last_error().decode(errors="replace")
+        raise BmxError(f"{what}: status {rc}: {msg}")
+    return rc

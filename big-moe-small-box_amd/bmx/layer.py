@@ -1,0 +1,86 @@
+"""MoELayer: the Python call surface the reference's engine sees at a layer's experts, on the HIP library.
+
+Names and argument meaning follow the reference:
+  routing_fn(bsz, cfg, z, params) -> (sel int64 [bsz, k], w fp16 [bsz, k])     exllamav3 BlockSparseMLP.routing_fn,
+                                                                                hooked at engine/tiers.py:707-726
+  layer(li, sel, w, z, bsz) -> (sel, w, cpu_flag)                               engine/nv2.py:374-437 (Nv2.layer)
+  run_bszN(z, sel, rw) -> out [bsz, H] fp32                                     exllamav3 bc.run_bszN, engine/nv2.py:634
+  cpu_split_combine(fhs, cpu_partial, cpu_pending, shape) -> fhs                engine/tiers.py:730-739
+  combine(fhs) -> fhs                                                           engine/nv2.py:489-493 (Nv2.combine)
+Every call enqueues on torch's current stream; nothing synchronises the host.
+"""
+import torch
+
+from . import _lib as L
+from . import ops
+
+
+class MoELayer:
+    def __init__(self, table, topk, first=0, score=L.SCORE_SIGMOID, bias=None, n_group=1, topk_group=1, renorm=True,
+                 scale=1.0, act=L.ACT_SILU, gated=True, act_limit=0.0, router_weight=None, slots=None, li=0):
+        self.table = table
+        self.num_experts_per_tok = topk
+        self.routing_first = first
+        self.num_local_experts = table.E
+        self.hidden_size, self.intermediate_size = table.H, table.I
+        self.score, self.bias, self.n_group, self.topk_group = score, bias, n_group, topk_group
+        self.renorm, self.scale = renorm, scale
+        self.act, self.gated, self.act_limit = act, gated, act_limit
+        self.router_weight = router_weight        # fp16 [H, E] or None (logits passed in params["logits"])
+        self.slots, self.li = slots, li           # optional ExpertSlots (expert-slot table) and this layer's index
+        self.desc = table.desc(topk, first, act, gated, act_limit)
+        self._ws = None
+        self.out_bszn = None
+
+    # ---- router ----
+    def router_logits(self, z):
+        if self.router_weight is None:
+            raise ValueError("MoELayer: no router weight; pass params['logits']")
+        return torch.matmul(z.view(-1, self.hidden_size), self.router_weight)
+
+    def routing_fn(self, bsz, cfg, z, params):
+        logits = params.get("logits") if params else None
+        if logits is None:
+            logits = self.router_logits(z)
+        logits = logits.view(bsz, -1).to(torch.float16).contiguous()
+        return ops.router_topk(logits, self.num_experts_per_tok, self.bias, self.n_group, self.topk_group, self.score,
+                               self.renorm, self.scale, self.routing_first)
+
+    # ---- engine hook: residency before the experts run ----
+    def layer(self, li, sel, w, z, bsz):
+        if self.slots is not None:
+            self.slots.step(li, sel)
+        return sel, w, False
+
+    # ---- experts + combine ----
+    def run_bszN(self, z, sel, rw, path=L.PATH_AUTO):
+        x = z.view(-1, self.hidden_size)
+        if x.dtype != torch.float16 or not x.is_contiguous():
+            x = x.half().contiguous()
+        sel = sel.view(x.shape[0], -1)
+        if sel.dtype != torch.int64 or not sel.is_contiguous():
+            sel = sel.long().contiguous()
+        rw = rw.view(x.shape[0], -1)
+        if rw.dtype != torch.float16 or not rw.is_contiguous():
+            rw = rw.half().contiguous()
+        desc = self.slots.desc(self.li) if self.slots is not None else self.desc
+        need = L.lib().bmx_moe_workspace(desc, x.shape[0], path)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        self.out_bszn = ops.moe_forward(desc, x, sel, rw, path, self._ws)
+        return self.out_bszn
+
+    def cpu_split_combine(self, fhs, cpu_partial=None, cpu_pending=False, shape=None):
+        if cpu_pending and cpu_partial is not None:
+            fhs = fhs + cpu_partial.to(fhs.dtype)
+        return fhs.view(shape) if shape is not None else fhs
+
+    def combine(self, fhs):
+        return fhs if fhs.is_contiguous() else fhs.contiguous()
+
+    def forward(self, z, logits=None, path=L.PATH_AUTO):
+        bsz = z.shape[0]
+        sel, w = self.routing_fn(bsz, None, z, {"logits": logits} if logits is not None else {})
+        sel, w, _ = self.layer(self.li, sel, w, z, bsz)
+        out = self.run_bszN(z, sel, w, path)
+        return self.cpu_split_combine(self.combine(out), None, False, None)

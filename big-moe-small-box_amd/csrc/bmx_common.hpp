@@ -1,0 +1,170 @@
+// Device-side building blocks shared by the bmx kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/bmx.h"
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace bmx {
+
+constexpr int WAVE = 64;
+constexpr float R_SCALE = 0.088388347648f;   // 1 / sqrt(128) in fp32 (engine/kernels/x16/x16_dev.cu:20)
+
+// ---- EXL3 trellis formats ------------------------------------------------------------------------------------------
+// Ring layout (engine/kernels/nv2/ft_n135.h:74-89; tests/gpu_dsv41_vbmi_tables.py:67-81): weight i of a 256-weight tile
+// adds d(i) = KA + bit (i & 15) of MASK bits to a ring of 256 K bits stored MSB-first in little-endian 32-bit words;
+// its 16-bit state is ring bits [S(i) - 16, S(i)), S = prefix sum of d. Weight -> position: the tensor-core fragment
+// order make_tc_perm (engine/kernels/nv2/ft_core.h:49-62).
+template <int F> struct Fmt;
+template <> struct Fmt<BMX_TF_K2>  { static constexpr int KA = 2, TB = 64;  static constexpr uint32_t MASK = 0x0000u; };
+template <> struct Fmt<BMX_TF_K25> { static constexpr int KA = 2, TB = 80;  static constexpr uint32_t MASK = 0xAAAAu; };
+template <> struct Fmt<BMX_TF_K3>  { static constexpr int KA = 3, TB = 96;  static constexpr uint32_t MASK = 0x0000u; };
+template <> struct Fmt<BMX_TF_K4>  { static constexpr int KA = 4, TB = 128; static constexpr uint32_t MASK = 0x0000u; };
+
+__host__ __device__ constexpr int popc16(uint32_t m)
+{
+    int c = 0;
+    for (int j = 0; j < 16; ++j) c += (m >> j) & 1u;
+    return c;
+}
+
+// S(i)
+template <int F> __host__ __device__ constexpr int ring_end(int i)
+{
+    int s = (i >> 4) * (16 * Fmt<F>::KA + popc16(Fmt<F>::MASK));
+    for (int j = 0; j <= (i & 15); ++j) s += Fmt<F>::KA + int((Fmt<F>::MASK >> j) & 1u);
+    return s;
+}
+
+__host__ inline int tile_bytes_of(int fmt)
+{
+    switch (fmt)
+    {
+        case BMX_TF_K2: return 64;
+        case BMX_TF_K25: return 80;
+        case BMX_TF_K3: return 96;
+        case BMX_TF_K4: return 128;
+        default: return -1;
+    }
+}
+
+// codebook constants: MUL1 (engine/kernels/nv2/ft_core.h:29); KINV = fp16 0x1eee, KBIAS = fp16 0xc931 (ft_core.h:38-39)
+constexpr uint32_t MUL1 = 0x83DCD12Du;
+constexpr uint32_t MUL1_LO = MUL1 & 0xffffu;           // 0xD12D
+constexpr uint32_t MUL1_HI_SHL16 = MUL1 & 0xffff0000u; // 0x83DC << 16
+constexpr uint32_t KINV_BITS = 0x1eeeu;
+constexpr uint32_t KBIAS_BITS = 0xc931u;
+constexpr uint32_t F16_1024 = 0x6400u;                 // fp16 bits of 1024.0: 1024 + s (s < 1024) is 0x6400 | s
+
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
+__device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, (f16)v); }
+
+// Codebook hash of one 16-bit state (only the low 16 bits of `st` are read; the bits above may hold anything):
+//   x = st * MUL1 mod 2^32 = st * 0xD12D + ((st * 0x83DC mod 2^16) << 16), then 0x6400 + bytesum(x) = fp16 bits of
+//   1024 + bytesum. Three full-rate VALU ops (v_pk_mul_lo_u16 writes the product into the high half, v_mad_u32_u16
+//   reads the low halves, v_dot4_u32_u8 sums the bytes).
+__device__ __forceinline__ uint32_t cb_index(uint32_t st, uint32_t ones)
+{
+    uint32_t t, x;
+    asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel_hi:[0,1]" : "=v"(t) : "v"(st), "s"(MUL1_HI_SHL16));
+    asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(st), "s"(MUL1_LO), "v"(t));
+    return __builtin_amdgcn_udot4(x, ones, F16_1024, false);
+}
+
+// two codebook indices (fp16 bits of 1024 + s) -> two fp16 weights RN16(fma(1024 + s, KINV, KBIAS)) (one rounding)
+__device__ __forceinline__ f16x2 cb_weights(uint32_t lo, uint32_t hi)
+{
+    const uint32_t p = (hi << 16) | lo;
+    const f16x2 kinv = __builtin_bit_cast(f16x2, (KINV_BITS << 16) | KINV_BITS);
+    const f16x2 kbias = __builtin_bit_cast(f16x2, (KBIAS_BITS << 16) | KBIAS_BITS);
+    return __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p), kinv, kbias);
+}
+
+// ---- 128-point Hadamard over a wave: lane l holds elements 2l, 2l + 1 --------------------------------------------------
+// Sylvester order, stages of span 1, 2, 4, ..., 64; at each stage the lower element of a pair becomes a + b and the upper
+// one a - b (engine/kernels/nv2/ft_core.h:90-95; the cross-lane butterfly of x16_dev.cu:31-129 adds the same pairs in
+// the same order). Results are bit-identical to the sequential form.
+__device__ __forceinline__ void had128_wave(float& v0, float& v1)
+{
+    const int lane = threadIdx.x & 63;
+    {
+        const float a = v0, b = v1;
+        v0 = a + b;
+        v1 = a - b;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1)
+    {
+        const float p0 = __shfl_xor(v0, m), p1 = __shfl_xor(v1, m);
+        if (lane & m) { v0 = p0 - v0; v1 = p1 - v1; }
+        else { v0 = v0 + p0; v1 = v1 + p1; }
+    }
+}
+
+// ---- fixed-sequence fp32 exp (the router's; the oracle evaluates the same sequence) ----------------------------------
+__device__ __forceinline__ float exp_fixed(float x)
+{
+    if (x != x) return x;
+    if (x > 88.72f) return __builtin_huge_valf();
+    if (x < -104.0f) return 0.0f;
+    const float n = __builtin_rintf(__fmul_rn(x, 1.44269504f));
+    float r = __builtin_fmaf(n, -0.693145751953125f, x);
+    r = __builtin_fmaf(n, -1.428606765330187e-06f, r);
+    float p = 1.98412698e-4f;
+    p = __builtin_fmaf(p, r, 1.38888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333333e-3f);
+    p = __builtin_fmaf(p, r, 4.16666667e-2f);
+    p = __builtin_fmaf(p, r, 1.66666667e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    const int n1 = ni / 2, n2 = ni - n1;
+    const float s1 = __builtin_bit_cast(float, (uint32_t)(n1 + 127) << 23);
+    const float s2 = __builtin_bit_cast(float, (uint32_t)(n2 + 127) << 23);
+    return __fmul_rn(__fmul_rn(p, s1), s2);
+}
+
+__device__ __forceinline__ float sigmoid_fixed(float x)
+{
+    const float e = exp_fixed(-x);
+    return __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
+}
+
+// ---- activations (exllamav3 act_gate semantics, engine/kernels/x16/x16_dev.cu:68-112) ----------------------------------
+__device__ __forceinline__ float act_gate(int act, int gated, float g, float u, float limit)
+{
+    if (act == BMX_ACT_SILU_OAI)
+    {
+        if (limit != 0.0f)
+        {
+            g = fminf(g, limit);
+            u = fminf(fmaxf(u, -limit), limit);
+        }
+        const float glu = g / (1.0f + __expf(-1.702f * g));
+        return (u + 1.0f) * glu;
+    }
+    float x;
+    if (!gated) x = fmaxf(0.0f, u);
+    else if (act == BMX_ACT_SILU) x = g / (1.0f + __expf(-g));
+    else if (act == BMX_ACT_GELU)
+    {
+        const float t = 0.797884560803f * (g + 0.044715f * g * g * g);
+        x = 0.5f * g * (1.0f + tanhf(t));
+    }
+    else { x = fmaxf(0.0f, g); x = x * x; }
+    if (limit != 0.0f)
+    {
+        u = fminf(fmaxf(u, -limit), limit);
+        x = fminf(x, limit);
+    }
+    return x * u;
+}
+
+}  // namespace bmx

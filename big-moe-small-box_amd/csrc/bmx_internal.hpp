@@ -1,0 +1,57 @@
+// Host-side internals shared by the bmx translation units: error state and kernel-launch entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/bmx.h"
+
+namespace bmx {
+
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// dequant.hip
+int launch_dequant(const void* trellis, int fmt, int k, int n, void* out, hipStream_t s);
+
+// router.hip
+int launch_router(const void* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,
+                  int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w, hipStream_t s);
+
+// dispatch.hip
+struct DispatchWs {
+    int32_t* rank;      // [T * topk]
+    int32_t* blk_hist;  // [nblk * (E + 1)]
+};
+size_t dispatch_ws_bytes(int T, int topk, int E);
+int launch_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int shared, int rows_per_group,
+                    const bmx_routes* out, void* ws, size_t ws_bytes, int32_t* zero_ptr, int zero_count,
+                    hipStream_t s);
+int groups_max(int T, int topk, int E, int shared, int rows_per_group);
+
+// moe_decode.hip
+struct MoeShape {
+    int H, I, E, topk, T, shared, act, gated;
+    float limit;
+    int64_t first;
+    const bmx_expert* experts;
+    const bmx_expert* shared_ex;
+};
+struct DecodePlan {
+    int KS_gu, KS_dn, NB, NBH, G_max, R_max;
+    size_t part_gu_bytes, part_dn_bytes, counters;   // counters: number of int32
+};
+DecodePlan decode_plan(const MoeShape& m);
+size_t decode_ws_bytes(const MoeShape& m);
+// ws layout: [counters][part_gu][part_dn][act rows (if act_out == NULL)]
+int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
+                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s,
+                          bool counters_zeroed, int stages);
+int decode_rows_per_group(int T);
+int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const int32_t* offsets, int T, int topk,
+                   int H, int E, int has_shared, float* out, hipStream_t s);
+int launch_zero_i32(int32_t* p, int n, hipStream_t s);
+
+}  // namespace bmx

@@ -1,0 +1,237 @@
+// C ABI of libbmx.so (include/bmx.h): argument checks, workspace layout, launch order.
+#include "bmx_common.hpp"
+#include "bmx_internal.hpp"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+namespace bmx {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char* what)
+{
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(BMX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return BMX_OK;
+}
+
+static int check_desc(const bmx_moe_desc* d, const char* who)
+{
+    if (!d) return set_error(BMX_ERR_ARG, "%s: null descriptor", who);
+    if (d->H <= 0 || d->I <= 0 || d->H % 128 || d->I % 128)
+        return set_error(BMX_ERR_ARG, "%s: H (%d) and I (%d) must be positive multiples of 128", who, d->H, d->I);
+    if (d->E <= 0 || d->E > 512 || d->topk <= 0 || d->topk > 32)
+        return set_error(BMX_ERR_ARG, "%s: unsupported E=%d topk=%d", who, d->E, d->topk);
+    if (!d->experts) return set_error(BMX_ERR_ARG, "%s: null expert table", who);
+    if (d->act < BMX_ACT_SILU || d->act > BMX_ACT_SILU_OAI) return set_error(BMX_ERR_ARG, "%s: unknown activation %d", who, d->act);
+    return BMX_OK;
+}
+
+static MoeShape shape_of(const bmx_moe_desc* d, int T)
+{
+    MoeShape m;
+    m.H = d->H; m.I = d->I; m.E = d->E; m.topk = d->topk; m.T = T; m.shared = d->shared ? 1 : 0;
+    m.act = d->act; m.gated = d->gated; m.limit = d->act_limit; m.first = d->first;
+    m.experts = d->experts; m.shared_ex = d->shared;
+    return m;
+}
+
+// routes carved from a workspace
+struct RoutesLayout {
+    size_t counts, offsets, row_token, row_slot, inv, uexp, nuniq, groups, ngroups, total;
+};
+
+static RoutesLayout routes_layout(int T, int topk, int E, int shared, int rpg)
+{
+    RoutesLayout L;
+    const size_t NE = (size_t)E + 1, R = (size_t)T * topk + (shared ? T : 0), G = (size_t)groups_max(T, topk, E, shared, rpg);
+    size_t o = 0;
+    auto take = [&](size_t bytes) { const size_t at = o; o += align_up(bytes, 256); return at; };
+    L.counts = take(NE * 4);
+    L.offsets = take((NE + 1) * 4);
+    L.row_token = take(R * 4 + 4);
+    L.row_slot = take(R * 4 + 4);
+    L.inv = take((size_t)T * topk * 4 + 4);
+    L.uexp = take(NE * 4);
+    L.nuniq = take(4);
+    L.groups = take(G * 12);
+    L.ngroups = take(4);
+    L.total = o;
+    return L;
+}
+
+static bmx_routes routes_at(char* base, const RoutesLayout& L)
+{
+    bmx_routes r;
+    r.counts = reinterpret_cast<int32_t*>(base + L.counts);
+    r.offsets = reinterpret_cast<int32_t*>(base + L.offsets);
+    r.row_token = reinterpret_cast<int32_t*>(base + L.row_token);
+    r.row_slot = reinterpret_cast<int32_t*>(base + L.row_slot);
+    r.inv = reinterpret_cast<int32_t*>(base + L.inv);
+    r.uexp = reinterpret_cast<int32_t*>(base + L.uexp);
+    r.nuniq = reinterpret_cast<int32_t*>(base + L.nuniq);
+    r.groups = reinterpret_cast<int32_t*>(base + L.groups);
+    r.ngroups = reinterpret_cast<int32_t*>(base + L.ngroups);
+    return r;
+}
+
+static int resolve_path(int path, int T)
+{
+    (void)T;
+    if (path == BMX_PATH_AUTO || path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL) return BMX_PATH_DECODE;
+    return -1;
+}
+
+}  // namespace bmx
+
+using namespace bmx;
+
+extern "C" {
+
+const char* bmx_last_error(void) { return g_err; }
+
+int bmx_abi_version(void) { return BMX_ABI_VERSION; }
+
+int bmx_tile_bytes(int fmt) { return tile_bytes_of(fmt); }
+
+int bmx_exl3_dequant(const void* trellis, int fmt, int k, int n, void* out_fp16, bmx_stream_t stream)
+{
+    if (k < 0 || n < 0 || k % 16 || n % 16) return set_error(BMX_ERR_ARG, "bmx_exl3_dequant: k (%d), n (%d) must be multiples of 16", k, n);
+    if (tile_bytes_of(fmt) < 0) return set_error(BMX_ERR_ARG, "bmx_exl3_dequant: unknown trellis format %d", fmt);
+    if ((k && n) && (!trellis || !out_fp16)) return set_error(BMX_ERR_ARG, "bmx_exl3_dequant: null pointer");
+    if (reinterpret_cast<uintptr_t>(trellis) % 16) return set_error(BMX_ERR_ARG, "bmx_exl3_dequant: trellis must be 16-byte aligned");
+    return launch_dequant(trellis, fmt, k, n, out_fp16, static_cast<hipStream_t>(stream));
+}
+
+int bmx_router_topk(const void* logits_fp16, const float* bias, int T, int E, int topk, int n_group, int topk_group,
+                    int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w_fp16, bmx_stream_t stream)
+{
+    return launch_router(logits_fp16, bias, T, E, topk, n_group, topk_group, score_fn, renorm, scale, first, sel,
+                         w_fp16, static_cast<hipStream_t>(stream));
+}
+
+int bmx_groups_max(int T, int topk, int E, int shared, int rows_per_group)
+{
+    if (T < 0 || topk <= 0 || E <= 0 || rows_per_group <= 0) return -1;
+    return groups_max(T, topk, E, shared, rows_per_group);
+}
+
+size_t bmx_dispatch_workspace(int T, int topk, int E) { return dispatch_ws_bytes(T, topk, E); }
+
+int bmx_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int shared, int rows_per_group,
+                 const bmx_routes* out, void* workspace, size_t workspace_bytes, bmx_stream_t stream)
+{
+    return launch_dispatch(sel, T, topk, E, first, shared, rows_per_group, out, workspace, workspace_bytes, nullptr, 0,
+                           static_cast<hipStream_t>(stream));
+}
+
+int bmx_rows_per_group(int T, int path)
+{
+    if (resolve_path(path, T) < 0 || T < 0) return -1;
+    return decode_rows_per_group(T);
+}
+
+size_t bmx_experts_workspace(const bmx_moe_desc* desc, int T, int path)
+{
+    if (check_desc(desc, "bmx_experts_workspace") || resolve_path(path, T) < 0 || T < 0) return 0;
+    return decode_ws_bytes(shape_of(desc, T));
+}
+
+int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, float* y_rows,
+                    void* act_rows_fp16, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream)
+{
+    int rc = check_desc(desc, "bmx_moe_experts");
+    if (rc) return rc;
+    if (resolve_path(path, T) < 0) return set_error(BMX_ERR_ARG, "bmx_moe_experts: unknown path %d", path);
+    if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_experts: T < 0");
+    if (T == 0) return BMX_OK;
+    if (!x_fp16 || !routes || !y_rows || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_experts: null pointer");
+    return launch_decode_experts(shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
+                                 nullptr, nullptr, static_cast<hipStream_t>(stream), false, 3);
+}
+
+int bmx_moe_gate_up(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, void* act_rows_fp16,
+                    void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream)
+{
+    int rc = check_desc(desc, "bmx_moe_gate_up");
+    if (rc) return rc;
+    if (resolve_path(path, T) < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_gate_up: bad path or T");
+    if (T == 0) return BMX_OK;
+    if (!x_fp16 || !routes || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_gate_up: null pointer");
+    return launch_decode_experts(shape_of(desc, T), x_fp16, routes, nullptr, act_rows_fp16, workspace, workspace_bytes,
+                                 nullptr, nullptr, static_cast<hipStream_t>(stream), true, 1);
+}
+
+int bmx_moe_down(const bmx_moe_desc* desc, int T, const bmx_routes* routes, const void* act_rows_fp16, float* y_rows,
+                 const void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream)
+{
+    int rc = check_desc(desc, "bmx_moe_down");
+    if (rc) return rc;
+    if (resolve_path(path, T) < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_down: bad path or T");
+    if (T == 0) return BMX_OK;
+    if (!routes || !y_rows || !workspace || (out && !w_fp16)) return set_error(BMX_ERR_ARG, "bmx_moe_down: null pointer");
+    return launch_decode_experts(shape_of(desc, T), nullptr, routes, y_rows, const_cast<void*>(act_rows_fp16), workspace,
+                                 workspace_bytes, out, w_fp16, static_cast<hipStream_t>(stream), true, 2);
+}
+
+int bmx_combine(const float* y_rows, const int32_t* inv, const void* w_fp16, const int32_t* offsets, int T, int topk,
+                int H, int E, int has_shared, float* out, bmx_stream_t stream)
+{
+    if (T < 0 || topk <= 0 || H <= 0 || E <= 0) return set_error(BMX_ERR_ARG, "bmx_combine: bad sizes");
+    if (T && (!y_rows || !inv || !w_fp16 || !out || (has_shared && !offsets)))
+        return set_error(BMX_ERR_ARG, "bmx_combine: null pointer");
+    return launch_combine(y_rows, inv, w_fp16, offsets, T, topk, H, E, has_shared, out, static_cast<hipStream_t>(stream));
+}
+
+size_t bmx_moe_workspace(const bmx_moe_desc* desc, int T, int path)
+{
+    if (check_desc(desc, "bmx_moe_workspace") || resolve_path(path, T) < 0 || T < 0) return 0;
+    const MoeShape m = shape_of(desc, T);
+    const int rpg = decode_rows_per_group(T);
+    const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
+    const size_t R = (size_t)T * desc->topk + (m.shared ? T : 0);
+    return L.total + align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256) + align_up(decode_ws_bytes(m), 256) +
+           align_up(R * desc->H * 4, 256);
+}
+
+int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const int64_t* sel, const void* w_fp16,
+                    float* out, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream)
+{
+    int rc = check_desc(desc, "bmx_moe_forward");
+    if (rc) return rc;
+    if (resolve_path(path, T) < 0) return set_error(BMX_ERR_ARG, "bmx_moe_forward: unknown path %d", path);
+    if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_forward: T < 0");
+    if (T == 0) return BMX_OK;
+    if (!x_fp16 || !sel || !w_fp16 || !out || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_forward: null pointer");
+    const size_t need = bmx_moe_workspace(desc, T, path);
+    if (workspace_bytes < need) return set_error(BMX_ERR_WORKSPACE, "bmx_moe_forward: workspace %zu < %zu", workspace_bytes, need);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const MoeShape m = shape_of(desc, T);
+    const int rpg = decode_rows_per_group(T);
+    const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
+    char* base = static_cast<char*>(workspace);
+    const bmx_routes r = routes_at(base, L);
+    char* dws = base + L.total;
+    const size_t dws_bytes = align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256);
+    char* ews = dws + dws_bytes;
+    const size_t ews_bytes = align_up(decode_ws_bytes(m), 256);
+    float* y_rows = reinterpret_cast<float*>(ews + ews_bytes);
+    const DecodePlan p = decode_plan(m);
+    rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes,
+                         reinterpret_cast<int32_t*>(ews), (int)p.counters, s);
+    if (rc) return rc;
+    return launch_decode_experts(m, x_fp16, &r, y_rows, nullptr, ews, ews_bytes, out, w_fp16, s, true, 3);
+}
+
+}  // extern "C"

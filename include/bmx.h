@@ -1,0 +1,151 @@
+/*
+ * bmx: MI355X-native (gfx950) routed-expert MoE layer. C ABI of libbmx.so.
+ *
+ * Every entry point is stream-ordered on the hipStream_t it is given (NULL = the legacy default stream), performs no
+ * host synchronisation and allocates nothing: the caller owns every buffer, including the workspace sized by the
+ * matching *_workspace() query. Pointers are device pointers unless stated. Status: BMX_OK or an error code; the text
+ * of the last error of the calling thread is bmx_last_error().
+ *
+ * Reference interfaces (Big-MoE-Small-Box, paths relative to src/bigmoe/) each entry point stands in for are cited
+ * beside it. The reference reaches its layer through exllamav3's BlockSparseMLP hooks (engine/tiers.py:703-739) and
+ * the pybind modules bigmoe_ec / bigmoe_nv2 (engine/ec.py:184-189, engine/kernels/nv2/nv2_host.cpp:2081-2139); this
+ * library is the native half of the same surface, reached from Python through ctypes (bmx/_lib.py).
+ */
+#ifndef BMX_H
+#define BMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BMX_ABI_VERSION 1
+
+typedef void* bmx_stream_t; /* hipStream_t */
+
+enum bmx_status {
+    BMX_OK = 0,
+    BMX_ERR_ARG = 1,         /* invalid argument (shape, format, null pointer, unsupported size) */
+    BMX_ERR_HIP = 2,         /* a HIP runtime call failed (launch, copy, event) */
+    BMX_ERR_WORKSPACE = 3,   /* workspace smaller than the matching *_workspace() query */
+    BMX_ERR_UNSUPPORTED = 4  /* valid request this build does not implement */
+};
+
+/* EXL3 trellis formats: the reference's TF_K2 / TF_K25 / TF_K3 numbering (engine/kernels/nv2/ft_n135.h:78-81) plus
+ * K 4. A tile is 16 x 16 weights in 32 K bytes; a matrix [k][n] is stored as tiles [k/16][n/16][32 K]. */
+enum bmx_trellis_fmt { BMX_TF_K2 = 0, BMX_TF_K25 = 1, BMX_TF_K3 = 2, BMX_TF_K4 = 3 };
+
+/* router score functions */
+enum bmx_score { BMX_SCORE_SOFTMAX = 0, BMX_SCORE_SIGMOID = 1 };
+
+/* expert activations, exllamav3's MOE_COOP_ACT_* numbering (engine/kernels/x16/x16_dev.cu:21-24) */
+enum bmx_act { BMX_ACT_SILU = 0, BMX_ACT_GELU = 1, BMX_ACT_RELU2 = 2, BMX_ACT_SILU_OAI = 3 };
+
+/* expert-products path */
+enum bmx_path { BMX_PATH_AUTO = 0, BMX_PATH_DECODE = 1, BMX_PATH_PREFILL = 2 };
+
+/* One expert: three EXL3 linears (gate [H->I], up [H->I], down [I->H]). Device-resident array, one entry per expert.
+ * tr[] is what the expert-slot table rewrites when an expert moves between its home and a VRAM slot (the reference's
+ * per-layer pointer tables multi_{gate,up,down}.ptrs_trellis, engine/tiers.py:321-340). suh / svh are fp16 [k] / [n]. */
+typedef struct bmx_expert {
+    uint64_t tr[3];
+    uint64_t suh[3];
+    uint64_t svh[3];
+    int32_t fmt[3];
+    int32_t reserved;
+} bmx_expert;
+
+/* One MoE layer's geometry (exllamav3 BlockSparseMLP attributes the engine reads: num_experts_per_tok,
+ * routing_first, num_local_experts, hidden_size, intermediate_size, activation_fn, act_limit, gated;
+ * engine/tiers.py:270-275, engine/x16.py:37-56). */
+typedef struct bmx_moe_desc {
+    int32_t H, I, E, topk;
+    int64_t first;               /* global id of local expert 0 (routing_first) */
+    int32_t act, gated;
+    float act_limit;             /* 0 = off */
+    const bmx_expert* experts;   /* device [E] */
+    const bmx_expert* shared;    /* device [1] or NULL: shared expert, weight 1, added after the routed slots */
+} bmx_moe_desc;
+
+/* Dispatch output: rows grouped per expert, stable by (expert, token, slot). R = T * topk (+ T with a shared expert,
+ * whose segment is expert index E). groups: work units of at most rows_per_group rows of one expert, [e, row0, nrows]. */
+typedef struct bmx_routes {
+    int32_t* counts;     /* [E + 1] rows per expert */
+    int32_t* offsets;    /* [E + 2] exclusive prefix of counts */
+    int32_t* row_token;  /* [R] token of each row */
+    int32_t* row_slot;   /* [R] slot k of each row (-1: shared expert) */
+    int32_t* inv;        /* [T * topk] row of pick (t, k); -1 = dropped pick (id outside [first, first + E)) */
+    int32_t* uexp;       /* [E + 1] experts with rows, ascending */
+    int32_t* nuniq;      /* [1] */
+    int32_t* groups;     /* [bmx_groups_max(...) * 3] */
+    int32_t* ngroups;    /* [1] */
+} bmx_routes;
+
+const char* bmx_last_error(void);
+int bmx_abi_version(void);
+int bmx_tile_bytes(int fmt);
+
+/* ---- EXL3 trellis dequantisation ----
+ * trellis [k/16][n/16][tile] -> fp16 [k][n] codebook weights, bit-exact with exllamav3's decode (the reference's CPU
+ * restatement: engine/kernels/nv2/ft_core.h:1007-1022 dense_weights; LinearEXL3.get_weight_tensor's trellis stage,
+ * called at engine/nv2.py:696). k, n multiples of 16. */
+int bmx_exl3_dequant(const void* trellis, int fmt, int k, int n, void* out_fp16, bmx_stream_t stream);
+
+/* ---- router ----
+ * exllamav3 routing_fn(bsz, cfg, z, params) -> (sel int64 [bsz, k], w fp16 [bsz, k]) as hooked at
+ * engine/tiers.py:707-726 and run at engine/nv2.py:473-487 (routing_ds3_nogroup: sigmoid + selection bias).
+ * logits fp16 [T, E]; bias fp32 [E] or NULL (selection only); n_group / topk_group = 1 / 1 for no group limit.
+ * Selection: softmax -> top-k of the logits; sigmoid -> top-k of sigmoid(l) + bias; groups -> DeepSeek-V3 group-limited
+ * (group score = sum of the top-2 choices, keep topk_group groups). Ties -> lower index. Weights: softmax probability or
+ * sigmoid score, renormalised over the picks when renorm, times scale, fp16. E <= 1024, topk <= 32. */
+int bmx_router_topk(const void* logits_fp16, const float* bias, int T, int E, int topk, int n_group, int topk_group,
+                    int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w_fp16,
+                    bmx_stream_t stream);
+
+/* ---- dispatch ----
+ * Token-to-expert counting sort (the histogram + ascending compaction of nv_pub_k, engine/kernels/nv2/
+ * nv2_dev.cu:23-95, as contiguous per-expert row segments). */
+int bmx_groups_max(int T, int topk, int E, int shared, int rows_per_group);
+size_t bmx_dispatch_workspace(int T, int topk, int E);
+int bmx_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int shared, int rows_per_group,
+                 const bmx_routes* out, void* workspace, size_t workspace_bytes, bmx_stream_t stream);
+
+/* ---- layer ----
+ * The routed experts of one layer call plus the combine: exllamav3's BC_BlockSparseMLP run_bszN(z, sel, rw) writing
+ * experts_cfg.out_bszn (engine/nv2.py:634-635) followed by cpu_split_combine (engine/tiers.py:730-739) and the
+ * reduction order of x16_red_k (engine/kernels/x16/x16_dev.cu:298-392).
+ * x fp16 [T, H]; sel int64 [T, topk], w fp16 [T, topk] (a router's output, or anything with dropped picks marked by
+ * ids outside [first, first + E) or weight 0); out fp32 [T, H] = sum over k of w * expert(x) + shared(x).
+ * Runs dispatch, the expert products (decode GEMV or prefill MFMA path) and the combine. */
+size_t bmx_moe_workspace(const bmx_moe_desc* desc, int T, int path);
+int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const int64_t* sel, const void* w_fp16,
+                    float* out, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
+
+/* Expert products only, on given routes (from bmx_dispatch with rows_per_group = bmx_rows_per_group(path)):
+ * y_rows fp32 [R, H] (expert output of each dispatch row), act_rows fp16 [R, I] (the rotated down input) or NULL. */
+int bmx_rows_per_group(int T, int path);
+size_t bmx_experts_workspace(const bmx_moe_desc* desc, int T, int path);
+int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, float* y_rows,
+                    void* act_rows_fp16, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
+
+/* The two halves of bmx_moe_experts, for callers that schedule or time them apart (exllamav3's kernel A and kernel B,
+ * docs/x16.md:38-54): gate_up writes the rotated fp16 down-input rows (act_rows, or the workspace's own copy when
+ * NULL); down reads them, writes y_rows and, when out != NULL, also combines into out with the routing weights w. Use
+ * the same workspace for both, gate_up first. The workspace must be zero-filled before its first use (its split
+ * counters reset themselves at the end of every call, so it stays ready). */
+int bmx_moe_gate_up(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, void* act_rows_fp16,
+                    void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
+int bmx_moe_down(const bmx_moe_desc* desc, int T, const bmx_routes* routes, const void* act_rows_fp16, float* y_rows,
+                 const void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
+
+/* Combine: out[t] = sum over k ascending of w[t, k] * y_rows[inv[t, k]] (picks with inv < 0 or w = 0 skipped), then
+ * + y_rows[offsets[E] + t] when has_shared (x16_red_k order, engine/kernels/x16/x16_dev.cu:354-384). */
+int bmx_combine(const float* y_rows, const int32_t* inv, const void* w_fp16, const int32_t* offsets, int T, int topk,
+                int H, int E, int has_shared, float* out, bmx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BMX_H */

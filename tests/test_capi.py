@@ -1,0 +1,69 @@
+"""The C ABI library loads, exports every entry point include/bmx.h declares, and rejects bad arguments on the host
+(no GPU work is launched by these calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "bmx.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bmx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for must in ("bmx_exl3_dequant", "bmx_router_topk", "bmx_dispatch", "bmx_moe_forward", "bmx_moe_experts",
+                 "bmx_combine", "bmx_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    import bmx
+    L = bmx.lib()
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, missing
+    # and the ctypes signatures cover them all
+    assert set(declared_functions()) <= set(bmx._lib.SIGNATURES)
+
+
+def test_host_side_checks():
+    import bmx
+    L = bmx.lib()
+    assert L.bmx_abi_version() == 1
+    assert [L.bmx_tile_bytes(f) for f in range(4)] == [64, 80, 96, 128] and L.bmx_tile_bytes(9) == -1
+    assert L.bmx_exl3_dequant(None, 7, 16, 16, None, None) == bmx._lib.BMX_ERR_ARG
+    assert b"format" in L.bmx_last_error()
+    assert L.bmx_exl3_dequant(None, 2, 15, 16, None, None) == bmx._lib.BMX_ERR_ARG
+    assert L.bmx_router_topk(None, None, 1, 2000, 8, 1, 1, 1, 1, 1.0, 0, None, None, None) == bmx._lib.BMX_ERR_ARG
+    assert L.bmx_router_topk(None, None, 1, 64, 8, 3, 1, 1, 1, 1.0, 0, None, None, None) == bmx._lib.BMX_ERR_ARG
+    d = bmx._lib.MoeDesc(4096, 1000, 8, 2, 0, 0, 1, 0.0, None, None)
+    assert L.bmx_moe_forward(ctypes.byref(d), None, 1, None, None, None, None, 0, 0, None) == bmx._lib.BMX_ERR_ARG
+    assert b"multiples of 128" in L.bmx_last_error()
+    assert L.bmx_rows_per_group(1, 0) == 1 and L.bmx_rows_per_group(3, 0) == 4 and L.bmx_rows_per_group(100, 0) == 8
+
+
+def test_workspace_queries():
+    import bmx
+    L = bmx.lib()
+    d = bmx._lib.MoeDesc(4096, 1536, 288, 8, 0, 0, 1, 0.0, ctypes.c_void_p(1), ctypes.c_void_p(2))
+    n1 = L.bmx_moe_workspace(ctypes.byref(d), 1, 0)
+    n8 = L.bmx_moe_workspace(ctypes.byref(d), 8, 0)
+    assert 0 < n1 < n8
+    assert L.bmx_groups_max(1, 8, 288, 1, 1) >= 9
+
+
+def test_geometry_known_answers():
+    """Slot geometry of the reference: tests/test_store.py:50-51 (3 x 4096 B trellis -> off_u 4096, off_d 8192,
+    slot 12288), GLM-5.3 (tests/test_engine.py:50-60: slot 9437184, off_u 3145728, off_d 6291456) and DeepSeek-V4.1
+    v2 layers (tests/test_engine.py:63-70: 11059200 / 3686400 / 7372800 at K 2.5, off_u 2949120 at K 2)."""
+    from bmx.experts import ExpertTable
+    assert ExpertTable.geometry(128, 128, [(0, 0, 0)]) == (4096, 8192, 12288)
+    assert ExpertTable.geometry(4096, 2048, [(2, 2, 2)]) == (3145728, 6291456, 9437184)
+    assert ExpertTable.geometry(5120, 2304, [(1, 1, 1)]) == (3686400, 7372800, 11059200)
+    assert ExpertTable.geometry(5120, 2304, [(0, 0, 0)])[0] == 2949120

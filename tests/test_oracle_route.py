@@ -1,0 +1,171 @@
+"""Pins the oracle's router, dispatch and expert-slot step by independent methods: numpy sorting of the closed forms,
+brute force over small cases, libm for exp, and invariants / hand-computed known answers for the CLOCK step."""
+import numpy as np
+import pytest
+
+
+def test_exp_fixed_accuracy(oracle):
+    xs = np.concatenate([np.linspace(-100, 88, 20001), np.array([0.0, -0.0, 1.0, -1.0, 1e-8, -1e-8])]).astype(np.float32)
+    got = np.array([oracle.exp32(v) for v in xs], np.float32)
+    want = np.exp(xs.astype(np.float64))
+    ok = want > np.finfo(np.float32).tiny
+    relerr = np.abs(got[ok] - want[ok]) / want[ok]
+    assert relerr.max() < 4 * 2.0 ** -23
+    assert oracle.exp32(-200.0) == 0.0 and np.isinf(oracle.exp32(100.0)) and oracle.exp32(0.0) == 1.0
+
+
+def _choice(oracle, lg, bias, score):
+    l = lg.astype(np.float32)
+    if score == oracle.SCORE_SOFTMAX:
+        return l, np.array([oracle.exp32(v - l.max()) for v in l], np.float32)
+    s = np.array([oracle.lib().bmxo_sigmoid(float(v)) for v in l], np.float32)
+    return (s + bias if bias is not None else s).astype(np.float32), s
+
+
+def _topk_order(vals, idx_ok):
+    """indices sorted by (value desc, index asc) restricted to idx_ok"""
+    cand = [i for i in range(len(vals)) if idx_ok[i]]
+    return sorted(cand, key=lambda i: (-float(vals[i]), i))
+
+
+@pytest.mark.parametrize("score", [0, 1])
+def test_router_plain_topk(oracle, score):
+    rng = np.random.default_rng(score)
+    T, E, k = 16, 64, 8
+    lg = rng.standard_normal((T, E)).astype(np.float16)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if score == 1 else None
+    sel, w = oracle.router(lg, k, bias=bias, score_fn=score, renorm=True, scale=2.5, first=3)
+    for t in range(T):
+        ch, sc = _choice(oracle, lg[t], bias, score)
+        want = _topk_order(ch, [True] * E)[:k]
+        assert (sel[t] - 3).tolist() == want
+        v = sc[want].astype(np.float64)
+        assert np.allclose(w[t].astype(np.float64), v / v.sum() * 2.5, rtol=2e-3)
+    if score == 0:   # softmax selection is the logits' top-k (monotone)
+        for t in range(T):
+            assert sorted((sel[t] - 3).tolist()) == sorted(np.argsort(-lg[t].astype(np.float64), kind="stable")[:k].tolist())
+
+
+def test_router_ties_lower_index(oracle):
+    lg = np.zeros((1, 16), np.float16)
+    lg[0, [3, 9, 12]] = 1.0
+    sel, _ = oracle.router(lg, 5, score_fn=oracle.SCORE_SIGMOID)
+    assert sel[0].tolist() == [3, 9, 12, 0, 1]
+    sel, w = oracle.router(lg, 4, score_fn=oracle.SCORE_SOFTMAX, renorm=False)
+    assert sel[0].tolist() == [3, 9, 12, 0]
+    p = np.exp(lg[0].astype(np.float64)); p /= p.sum()
+    assert np.allclose(w[0].astype(np.float64), p[[3, 9, 12, 0]], rtol=2e-3)
+
+
+def test_router_group_limited_vs_brute_force(oracle):
+    rng = np.random.default_rng(2)
+    T, E, G, TG, k = 24, 64, 8, 3, 6
+    lg = rng.standard_normal((T, E)).astype(np.float16)
+    bias = (rng.standard_normal(E) * 0.2).astype(np.float32)
+    sel, w = oracle.router(lg, k, bias=bias, n_group=G, topk_group=TG, score_fn=oracle.SCORE_SIGMOID, renorm=True)
+    gs = E // G
+    for t in range(T):
+        ch, sc = _choice(oracle, lg[t], bias, oracle.SCORE_SIGMOID)
+        gsc = []
+        for g in range(G):
+            top2 = sorted(ch[g * gs:(g + 1) * gs].tolist(), reverse=True)[:2]
+            gsc.append(np.float32(np.float32(top2[0]) + np.float32(top2[1])))
+        keep = sorted(range(G), key=lambda g: (-float(gsc[g]), g))[:TG]
+        ok = [e // gs in keep for e in range(E)]
+        want = _topk_order(ch, ok)[:k]
+        assert sel[t].tolist() == want
+        assert all((e // gs) in keep for e in sel[t])
+
+
+def test_router_selection_matters(oracle):
+    """Planted mistake check: with the bias omitted the selection changes for this seed."""
+    rng = np.random.default_rng(8)
+    lg = rng.standard_normal((8, 64)).astype(np.float16)
+    bias = (rng.standard_normal(64) * 0.5).astype(np.float32)
+    a, _ = oracle.router(lg, 8, bias=bias)
+    b, _ = oracle.router(lg, 8, bias=None)
+    assert not np.array_equal(a, b)
+
+
+def test_dispatch_vs_stable_argsort(oracle):
+    rng = np.random.default_rng(3)
+    T, k, E = 50, 6, 20
+    sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64) + 5
+    sel[3, 2] = 5 + E          # sentinel (dropped)
+    sel[7, 0] = -1             # masked
+    d = oracle.dispatch(sel, E, first=5, shared=True)
+    flat = (sel - 5).ravel()
+    valid = (flat >= 0) & (flat < E)
+    order = np.argsort(np.where(valid, flat, E + 10), kind="stable")[:valid.sum()]
+    assert d["row_token"][:valid.sum()].tolist() == (order // k).tolist()
+    assert d["row_slot"][:valid.sum()].tolist() == (order % k).tolist()
+    assert np.array_equal(d["counts"][:E], np.bincount(flat[valid], minlength=E))
+    assert d["counts"][E] == T and d["offsets"][E + 1] == valid.sum() + T
+    assert d["inv"][3, 2] == -1 and d["inv"][7, 0] == -1
+    inv = d["inv"].ravel()
+    assert np.array_equal(np.sort(inv[inv >= 0]), np.arange(valid.sum()))
+    assert d["row_token"][valid.sum():].tolist() == list(range(T))
+    assert d["uexp"].tolist() == sorted(set(flat[valid].tolist())) + [E]
+
+
+def test_dispatch_empty_and_all_dropped(oracle):
+    sel = np.full((4, 2), -1, np.int64)
+    d = oracle.dispatch(sel, 8)
+    assert d["nuniq"] == 0 and np.all(d["inv"] == -1) and d["offsets"][-1] == 0
+
+
+# ---- expert-slot table ----
+
+def _check_maps(st):
+    for s in range(st.S):
+        o = st.owner[s]
+        if o >= 0:
+            assert st.slotof[o] == s
+    for key in range(st.L * st.E):
+        s = st.slotof[key]
+        if s >= 0:
+            assert st.owner[s] == key
+
+
+def test_slot_step_known_answer(oracle):
+    st = oracle.SlotTable(L=2, E=8, S=3)
+    jobs, ev = st.step(0, [1, 4])          # empty table: 1 -> slot 0, 4 -> slot 1
+    assert jobs.tolist() == [[1, 0], [4, 1]] and ev.tolist() == [-1, -1]
+    assert st.stats.tolist() == [0, 2, 2, 0, 0]
+    jobs, ev = st.step(1, [2, 4])          # layer 1: 2 -> slot 2; 4: slots 0, 1 referenced (cleared), 2 pinned
+    assert jobs.tolist() == [[2, 2], [4, 0]] and ev.tolist() == [-1, 1]
+    # second miss: hand cleared refb of 0 and 1 on the way to slot 2 then wrapped to slot 0 (refb now clear)
+    assert st.slotof[1] == -1 and st.owner[0] == 8 + 4
+    jobs, ev = st.step(0, [4])             # hit: no jobs
+    assert jobs.size == 0 and st.stats[0] == 1
+    _check_maps(st)
+
+
+def test_slot_step_invariants_random(oracle):
+    rng = np.random.default_rng(0)
+    L, E, S = 4, 32, 20
+    st = oracle.SlotTable(L, E, S)
+    for it in range(300):
+        li = int(rng.integers(L))
+        sel = rng.choice(E, 6, replace=False)
+        before_pin_epoch = st.epoch + 1
+        jobs, ev = st.step(li, sel)
+        _check_maps(st)
+        # every pick is resident afterwards (6 picks <= S slots, each epoch pins at most 6)
+        for e in sel:
+            assert st.slotof[li * E + e] >= 0
+            assert st.pin[st.slotof[li * E + e]] == before_pin_epoch
+        # admitted experts were misses; victims were not picked this step
+        for (e, s), old in zip(jobs, ev):
+            assert e in sel
+            if old >= 0:
+                assert not (old // E == li and (old % E) in sel)
+    assert st.stats[0] + st.stats[1] == 300 * 6
+
+
+def test_slot_disabled_slots_never_used(oracle):
+    st = oracle.SlotTable(1, 16, 4)
+    st.pin[1] = -1
+    st.pin[3] = -1
+    jobs, _ = st.step(0, [0, 1, 2])
+    assert sorted(jobs[:, 1].tolist()) == [0, 2] and st.stats[3] == 1     # third miss: no victim
