@@ -62,6 +62,18 @@ constexpr uint32_t KINV_BITS = 0x1eeeu;
 constexpr uint32_t KBIAS_BITS = 0xc931u;
 constexpr uint32_t F16_1024 = 0x6400u;                 // fp16 bits of 1024.0: 1024 + s (s < 1024) is 0x6400 | s
 
+// global-memory views of generic pointers (addresses read from the expert table are generic; loading through a
+// global pointer gives global_load instead of flat_load, which would also count against the LDS wait counter)
+typedef const __attribute__((address_space(1))) uint32_t* gptr_u32;
+__device__ __forceinline__ uint32_t ldg_nt(const void* p, int i)
+{
+    return __builtin_nontemporal_load(reinterpret_cast<gptr_u32>(reinterpret_cast<uintptr_t>(p)) + i);
+}
+__device__ __forceinline__ uint32_t ldg(const void* p, int i)
+{
+    return reinterpret_cast<gptr_u32>(reinterpret_cast<uintptr_t>(p))[i];
+}
+
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, (f16)v); }
 

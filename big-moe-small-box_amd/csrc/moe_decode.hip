@@ -102,7 +102,7 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ mat, int t
     const uint8_t* p = mat + (size_t)(tr0 + h) * row_bytes + (size_t)(cb * 8 + t) * TB + s * (TB / 4);
     uint32_t Wn[NW];
 #pragma unroll
-    for (int i = 0; i < NW; ++i) Wn[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p) + i);
+    for (int i = 0; i < NW; ++i) Wn[i] = ldg_nt(p, i);
     for (int it = 0; it < ntr; it += 2)
     {
         uint32_t W[NW + 1];
@@ -113,7 +113,7 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ mat, int t
         {
             p += 2 * row_bytes;
 #pragma unroll
-            for (int i = 0; i < NW; ++i) Wn[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p) + i);
+            for (int i = 0; i < NW; ++i) Wn[i] = ldg_nt(p, i);
         }
         strip<F, MR>(W, xs + (tr0 + it + h - xtr0) * 8, xstride, acc, ones);
     }
@@ -217,8 +217,8 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu(GvArgs a)
         {
             const int tok = a.row_token[r0 + m];
             const int k = k0 + b * 128 + 2 * lane;
-            const uint32_t xv = *reinterpret_cast<const uint32_t*>(a.x + (size_t)tok * a.H + k);
-            const uint32_t sv = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k);
+            const uint32_t xv = ldg(a.x + (size_t)tok * a.H + k, 0);
+            const uint32_t sv = ldg(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k, 0);
             float v0 = h2f(xv & 0xffffu) * h2f(sv & 0xffffu), v1 = h2f(xv >> 16) * h2f(sv >> 16);
             had128_wave(v0, v1);
             val = (uint32_t)f2h(v0 * R_SCALE) | ((uint32_t)f2h(v1 * R_SCALE) << 16);
@@ -257,9 +257,9 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu(GvArgs a)
 
     // epilogue: one wave per token row, lane l holds columns 2l, 2l + 1
     const int col = cb * 128 + 2 * lane;
-    const uint32_t svg = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col);
-    const uint32_t svu = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col);
-    const uint32_t sud = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(ex.suh[2]) + col);
+    const uint32_t svg = ldg(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col, 0);
+    const uint32_t svu = ldg(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col, 0);
+    const uint32_t sud = ldg(reinterpret_cast<const uint16_t*>(ex.suh[2]) + col, 0);
     for (int m = wave; m < nr; m += GV_WAVES)
     {
         const float* rg = red + (0 * GV_WAVES) * MR * 128 + m * 128;
@@ -329,7 +329,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn(GvArgs a)
         return;
 
     const int col = cb * 128 + 2 * lane;
-    const uint32_t svd = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(ex.svh[2]) + col);
+    const uint32_t svd = ldg(reinterpret_cast<const uint16_t*>(ex.svh[2]) + col, 0);
     for (int m = wave; m < nr; m += GV_WAVES)
     {
         float v0 = red[m * 128 + 2 * lane], v1 = red[m * 128 + 2 * lane + 1];
