@@ -139,21 +139,54 @@ def main():
                          topk_group=c["topk_group"], renorm=c["renorm"], scale=c["scale"])
     torch.cuda.synchronize()
 
+    L = bmx.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    desc, router = layer.desc, layer.router
+    need = L.bmx_moe_layer_workspace(ctypes.byref(desc), T, 0)
+    lws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    sel_b = torch.empty((T, c["topk"]), dtype=torch.int64, device=dev)
+    w_b = torch.empty((T, c["topk"]), dtype=torch.float16, device=dev)
+    out_b = torch.empty((T, tab.H), dtype=torch.float32, device=dev)
+
     def step():
-        return layer.forward(x, lg)
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        bmx._lib.check(L.bmx_moe_layer(ctypes.byref(desc), ctypes.byref(router), P(x), P(lg), T, P(sel_b), P(w_b),
+                                       P(out_b), P(lws), need, 0, s), "bmx_moe_layer")
+
+    def timed(fn, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    log(f"bench: timing {args.steps} steps")
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
+    log(f"bench: timing {args.steps} steps (eager launches)")
+    ms_eager = timed(step, args.steps)
+    # the same call captured once into a HIP graph and replayed (no host launch cost per kernel)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
         step()
+    ref_out = out_b.clone()
+    for _ in range(args.warmup):
+        graph.replay()
+    log(f"bench: timing {args.steps} steps (graph replay)")
+    ms_graph = timed(graph.replay, args.steps)
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    if not torch.equal(out_b, ref_out):
+        raise RuntimeError("graph replay output differs from the eager call")
+    ms = min(ms_eager, ms_graph)
 
     # per-stage timing with events on the launch stream (torch's current stream): gate/up (dominant) and down+combine
-    sel, w = layer.routing_fn(T, None, x, {"logits": lg})
+    sel, w = sel_b.clone(), w_b.clone()
     rpg = bmx.lib().bmx_rows_per_group(T, 0)
     routes = bmx.ops.dispatch(sel, tab.E, 0, tab.has_shared, rpg)
     desc = layer.desc
@@ -162,8 +195,6 @@ def main():
     y = torch.empty((routes.R, tab.H), dtype=torch.float32, device=dev)
     out = torch.empty((T, tab.H), dtype=torch.float32, device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    L = bmx.lib()
-    P = lambda t: ctypes.c_void_p(t.data_ptr())
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     for i in range(args.steps + args.warmup):
         e = evs[i - args.warmup] if i >= args.warmup else None
@@ -205,6 +236,9 @@ def main():
                                f"{' + 1 shared' if c['shared'] else ''}, H {c['H']}, I {c['I']}, EXL3 "
                                f"{ {'c1': '4', 'c2': '3', 'c4': '3'}.get(args.config, 'mixed') } bpw",
                    "tokens": T, "step": "router + dispatch + gate/up + down + combine"},
+        "timing": "min of eager launches and HIP-graph replay of the same bmx_moe_layer call",
+        "us_per_layer_eager": round(ms_eager * 1e3, 3),
+        "us_per_layer_graph": round(ms_graph * 1e3, 3),
         "us_per_token": round(ms * 1e3 / T, 3),
         "us_per_layer": round(ms * 1e3, 3),
         "quantized_bytes_per_layer": q_bytes,

@@ -29,9 +29,14 @@ class MoeDesc(ctypes.Structure):
                 ("act_limit", ctypes.c_float), ("experts", _P), ("shared", _P)]
 
 
+class RouterDesc(ctypes.Structure):
+    _fields_ = [("score_fn", ctypes.c_int32), ("renorm", ctypes.c_int32), ("n_group", ctypes.c_int32),
+                ("topk_group", ctypes.c_int32), ("scale", ctypes.c_float), ("reserved", ctypes.c_int32), ("bias", _P)]
+
+
 class Routes(ctypes.Structure):
     _fields_ = [(n, _P) for n in ("counts", "offsets", "row_token", "row_slot", "inv", "uexp", "nuniq", "groups",
-                                  "ngroups")]
+                                  "ngroups", "row_expert")]
 
 
 # name -> (restype, argtypes): every symbol include/bmx.h declares
@@ -52,6 +57,8 @@ SIGNATURES = {
     "bmx_moe_gate_up": (_I, [ctypes.POINTER(MoeDesc), _P, _I, ctypes.POINTER(Routes), _P, _P, _SZ, _I, _P]),
     "bmx_moe_down": (_I, [ctypes.POINTER(MoeDesc), _I, ctypes.POINTER(Routes), _P, _P, _P, _P, _P, _SZ, _I, _P]),
     "bmx_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "bmx_moe_layer_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
+    "bmx_moe_layer": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
 }
 
 _lib = None

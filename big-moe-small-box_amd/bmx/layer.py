@@ -29,6 +29,8 @@ class MoELayer:
         self.router_weight = router_weight        # fp16 [H, E] or None (logits passed in params["logits"])
         self.slots, self.li = slots, li           # optional ExpertSlots (expert-slot table) and this layer's index
         self.desc = table.desc(topk, first, act, gated, act_limit)
+        self.router = L.RouterDesc(score, int(renorm), n_group, topk_group, scale, 0,
+                                   bias.data_ptr() if bias is not None else None)
         self._ws = None
         self.out_bszn = None
 
@@ -79,6 +81,18 @@ class MoELayer:
         return fhs if fhs.is_contiguous() else fhs.contiguous()
 
     def forward(self, z, logits=None, path=L.PATH_AUTO):
+        if logits is not None and self.slots is None:
+            # the whole call in one library entry (router + dispatch fused at decode sizes)
+            x = z.view(-1, self.hidden_size)
+            if x.dtype != torch.float16 or not x.is_contiguous():
+                x = x.half().contiguous()
+            lg = logits.view(x.shape[0], -1).to(torch.float16).contiguous()
+            need = L.lib().bmx_moe_layer_workspace(self.desc, x.shape[0], path)
+            if self._ws is None or self._ws.numel() < need:
+                self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+            out, self.sel, self.w = ops.moe_layer(self.desc, self.router, x, lg, path, self._ws)
+            self.out_bszn = out
+            return out
         bsz = z.shape[0]
         sel, w = self.routing_fn(bsz, None, z, {"logits": logits} if logits is not None else {})
         sel, w, _ = self.layer(self.li, sel, w, z, bsz)

@@ -62,9 +62,11 @@ class RoutesBuf:
         self.nuniq = torch.zeros(1, **i32)
         self.groups = torch.zeros(max(G, 1) * 3, **i32)
         self.ngroups = torch.zeros(1, **i32)
+        self.row_expert = torch.full((max(R, 1),), -1, **i32)
         self.T, self.topk, self.E, self.shared, self.R = T, topk, E, bool(shared), R
         self.struct = L.Routes(*[t.data_ptr() for t in (self.counts, self.offsets, self.row_token, self.row_slot,
-                                                          self.inv, self.uexp, self.nuniq, self.groups, self.ngroups)])
+                                                          self.inv, self.uexp, self.nuniq, self.groups, self.ngroups,
+                                                          self.row_expert)])
 
 
 def dispatch(sel, E, first=0, shared=False, rows_per_group=8):
@@ -115,3 +117,20 @@ def combine(y_rows, routes, w, H):
     check(lib().bmx_combine(_ptr(y_rows), _ptr(routes.inv), _ptr(w), _ptr(routes.offsets), T, topk, H, routes.E,
                             int(routes.shared), _ptr(out), _stream()), "bmx_combine")
     return out
+
+
+def moe_layer(desc, router, x, logits, path=L.PATH_AUTO, workspace=None):
+    """Router + dispatch + experts + combine from logits fp16 [T, E] -> (out fp32 [T, H], sel, w)."""
+    _need(x, torch.float16, "x"); _need(logits, torch.float16, "logits")
+    T = x.shape[0]
+    sel = torch.empty((T, desc.topk), dtype=torch.int64, device=x.device)
+    w = torch.empty((T, desc.topk), dtype=torch.float16, device=x.device)
+    out = torch.empty((T, desc.H), dtype=torch.float32, device=x.device)
+    if T == 0:
+        return out, sel, w
+    need = lib().bmx_moe_layer_workspace(ctypes.byref(desc), T, path)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    check(lib().bmx_moe_layer(ctypes.byref(desc), ctypes.byref(router), _ptr(x), _ptr(logits), T, _ptr(sel), _ptr(w),
+                              _ptr(out), _ptr(workspace), workspace.numel(), path, _stream()), "bmx_moe_layer")
+    return out, sel, w

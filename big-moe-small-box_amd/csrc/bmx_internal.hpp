@@ -20,6 +20,11 @@ int launch_dequant(const void* trellis, int fmt, int k, int n, void* out, hipStr
 int launch_router(const void* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,
                   int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w, hipStream_t s);
 
+bool route_dispatch_small_fits(int T, int E, int topk);
+int launch_route_dispatch_small(const void* logits, const float* bias, int T, int E, int topk, int n_group,
+                                int topk_group, int score_fn, int renorm, float scale, int64_t first, int64_t* sel,
+                                void* w, int shared, int rpg, const bmx_routes* routes, hipStream_t s);
+
 // dispatch.hip
 struct DispatchWs {
     int32_t* rank;      // [T * topk]
@@ -41,14 +46,13 @@ struct MoeShape {
 };
 struct DecodePlan {
     int KS_gu, KS_dn, NB, NBH, G_max, R_max;
-    size_t part_gu_bytes, part_dn_bytes, counters;   // counters: number of int32
+    size_t part_gu_bytes, part_dn_bytes, counters;
 };
 DecodePlan decode_plan(const MoeShape& m);
 size_t decode_ws_bytes(const MoeShape& m);
-// ws layout: [counters][part_gu][part_dn][act rows (if act_out == NULL)]
+// ws layout: [part_gu][part_dn][act rows (used when act_rows == NULL)]; stages: 1 = gate/up, 2 = down (+ combine)
 int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
-                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s,
-                          bool counters_zeroed, int stages);
+                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages);
 int decode_rows_per_group(int T);
 int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const int32_t* offsets, int T, int topk,
                    int H, int E, int has_shared, float* out, hipStream_t s);

@@ -49,7 +49,7 @@ static MoeShape shape_of(const bmx_moe_desc* d, int T)
 
 // routes carved from a workspace
 struct RoutesLayout {
-    size_t counts, offsets, row_token, row_slot, inv, uexp, nuniq, groups, ngroups, total;
+    size_t counts, offsets, row_token, row_slot, inv, uexp, nuniq, groups, ngroups, row_expert, total;
 };
 
 static RoutesLayout routes_layout(int T, int topk, int E, int shared, int rpg)
@@ -67,6 +67,7 @@ static RoutesLayout routes_layout(int T, int topk, int E, int shared, int rpg)
     L.nuniq = take(4);
     L.groups = take(G * 12);
     L.ngroups = take(4);
+    L.row_expert = take(R * 4 + 4);
     L.total = o;
     return L;
 }
@@ -83,6 +84,7 @@ static bmx_routes routes_at(char* base, const RoutesLayout& L)
     r.nuniq = reinterpret_cast<int32_t*>(base + L.nuniq);
     r.groups = reinterpret_cast<int32_t*>(base + L.groups);
     r.ngroups = reinterpret_cast<int32_t*>(base + L.ngroups);
+    r.row_expert = reinterpret_cast<int32_t*>(base + L.row_expert);
     return r;
 }
 
@@ -158,7 +160,7 @@ int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const b
     if (T == 0) return BMX_OK;
     if (!x_fp16 || !routes || !y_rows || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_experts: null pointer");
     return launch_decode_experts(shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
-                                 nullptr, nullptr, static_cast<hipStream_t>(stream), false, 3);
+                                 nullptr, nullptr, static_cast<hipStream_t>(stream), 3);
 }
 
 int bmx_moe_gate_up(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, void* act_rows_fp16,
@@ -170,7 +172,7 @@ int bmx_moe_gate_up(const bmx_moe_desc* desc, const void* x_fp16, int T, const b
     if (T == 0) return BMX_OK;
     if (!x_fp16 || !routes || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_gate_up: null pointer");
     return launch_decode_experts(shape_of(desc, T), x_fp16, routes, nullptr, act_rows_fp16, workspace, workspace_bytes,
-                                 nullptr, nullptr, static_cast<hipStream_t>(stream), true, 1);
+                                 nullptr, nullptr, static_cast<hipStream_t>(stream), 1);
 }
 
 int bmx_moe_down(const bmx_moe_desc* desc, int T, const bmx_routes* routes, const void* act_rows_fp16, float* y_rows,
@@ -182,7 +184,7 @@ int bmx_moe_down(const bmx_moe_desc* desc, int T, const bmx_routes* routes, cons
     if (T == 0) return BMX_OK;
     if (!routes || !y_rows || !workspace || (out && !w_fp16)) return set_error(BMX_ERR_ARG, "bmx_moe_down: null pointer");
     return launch_decode_experts(shape_of(desc, T), nullptr, routes, y_rows, const_cast<void*>(act_rows_fp16), workspace,
-                                 workspace_bytes, out, w_fp16, static_cast<hipStream_t>(stream), true, 2);
+                                 workspace_bytes, out, w_fp16, static_cast<hipStream_t>(stream), 2);
 }
 
 int bmx_combine(const float* y_rows, const int32_t* inv, const void* w_fp16, const int32_t* offsets, int T, int topk,
@@ -201,8 +203,8 @@ size_t bmx_moe_workspace(const bmx_moe_desc* desc, int T, int path)
     const int rpg = decode_rows_per_group(T);
     const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
     const size_t R = (size_t)T * desc->topk + (m.shared ? T : 0);
-    return L.total + align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256) + align_up(decode_ws_bytes(m), 256) +
-           align_up(R * desc->H * 4, 256);
+    (void)R;
+    return L.total + align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256) + align_up(decode_ws_bytes(m), 256);
 }
 
 int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const int64_t* sel, const void* w_fp16,
@@ -226,12 +228,49 @@ int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const i
     const size_t dws_bytes = align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256);
     char* ews = dws + dws_bytes;
     const size_t ews_bytes = align_up(decode_ws_bytes(m), 256);
-    float* y_rows = reinterpret_cast<float*>(ews + ews_bytes);
-    const DecodePlan p = decode_plan(m);
-    rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes,
-                         reinterpret_cast<int32_t*>(ews), (int)p.counters, s);
+    rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr, 0, s);
     if (rc) return rc;
-    return launch_decode_experts(m, x_fp16, &r, y_rows, nullptr, ews, ews_bytes, out, w_fp16, s, true, 3);
+    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, 3);
+}
+
+size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path) { return bmx_moe_workspace(desc, T, path); }
+
+int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
+                  int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
+                  bmx_stream_t stream)
+{
+    int rc = check_desc(desc, "bmx_moe_layer");
+    if (rc) return rc;
+    if (!router) return set_error(BMX_ERR_ARG, "bmx_moe_layer: null router descriptor");
+    if (resolve_path(path, T) < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: unknown path %d", path);
+    if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: T < 0");
+    if (T == 0) return BMX_OK;
+    if (!x_fp16 || !logits_fp16 || !sel || !w_fp16 || !out || !workspace)
+        return set_error(BMX_ERR_ARG, "bmx_moe_layer: null pointer");
+    const size_t need = bmx_moe_workspace(desc, T, path);
+    if (workspace_bytes < need) return set_error(BMX_ERR_WORKSPACE, "bmx_moe_layer: workspace %zu < %zu", workspace_bytes, need);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const MoeShape m = shape_of(desc, T);
+    const int rpg = decode_rows_per_group(T);
+    const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
+    char* base = static_cast<char*>(workspace);
+    const bmx_routes r = routes_at(base, L);
+    char* dws = base + L.total;
+    const size_t dws_bytes = align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256);
+    char* ews = dws + dws_bytes;
+    const size_t ews_bytes = align_up(decode_ws_bytes(m), 256);
+    if (route_dispatch_small_fits(T, desc->E, desc->topk))
+        rc = launch_route_dispatch_small(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group,
+                                         router->topk_group, router->score_fn, router->renorm, router->scale,
+                                         desc->first, sel, w_fp16, m.shared, rpg, &r, s);
+    else
+    {
+        rc = launch_router(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group, router->topk_group,
+                           router->score_fn, router->renorm, router->scale, desc->first, sel, w_fp16, s);
+        if (!rc) rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr, 0, s);
+    }
+    if (rc) return rc;
+    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, 3);
 }
 
 }  // extern "C"

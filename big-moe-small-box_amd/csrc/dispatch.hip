@@ -171,11 +171,17 @@ __global__ __launch_bounds__(DP_THREADS) void k_dispatch_single(DpArgs a)
             a.r.inv[p] = row;
             a.r.row_token[row] = p / a.topk;
             a.r.row_slot[row] = p % a.topk;
+            a.r.row_expert[row] = e;
         }
         else a.r.inv[p] = -1;
     }
     if (a.shared)
-        for (int t = tid; t < a.T; t += DP_THREADS) { a.r.row_token[off[E] + t] = t; a.r.row_slot[off[E] + t] = -1; }
+        for (int t = tid; t < a.T; t += DP_THREADS)
+        {
+            a.r.row_token[off[E] + t] = t;
+            a.r.row_slot[off[E] + t] = -1;
+            a.r.row_expert[off[E] + t] = E;
+        }
     if (wave == 0) emit_groups(base, off, NE, a.rpg, a.r.uexp, a.r.nuniq, a.r.groups, a.r.ngroups, nullptr);
 }
 
@@ -233,7 +239,12 @@ __global__ __launch_bounds__(DP_THREADS) void k_dispatch_scan(DpArgs a, int nblk
     for (int e = tid; e < NE; e += DP_THREADS) { a.r.counts[e] = cnt[e]; a.r.offsets[e] = off[e]; }
     if (tid == 0) a.r.offsets[NE] = off[NE];
     if (a.shared)
-        for (int t = tid; t < a.T; t += DP_THREADS) { a.r.row_token[off[E] + t] = t; a.r.row_slot[off[E] + t] = -1; }
+        for (int t = tid; t < a.T; t += DP_THREADS)
+        {
+            a.r.row_token[off[E] + t] = t;
+            a.r.row_slot[off[E] + t] = -1;
+            a.r.row_expert[off[E] + t] = E;
+        }
     if (tid < 64) emit_groups(cnt, off, NE, a.rpg, a.r.uexp, a.r.nuniq, a.r.groups, a.r.ngroups, nullptr);
 }
 
@@ -250,6 +261,7 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(DpArgs a)
     a.r.inv[p] = row;
     a.r.row_token[row] = p / a.topk;
     a.r.row_slot[row] = p % a.topk;
+    a.r.row_expert[row] = e;
 }
 
 int groups_max(int T, int topk, int E, int shared, int rpg)
@@ -275,7 +287,7 @@ int launch_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, i
     if (T < 0 || topk <= 0 || E <= 0 || E + 1 > DP_MAXNE || rpg <= 0)
         return set_error(BMX_ERR_ARG, "bmx_dispatch: unsupported sizes T=%d topk=%d E=%d rows_per_group=%d", T, topk, E, rpg);
     if (!out || !out->counts || !out->offsets || !out->row_token || !out->row_slot || !out->inv || !out->uexp ||
-        !out->nuniq || !out->groups || !out->ngroups || (T > 0 && !sel))
+        !out->nuniq || !out->groups || !out->ngroups || !out->row_expert || (T > 0 && !sel))
         return set_error(BMX_ERR_ARG, "bmx_dispatch: null pointer");
     if (ws_bytes < dispatch_ws_bytes(T, topk, E))
         return set_error(BMX_ERR_WORKSPACE, "bmx_dispatch: workspace %zu < %zu", ws_bytes, dispatch_ws_bytes(T, topk, E));

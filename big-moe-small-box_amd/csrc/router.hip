@@ -1,157 +1,226 @@
-// Router: one wavefront per token. Scores, optional group limit, top-k and weights, all in registers of one wave;
-// selections follow a strict total order (larger choice, then lower index), so they are independent of reduction order.
+// Router and decode-size route + dispatch.
+//
+// Selection by rank: every candidate counts the candidates that beat it under the strict total order (larger choice,
+// then lower index); rank < k selects it into slot `rank`. The group limit ranks the top-2 of each group the same way,
+// then the groups by their top-2 sums. All threads read the same LDS word at each step (broadcast), so a token costs
+// E LDS reads per thread and no serial reduction chain; the result is the order the oracle's sequential selection
+// produces, independent of scheduling.
 #include "bmx_common.hpp"
 #include "bmx_internal.hpp"
 
 namespace bmx {
 
-constexpr int RT_WAVES = 4;
-constexpr int RT_MAXJ = 16;          // experts per lane: E <= 1024
+constexpr int RT_THREADS = 1024;
+constexpr int RT_MAXE = 1024;
 constexpr int RT_MAXG = 64;
 constexpr int RT_MAXK = 32;
+constexpr int SM_MAXN = 256;       // picks of the fused decode kernel
 
 __device__ __forceinline__ float canon(float v) { return v != v ? -__builtin_huge_valf() : __fadd_rn(v, 0.0f); }
-
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) { return va > vb || (va == vb && ia < ib); }
 
-// wave-wide argmax of (v, i) under `better`; idx -1 = none. Every lane returns the winner.
-__device__ __forceinline__ void wave_best(float& v, int& i, float& s)
-{
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1)
-    {
-        const float ov = __shfl_xor(v, m), os = __shfl_xor(s, m);
-        const int oi = __shfl_xor(i, m);
-        const bool take = oi >= 0 && (i < 0 || better(ov, oi, v, i));
-        if (take) { v = ov; i = oi; s = os; }
-    }
-}
+struct RouterArgs {
+    const uint16_t* logits;
+    const float* bias;
+    int T, E, topk, G, TG, score_fn, renorm;
+    float scale;
+    int64_t first;
+    int64_t* sel;
+    uint16_t* w;
+};
 
-template <int J>
-__global__ __launch_bounds__(RT_WAVES * 64) void k_router(const uint16_t* __restrict__ logits, const float* __restrict__ bias,
-                                                          int T, int E, int topk, int G, int TG, int score_fn, int renorm,
-                                                          float scale, int64_t first, int64_t* __restrict__ sel,
-                                                          uint16_t* __restrict__ wout)
+struct RouteShared {
+    float ch[RT_MAXE], sc[RT_MAXE];
+    float gtop[RT_MAXG][2], gsc[RT_MAXG];
+    int gok[RT_MAXG];
+    int idx[RT_MAXK];
+    float wmax[RT_THREADS / 64];
+};
+
+// Route token t with threads [tid0, tid0 + E) of the workgroup (one thread per expert). Writes sel / w of the token and
+// leaves the local picks in S.idx. Every thread of the workgroup must call it (it synchronises).
+__device__ void route_token(const RouterArgs& a, int t, RouteShared& S)
 {
-    __shared__ float sh_sc[RT_WAVES][J * 64];
-    __shared__ float sh_g[RT_WAVES][RT_MAXG];
-    __shared__ int sh_idx[RT_WAVES][RT_MAXK];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = blockIdx.x * RT_WAVES + wave;
-    if (t >= T) return;
-    const uint16_t* lg = logits + (size_t)t * E;
-    float sc[J], ch[J];
-    float mx = -__builtin_huge_valf();
-    if (score_fn == BMX_SCORE_SOFTMAX)
+    const int e = threadIdx.x, E = a.E;
+    const bool mine = e < E;
+    const uint16_t* lg = a.logits + (size_t)t * E;
+    float l = mine ? canon(h2f(lg[e])) : -__builtin_huge_valf();
+    float mx = 0.0f;
+    if (a.score_fn == BMX_SCORE_SOFTMAX)
     {
+        float v = l;
 #pragma unroll
-        for (int j = 0; j < J; ++j)
-        {
-            const int e = lane + 64 * j;
-            if (e < E) mx = fmaxf(mx, canon(h2f(lg[e])));
-        }
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+        for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+        if ((threadIdx.x & 63) == 0) S.wmax[threadIdx.x >> 6] = v;
+        __syncthreads();
+        mx = S.wmax[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, S.wmax[w]);
     }
-#pragma unroll
-    for (int j = 0; j < J; ++j)
+    if (mine)
     {
-        const int e = lane + 64 * j;
-        sc[j] = 0.0f;
-        ch[j] = -__builtin_huge_valf();
-        if (e < E)
+        if (a.score_fn == BMX_SCORE_SOFTMAX) { S.sc[e] = exp_fixed(__fsub_rn(l, mx)); S.ch[e] = l; }
+        else
         {
-            const float l = canon(h2f(lg[e]));
-            if (score_fn == BMX_SCORE_SOFTMAX) { sc[j] = exp_fixed(__fsub_rn(l, mx)); ch[j] = l; }
-            else
-            {
-                sc[j] = sigmoid_fixed(l);
-                ch[j] = canon(bias ? __fadd_rn(sc[j], bias[e]) : sc[j]);
-            }
-            sh_sc[wave][e] = sc[j];
+            const float s = sigmoid_fixed(l);
+            S.sc[e] = s;
+            S.ch[e] = canon(a.bias ? __fadd_rn(s, a.bias[e]) : s);
         }
     }
-    // group limit: group score = top1 + top2 choice of each group; keep the TG best groups
-    uint64_t gmask = ~0ull;
-    const int gs = E / G;
+    __syncthreads();
+    const int G = a.G, gs = E / G;
     if (G > 1)
     {
-        for (int g = 0; g < G; ++g)
+        if (mine)
         {
-            float v1 = 0.0f, s1 = 0.0f;
-            int i1 = -1;
-#pragma unroll
-            for (int j = 0; j < J; ++j)
-            {
-                const int e = lane + 64 * j;
-                if (e >= g * gs && e < (g + 1) * gs && (i1 < 0 || better(ch[j], e, v1, i1))) { v1 = ch[j]; i1 = e; }
-            }
-            wave_best(v1, i1, s1);
-            float v2 = 0.0f, s2 = 0.0f;
-            int i2 = -1;
-#pragma unroll
-            for (int j = 0; j < J; ++j)
-            {
-                const int e = lane + 64 * j;
-                if (e >= g * gs && e < (g + 1) * gs && e != i1 && (i2 < 0 || better(ch[j], e, v2, i2))) { v2 = ch[j]; i2 = e; }
-            }
-            wave_best(v2, i2, s2);
-            if (lane == 0) sh_g[wave][g] = canon(i2 >= 0 ? __fadd_rn(v1, v2) : v1);
+            const int g = e / gs;
+            const float c = S.ch[e];
+            int r = 0;
+            for (int q = g * gs; q < (g + 1) * gs; ++q) r += better(S.ch[q], q, c, e) ? 1 : 0;
+            if (r < 2) S.gtop[g][r] = c;
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        gmask = 0;
-        for (int r = 0; r < TG && r < G; ++r)
+        __syncthreads();
+        if (e < G) S.gsc[e] = canon(gs >= 2 ? __fadd_rn(S.gtop[e][0], S.gtop[e][1]) : S.gtop[e][0]);
+        __syncthreads();
+        if (e < G)
         {
-            int bg = -1;
-            for (int g = 0; g < G; ++g)
-                if (!((gmask >> g) & 1ull) && (bg < 0 || better(sh_g[wave][g], g, sh_g[wave][bg], bg))) bg = g;
-            gmask |= 1ull << bg;
+            int r = 0;
+            for (int q = 0; q < G; ++q) r += better(S.gsc[q], q, S.gsc[e], e) ? 1 : 0;
+            S.gok[e] = r < a.TG;
+        }
+        __syncthreads();
+    }
+    const bool allowed = mine && (G <= 1 || S.gok[e / gs]);
+    if (allowed)
+    {
+        const float c = S.ch[e];
+        int r = 0;
+        if (G <= 1)
+            for (int q = 0; q < E; ++q) r += better(S.ch[q], q, c, e) ? 1 : 0;
+        else
+            for (int q = 0; q < E; ++q) r += (S.gok[q / gs] && better(S.ch[q], q, c, e)) ? 1 : 0;
+        if (r < a.topk) S.idx[r] = e;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        float vsum = 0.0f;
+        for (int k = 0; k < a.topk; ++k) vsum = __fadd_rn(vsum, S.sc[S.idx[k]]);
+        float den = 1.0f;
+        if (a.score_fn == BMX_SCORE_SOFTMAX && !a.renorm)
+        {
+            den = 0.0f;
+            for (int q = 0; q < E; ++q) den = __fadd_rn(den, S.sc[q]);
+        }
+        else if (a.renorm) den = vsum;
+        for (int k = 0; k < a.topk; ++k)
+        {
+            const float v = S.sc[S.idx[k]];
+            const float qv = (a.score_fn == BMX_SCORE_SIGMOID && !a.renorm) ? v : __fdiv_rn(v, den);
+            a.sel[(size_t)t * a.topk + k] = (int64_t)S.idx[k] + a.first;
+            a.w[(size_t)t * a.topk + k] = f2h(__fmul_rn(qv, a.scale));
         }
     }
-    // top-k
-    uint32_t taken = 0;
-    float vsum = 0.0f;
-    for (int k = 0; k < topk; ++k)
+    __syncthreads();
+}
+
+// one workgroup per token
+__global__ __launch_bounds__(RT_THREADS) void k_router(RouterArgs a)
+{
+    __shared__ RouteShared S;
+    route_token(a, blockIdx.x, S);
+}
+
+// ---- fused decode kernel: route every token, then the counting sort of its picks, in one workgroup ------------------
+struct SmallDispatch {
+    int shared, rpg;
+    bmx_routes r;
+};
+
+__global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs a, SmallDispatch d)
+{
+    __shared__ RouteShared S;
+    __shared__ int pe[SM_MAXN];          // local expert of each pick (-1: dropped)
+    __shared__ int cnt[RT_MAXE + 1];
+    const int E = a.E, n = a.T * a.topk, tid = threadIdx.x;
+    for (int t = 0; t < a.T; ++t)
     {
-        float bv = 0.0f, bs = 0.0f;
-        int bi = -1;
-#pragma unroll
-        for (int j = 0; j < J; ++j)
+        route_token(a, t, S);
+        if (tid < a.topk) pe[t * a.topk + tid] = S.idx[tid];
+        __syncthreads();
+    }
+    const int NE = E + (d.shared ? 1 : 0);
+    // counts and offsets per expert
+    int nvalid = 0;
+    for (int e = tid; e < NE; e += blockDim.x)
+    {
+        int c = 0, below = 0;
+        if (e < E)
+            for (int p = 0; p < n; ++p) { c += pe[p] == e; below += pe[p] >= 0 && pe[p] < e; }
+        else
         {
-            const int e = lane + 64 * j;
-            const bool ok = e < E && !((taken >> j) & 1u) && (G <= 1 || ((gmask >> (e / gs)) & 1ull));
-            if (ok && (bi < 0 || better(ch[j], e, bv, bi))) { bv = ch[j]; bi = e; bs = sc[j]; }
+            c = a.T;
+            for (int p = 0; p < n; ++p) below += pe[p] >= 0;
         }
-        wave_best(bv, bi, bs);
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == 0) sh_idx[wave][k] = bi;
-        vsum = __fadd_rn(vsum, bs);
+        cnt[e] = c;
+        d.r.counts[e] = c;
+        d.r.offsets[e] = below;
+        if (e == NE - 1) d.r.offsets[NE] = below + c;
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    if (lane != 0) return;
-    float den = 1.0f;
-    if (score_fn == BMX_SCORE_SOFTMAX && !renorm)
+    for (int p = 0; p < n; ++p) nvalid += pe[p] >= 0;
+    __syncthreads();
+    // rows: stable by (expert, pick)
+    for (int p = tid; p < n; p += blockDim.x)
     {
-        den = 0.0f;
-        for (int e = 0; e < E; ++e) den = __fadd_rn(den, sh_sc[wave][e]);
+        const int e = pe[p];
+        if (e < 0) { d.r.inv[p] = -1; continue; }
+        int row = 0;
+        for (int q = 0; q < n; ++q) row += pe[q] >= 0 && (pe[q] < e || (pe[q] == e && q < p));
+        d.r.inv[p] = row;
+        d.r.row_token[row] = p / a.topk;
+        d.r.row_slot[row] = p % a.topk;
+        d.r.row_expert[row] = e;
     }
-    else if (renorm) den = vsum;
-    for (int k = 0; k < topk; ++k)
+    if (d.shared)
+        for (int t = tid; t < a.T; t += blockDim.x)
+        {
+            d.r.row_token[nvalid + t] = t;
+            d.r.row_slot[nvalid + t] = -1;
+            d.r.row_expert[nvalid + t] = E;
+        }
+    // used experts (ascending) and their groups of at most rpg rows
+    for (int e = tid; e < NE; e += blockDim.x)
     {
-        const int e = sh_idx[wave][k];
-        const float v = sh_sc[wave][e];
-        const float q = (score_fn == BMX_SCORE_SIGMOID && !renorm) ? v : __fdiv_rn(v, den);
-        sel[(size_t)t * topk + k] = (int64_t)e + first;
-        wout[(size_t)t * topk + k] = f2h(__fmul_rn(q, scale));
+        const int c = cnt[e];
+        if (!c) continue;
+        int ui = 0, g0 = 0, row0 = 0;
+        for (int q = 0; q < e; ++q)
+        {
+            const int cq = cnt[q];
+            ui += cq > 0;
+            g0 += (cq + d.rpg - 1) / d.rpg;
+            row0 += cq;
+        }
+        d.r.uexp[ui] = e;
+        for (int q = 0; q * d.rpg < c; ++q)
+        {
+            d.r.groups[3 * (g0 + q) + 0] = e;
+            d.r.groups[3 * (g0 + q) + 1] = row0 + q * d.rpg;
+            d.r.groups[3 * (g0 + q) + 2] = min(d.rpg, c - q * d.rpg);
+        }
+    }
+    if (tid == 0)
+    {
+        int nu = 0, ng = 0;
+        for (int q = 0; q < NE; ++q) { nu += cnt[q] > 0; ng += (cnt[q] + d.rpg - 1) / d.rpg; }
+        *d.r.nuniq = nu;
+        *d.r.ngroups = ng;
     }
 }
 
-int launch_router(const void* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,
-                  int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w, hipStream_t s)
+static int check_router(int T, int E, int topk, int n_group, int topk_group, int score_fn, const void* logits,
+                        const void* sel, const void* w)
 {
-    if (T < 0 || E <= 0 || E > RT_MAXJ * 64 || topk <= 0 || topk > RT_MAXK || topk > E)
+    if (T < 0 || E <= 0 || E > RT_MAXE || topk <= 0 || topk > RT_MAXK || topk > E)
         return set_error(BMX_ERR_ARG, "bmx_router_topk: unsupported sizes T=%d E=%d topk=%d", T, E, topk);
     if (n_group < 1 || n_group > RT_MAXG || E % n_group || topk_group < 1 || topk_group > n_group)
         return set_error(BMX_ERR_ARG, "bmx_router_topk: bad groups n_group=%d topk_group=%d (E=%d)", n_group, topk_group, E);
@@ -159,21 +228,49 @@ int launch_router(const void* logits, const float* bias, int T, int E, int topk,
         return set_error(BMX_ERR_ARG, "bmx_router_topk: topk %d exceeds the experts of %d groups", topk, topk_group);
     if (score_fn != BMX_SCORE_SOFTMAX && score_fn != BMX_SCORE_SIGMOID)
         return set_error(BMX_ERR_ARG, "bmx_router_topk: unknown score function %d", score_fn);
-    if (!logits || !sel || !w) return set_error(BMX_ERR_ARG, "bmx_router_topk: null pointer");
-    if (T == 0) return BMX_OK;
-    const dim3 grid((T + RT_WAVES - 1) / RT_WAVES), block(RT_WAVES * 64);
-    const uint16_t* lg = static_cast<const uint16_t*>(logits);
-    uint16_t* wo = static_cast<uint16_t*>(w);
-    const int J = (E + 63) / 64;
-#define BMX_RT(JJ) hipLaunchKernelGGL(k_router<JJ>, grid, block, 0, s, lg, bias, T, E, topk, n_group, topk_group, score_fn, \
-                                      renorm, scale, first, sel, wo)
-    if (J <= 1) BMX_RT(1);
-    else if (J <= 2) BMX_RT(2);
-    else if (J <= 4) BMX_RT(4);
-    else if (J <= 8) BMX_RT(8);
-    else BMX_RT(16);
-#undef BMX_RT
+    if (T > 0 && (!logits || !sel || !w)) return set_error(BMX_ERR_ARG, "bmx_router_topk: null pointer");
+    return BMX_OK;
+}
+
+static RouterArgs router_args(const void* logits, const float* bias, int T, int E, int topk, int n_group,
+                              int topk_group, int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w)
+{
+    RouterArgs a;
+    a.logits = static_cast<const uint16_t*>(logits); a.bias = bias; a.T = T; a.E = E; a.topk = topk; a.G = n_group;
+    a.TG = topk_group; a.score_fn = score_fn; a.renorm = renorm; a.scale = scale; a.first = first; a.sel = sel;
+    a.w = static_cast<uint16_t*>(w);
+    return a;
+}
+
+static unsigned router_threads(int E) { return (unsigned)((E + 63) / 64 * 64); }
+
+int launch_router(const void* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,
+                  int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w, hipStream_t s)
+{
+    int rc = check_router(T, E, topk, n_group, topk_group, score_fn, logits, sel, w);
+    if (rc || T == 0) return rc;
+    const RouterArgs a = router_args(logits, bias, T, E, topk, n_group, topk_group, score_fn, renorm, scale, first, sel, w);
+    hipLaunchKernelGGL(k_router, dim3((unsigned)T), dim3(router_threads(E)), 0, s, a);
     return check_launch("bmx_router_topk");
+}
+
+bool route_dispatch_small_fits(int T, int E, int topk) { return (long)T * topk <= SM_MAXN && E <= RT_MAXE; }
+
+int launch_route_dispatch_small(const void* logits, const float* bias, int T, int E, int topk, int n_group,
+                                int topk_group, int score_fn, int renorm, float scale, int64_t first, int64_t* sel,
+                                void* w, int shared, int rpg, const bmx_routes* routes, hipStream_t s)
+{
+    int rc = check_router(T, E, topk, n_group, topk_group, score_fn, logits, sel, w);
+    if (rc || T == 0) return rc;
+    if (!route_dispatch_small_fits(T, E, topk)) return set_error(BMX_ERR_ARG, "route+dispatch: too many picks (%d)", T * topk);
+    const RouterArgs a = router_args(logits, bias, T, E, topk, n_group, topk_group, score_fn, renorm, scale, first, sel, w);
+    SmallDispatch d;
+    d.shared = shared ? 1 : 0;
+    d.rpg = rpg;
+    d.r = *routes;
+    const unsigned nt = router_threads(E) > 256 ? router_threads(E) : 256;
+    hipLaunchKernelGGL(k_route_dispatch_small, dim3(1), dim3(nt), 0, s, a, d);
+    return check_launch("route + dispatch");
 }
 
 }  // namespace bmx

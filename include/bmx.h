@@ -81,6 +81,7 @@ typedef struct bmx_routes {
     int32_t* nuniq;      /* [1] */
     int32_t* groups;     /* [bmx_groups_max(...) * 3] */
     int32_t* ngroups;    /* [1] */
+    int32_t* row_expert; /* [R] expert of each row (E: shared expert) */
 } bmx_routes;
 
 const char* bmx_last_error(void);
@@ -123,6 +124,23 @@ size_t bmx_moe_workspace(const bmx_moe_desc* desc, int T, int path);
 int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const int64_t* sel, const void* w_fp16,
                     float* out, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
 
+/* Router settings of a layer (exllamav3 routing_cfg as the engine reads it: sigmoid / softmax scoring, selection bias
+ * e_score_correction_bias, n_group / topk_group, norm_topk_prob, routed_scaling_factor; engine/nv2.py:146-148). */
+typedef struct bmx_router_desc {
+    int32_t score_fn, renorm, n_group, topk_group;
+    float scale;
+    int32_t reserved;
+    const float* bias;      /* device fp32 [E] or NULL */
+} bmx_router_desc;
+
+/* The whole layer call from router logits: router + dispatch (one kernel at decode sizes), expert products, combine.
+ * The reference's per-layer sequence routing_fn -> Nv2.layer -> run_bszN -> cpu_split_combine (engine/tiers.py:707-739)
+ * with the expert arithmetic of exllamav3. sel int64 [T, topk] and w fp16 [T, topk] receive the routing. */
+size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path);
+int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
+                  int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
+                  bmx_stream_t stream);
+
 /* Expert products only, on given routes (from bmx_dispatch with rows_per_group = bmx_rows_per_group(path)):
  * y_rows fp32 [R, H] (expert output of each dispatch row), act_rows fp16 [R, I] (the rotated down input) or NULL. */
 int bmx_rows_per_group(int T, int path);
@@ -133,8 +151,7 @@ int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const b
 /* The two halves of bmx_moe_experts, for callers that schedule or time them apart (exllamav3's kernel A and kernel B,
  * docs/x16.md:38-54): gate_up writes the rotated fp16 down-input rows (act_rows, or the workspace's own copy when
  * NULL); down reads them, writes y_rows and, when out != NULL, also combines into out with the routing weights w. Use
- * the same workspace for both, gate_up first. The workspace must be zero-filled before its first use (its split
- * counters reset themselves at the end of every call, so it stays ready). */
+ * the same workspace for both, gate_up first. */
 int bmx_moe_gate_up(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, void* act_rows_fp16,
                     void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
 int bmx_moe_down(const bmx_moe_desc* desc, int T, const bmx_routes* routes, const void* act_rows_fp16, float* y_rows,
