@@ -78,24 +78,27 @@ __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_c
 __device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, (f16)v); }
 
 // Codebook hash of one 16-bit state (only the low 16 bits of `st` are read; the bits above may hold anything):
-//   x = st * MUL1 mod 2^32 = st * 0xD12D + ((st * 0x83DC mod 2^16) << 16), then 0x6400 + bytesum(x) = fp16 bits of
-//   1024 + bytesum. Three full-rate VALU ops (v_pk_mul_lo_u16 writes the product into the high half, v_mad_u32_u16
-//   reads the low halves, v_dot4_u32_u8 sums the bytes).
-__device__ __forceinline__ uint32_t cb_index(uint32_t st, uint32_t ones)
+//   x = st * MUL1 mod 2^32 = st * 0xD12D + ((st * 0x83DC mod 2^16) << 16)
+// in two full-rate VALU ops (v_pk_mul_lo_u16 writes the high product into the high half, v_mad_u32_u16 reads the low
+// halves).
+__device__ __forceinline__ uint32_t cb_hash(uint32_t st)
 {
     uint32_t t, x;
     asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel_hi:[0,1]" : "=v"(t) : "v"(st), "s"(MUL1_HI_SHL16));
     asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(st), "s"(MUL1_LO), "v"(t));
-    return __builtin_amdgcn_udot4(x, ones, F16_1024, false);
+    return x;
 }
 
-// two codebook indices (fp16 bits of 1024 + s) -> two fp16 weights RN16(fma(1024 + s, KINV, KBIAS)) (one rounding)
-__device__ __forceinline__ f16x2 cb_weights(uint32_t lo, uint32_t hi)
+// Two hashes -> two fp16 codebook weights RN16(fma(1024 + bytesum, KINV, KBIAS)) packed (lo = a, hi = b):
+// v_sad_u8 adds the bytes of xa to 0x64006400, v_sad_hi_u8 adds the bytes of xb shifted into the high half, so the
+// register holds the fp16 bits of 1024 + s_a and 1024 + s_b (s < 1024 never carries out of its half); one v_pk_fma_f16
+// then applies the affine map with a single rounding per weight.
+__device__ __forceinline__ f16x2 cb_pair(uint32_t xa, uint32_t xb)
 {
-    const uint32_t p = (hi << 16) | lo;
+    const uint32_t r = __builtin_amdgcn_sad_hi_u8(xb, 0u, __builtin_amdgcn_sad_u8(xa, 0u, (F16_1024 << 16) | F16_1024));
     const f16x2 kinv = __builtin_bit_cast(f16x2, (KINV_BITS << 16) | KINV_BITS);
     const f16x2 kbias = __builtin_bit_cast(f16x2, (KBIAS_BITS << 16) | KBIAS_BITS);
-    return __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p), kinv, kbias);
+    return __builtin_elementwise_fma(__builtin_bit_cast(f16x2, r), kinv, kbias);
 }
 
 // ---- 128-point Hadamard over a wave: lane l holds elements 2l, 2l + 1 --------------------------------------------------

@@ -22,8 +22,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ tr,
     p = ((p % NBITS) + NBITS) % NBITS;
     const uint32_t w0 = words[(p >> 5) % NW], w1 = words[((p >> 5) + 1) % NW];
     const uint32_t st = (uint32_t)((((uint64_t)w0 << 32) | w1) >> (48 - (p & 31))) & 0xffffu;
-    const uint32_t ci = cb_index(st, 0x01010101u);
-    const f16x2 w = cb_weights(ci, ci);
+    const uint32_t x = cb_hash(st);
+    const f16x2 w = cb_pair(x, x);
     const int g = i >> 3, j = i & 7;
     const int r = 2 * (g & 3) + ((j & 3) == 0 ? 0 : (j & 3) == 1 ? 1 : (j & 3) == 2 ? 8 : 9);
     const int c = (g >> 2) + (j >= 4 ? 8 : 0);

@@ -67,7 +67,7 @@ __device__ __forceinline__ uint32_t win_state(const uint32_t (&W)[NW1], int q)
 // with MR token rows. xr: LDS fp16 pairs of the strip's 16 input rows, 8 dwords per token row, token stride xstride.
 template <int F, int MR>
 __device__ __forceinline__ void strip(const uint32_t (&W)[Fmt<F>::TB / 16 + 1], const uint32_t* xr, int xstride,
-                                      float (&acc)[4][MR], uint32_t ones)
+                                      float (&acc)[4][MR])
 {
     constexpr RingTab<F> tab;
     uint32_t X[MR][8];
@@ -78,9 +78,7 @@ __device__ __forceinline__ void strip(const uint32_t (&W)[Fmt<F>::TB / 16 + 1], 
 #pragma unroll
     for (int jj = 0; jj < 64; jj += 2)
     {
-        const uint32_t i0 = cb_index(win_state(W, tab.q[jj]), ones);
-        const uint32_t i1 = cb_index(win_state(W, tab.q[jj + 1]), ones);
-        const f16x2 w2 = cb_weights(i0, i1);
+        const f16x2 w2 = cb_pair(cb_hash(win_state(W, tab.q[jj])), cb_hash(win_state(W, tab.q[jj + 1])));
         const int gg = jj >> 3, j = jj & 7;
         const int cidx = (gg >> 2) + (j >= 4 ? 2 : 0);
         const int dw = (gg & 3) + ((j & 2) ? 4 : 0);
@@ -98,7 +96,6 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ mat, int t
 {
     constexpr int TB = Fmt<F>::TB, NW = TB / 16;
     const int lane = threadIdx.x & 63, h = lane >> 5, t = (lane >> 2) & 7, s = lane & 3;
-    const uint32_t ones = 0x01010101u;
     const size_t row_bytes = (size_t)tn * TB;
     const uint8_t* p = mat + (size_t)(tr0 + h) * row_bytes + (size_t)(cb * 8 + t) * TB + s * (TB / 4);
     uint32_t Wn[NW];
@@ -116,7 +113,7 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ mat, int t
 #pragma unroll
             for (int i = 0; i < NW; ++i) Wn[i] = ldg_nt(p, i);
         }
-        strip<F, MR>(W, xs + (tr0 + it + h - xtr0) * 8, xstride, acc, ones);
+        strip<F, MR>(W, xs + (tr0 + it + h - xtr0) * 8, xstride, acc);
     }
 }
 
@@ -300,36 +297,48 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_epi(GvArgs a)
     *reinterpret_cast<float2*>(a.y_rows + (size_t)r * a.H + cb * 128 + 2 * lane) = make_float2(v0, v1);
 }
 
-// ---- down epilogue + combine: one wave per (token, 128-column block) --------------------------------------------------
+// ---- down epilogue + combine: one workgroup per (token, 128-column block) ---------------------------------------------
+// the slots' expert outputs are computed in parallel (wave w takes slots w, w + 4, ...), then wave 0 sums them:
 // out[t] = sum over k ascending of w[t, k] * y(inv[t, k]) (picks with inv < 0 or w = 0 skipped), then + y(shared row)
 // (engine/kernels/x16/x16_dev.cu:354-384)
+constexpr int CB_MAXK = 33;
 __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
 {
+    __shared__ float ys[CB_MAXK][128];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int u = blockIdx.x * GV_WAVES + wave;
-    const int t = u / a.NBH, cb = u % a.NBH;
-    if (t >= a.T) return;
+    const int t = blockIdx.x / a.NBH, cb = blockIdx.x % a.NBH;
+    const int ns = a.topk + (a.has_shared ? 1 : 0);
+    for (int k = wave; k < ns; k += GV_WAVES)
+    {
+        int r;
+        if (k < a.topk)
+        {
+            r = a.inv[t * a.topk + k];
+            if (r < 0 || h2f(a.w[t * a.topk + k]) == 0.0f) continue;
+        }
+        else r = a.offsets[a.E] + t;
+        float v0, v1;
+        down_out(a, r, cb, v0, v1);
+        if (a.y_rows) *reinterpret_cast<float2*>(a.y_rows + (size_t)r * a.H + cb * 128 + 2 * lane) = make_float2(v0, v1);
+        ys[k][2 * lane] = v0;
+        ys[k][2 * lane + 1] = v1;
+    }
+    __syncthreads();
+    if (wave) return;
     float o0 = 0.0f, o1 = 0.0f;
     for (int k = 0; k < a.topk; ++k)
     {
         const int r = a.inv[t * a.topk + k];
         const float wk = h2f(a.w[t * a.topk + k]);
         if (r < 0 || wk == 0.0f) continue;
-        float v0, v1;
-        down_out(a, r, cb, v0, v1);
-        if (a.y_rows) *reinterpret_cast<float2*>(a.y_rows + (size_t)r * a.H + cb * 128 + 2 * lane) = make_float2(v0, v1);
-        const float p0 = wk * v0, p1 = wk * v1;
+        const float p0 = wk * ys[k][2 * lane], p1 = wk * ys[k][2 * lane + 1];
         o0 = o0 + p0;
         o1 = o1 + p1;
     }
     if (a.has_shared)
     {
-        const int r = a.offsets[a.E] + t;
-        float v0, v1;
-        down_out(a, r, cb, v0, v1);
-        if (a.y_rows) *reinterpret_cast<float2*>(a.y_rows + (size_t)r * a.H + cb * 128 + 2 * lane) = make_float2(v0, v1);
-        o0 = o0 + v0;
-        o1 = o1 + v1;
+        o0 = o0 + ys[a.topk][2 * lane];
+        o1 = o1 + ys[a.topk][2 * lane + 1];
     }
     *reinterpret_cast<float2*>(a.out + (size_t)t * a.H + cb * 128 + 2 * lane) = make_float2(o0, o1);
 }
@@ -452,7 +461,7 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
     {
         hipLaunchKernelGGL((k_gemv_part<MR, 1>), dim3((unsigned)(p.G_max * p.NBH * p.KS_dn)), dim3(GV_THREADS), lds_dn, s, a);
         if (a.out)
-            hipLaunchKernelGGL(k_dn_combine, dim3((unsigned)((a.T * p.NBH + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+            hipLaunchKernelGGL(k_dn_combine, dim3((unsigned)(a.T * p.NBH)), dim3(GV_THREADS), 0, s, a);
         else
             hipLaunchKernelGGL(k_dn_epi, dim3((unsigned)((p.R_max * p.NBH + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
     }

@@ -56,6 +56,7 @@ __device__ void route_token(const RouterArgs& a, int t, RouteShared& S)
         mx = S.wmax[0];
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, S.wmax[w]);
     }
+    if (e >= E && e < ((E + 3) & ~3)) S.ch[e] = -__builtin_huge_valf();     // padding never beats a real expert
     if (mine)
     {
         if (a.score_fn == BMX_SCORE_SOFTMAX) { S.sc[e] = exp_fixed(__fsub_rn(l, mx)); S.ch[e] = l; }
@@ -95,9 +96,24 @@ __device__ void route_token(const RouterArgs& a, int t, RouteShared& S)
         const float c = S.ch[e];
         int r = 0;
         if (G <= 1)
-            for (int q = 0; q < E; ++q) r += better(S.ch[q], q, c, e) ? 1 : 0;
+        {
+#pragma unroll 4
+            for (int q = 0; q < E; q += 4)
+            {
+                const float4 v = *reinterpret_cast<const float4*>(&S.ch[q]);
+                r += (better(v.x, q, c, e) ? 1 : 0) + (better(v.y, q + 1, c, e) ? 1 : 0) +
+                     (better(v.z, q + 2, c, e) ? 1 : 0) + (better(v.w, q + 3, c, e) ? 1 : 0);
+            }
+        }
         else
-            for (int q = 0; q < E; ++q) r += (S.gok[q / gs] && better(S.ch[q], q, c, e)) ? 1 : 0;
+        {
+            for (int g = 0; g < G; ++g)
+            {
+                if (!S.gok[g]) continue;
+#pragma unroll 4
+                for (int q = g * gs; q < (g + 1) * gs; ++q) r += better(S.ch[q], q, c, e) ? 1 : 0;
+            }
+        }
         if (r < a.topk) S.idx[r] = e;
     }
     __syncthreads();
@@ -149,71 +165,80 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
         __syncthreads();
     }
     const int NE = E + (d.shared ? 1 : 0);
-    // counts and offsets per expert
+    __shared__ int firstocc[SM_MAXN];
+    // counts and offsets per expert (the shared segment last)
     int nvalid = 0;
+    for (int p = 0; p < n; ++p) nvalid += pe[p] >= 0;
     for (int e = tid; e < NE; e += blockDim.x)
     {
         int c = 0, below = 0;
         if (e < E)
-            for (int p = 0; p < n; ++p) { c += pe[p] == e; below += pe[p] >= 0 && pe[p] < e; }
-        else
-        {
-            c = a.T;
-            for (int p = 0; p < n; ++p) below += pe[p] >= 0;
-        }
+            for (int p = 0; p < n; ++p) { const int q = pe[p]; c += q == e; below += q >= 0 && q < e; }
+        else { c = a.T; below = nvalid; }
         cnt[e] = c;
         d.r.counts[e] = c;
         d.r.offsets[e] = below;
         if (e == NE - 1) d.r.offsets[NE] = below + c;
     }
-    for (int p = 0; p < n; ++p) nvalid += pe[p] >= 0;
+    for (int p = tid; p < n; p += blockDim.x)
+    {
+        const int e = pe[p];
+        int f = e >= 0;
+        for (int q = 0; q < p && f; ++q) f = pe[q] != e;
+        firstocc[p] = f;
+    }
     __syncthreads();
-    // rows: stable by (expert, pick)
+    // rows: stable by (expert, pick); per used expert (its first pick): list position and groups of <= rpg rows
+    int nu_r = 0, ng_r = 0;
+    for (int q = 0; q < n; ++q)
+        if (firstocc[q]) { ++nu_r; ng_r += (cnt[pe[q]] + d.rpg - 1) / d.rpg; }
     for (int p = tid; p < n; p += blockDim.x)
     {
         const int e = pe[p];
         if (e < 0) { d.r.inv[p] = -1; continue; }
-        int row = 0;
-        for (int q = 0; q < n; ++q) row += pe[q] >= 0 && (pe[q] < e || (pe[q] == e && q < p));
+        int row = 0, ui = 0, g0 = 0;
+        for (int q = 0; q < n; ++q)
+        {
+            const int eq = pe[q];
+            row += eq >= 0 && (eq < e || (eq == e && q < p));
+            if (firstocc[q] && eq < e) { ++ui; g0 += (cnt[eq] + d.rpg - 1) / d.rpg; }
+        }
         d.r.inv[p] = row;
         d.r.row_token[row] = p / a.topk;
         d.r.row_slot[row] = p % a.topk;
         d.r.row_expert[row] = e;
+        if (firstocc[p])
+        {
+            const int c = cnt[e], row0 = row;          // the expert's first row is its first pick's
+            d.r.uexp[ui] = e;
+            for (int q = 0; q * d.rpg < c; ++q)
+            {
+                d.r.groups[3 * (g0 + q) + 0] = e;
+                d.r.groups[3 * (g0 + q) + 1] = row0 + q * d.rpg;
+                d.r.groups[3 * (g0 + q) + 2] = min(d.rpg, c - q * d.rpg);
+            }
+        }
     }
     if (d.shared)
+    {
         for (int t = tid; t < a.T; t += blockDim.x)
         {
             d.r.row_token[nvalid + t] = t;
             d.r.row_slot[nvalid + t] = -1;
             d.r.row_expert[nvalid + t] = E;
         }
-    // used experts (ascending) and their groups of at most rpg rows
-    for (int e = tid; e < NE; e += blockDim.x)
-    {
-        const int c = cnt[e];
-        if (!c) continue;
-        int ui = 0, g0 = 0, row0 = 0;
-        for (int q = 0; q < e; ++q)
+        for (int q = tid; q * d.rpg < a.T; q += blockDim.x)
         {
-            const int cq = cnt[q];
-            ui += cq > 0;
-            g0 += (cq + d.rpg - 1) / d.rpg;
-            row0 += cq;
+            d.r.groups[3 * (ng_r + q) + 0] = E;
+            d.r.groups[3 * (ng_r + q) + 1] = nvalid + q * d.rpg;
+            d.r.groups[3 * (ng_r + q) + 2] = min(d.rpg, a.T - q * d.rpg);
         }
-        d.r.uexp[ui] = e;
-        for (int q = 0; q * d.rpg < c; ++q)
-        {
-            d.r.groups[3 * (g0 + q) + 0] = e;
-            d.r.groups[3 * (g0 + q) + 1] = row0 + q * d.rpg;
-            d.r.groups[3 * (g0 + q) + 2] = min(d.rpg, c - q * d.rpg);
-        }
+        if (tid == 0) d.r.uexp[nu_r] = E;
     }
     if (tid == 0)
     {
-        int nu = 0, ng = 0;
-        for (int q = 0; q < NE; ++q) { nu += cnt[q] > 0; ng += (cnt[q] + d.rpg - 1) / d.rpg; }
-        *d.r.nuniq = nu;
-        *d.r.ngroups = ng;
+        *d.r.nuniq = nu_r + (d.shared ? 1 : 0);
+        *d.r.ngroups = ng_r + (d.shared ? (a.T + d.rpg - 1) / d.rpg : 0);
     }
 }
 
