@@ -54,22 +54,27 @@ template <int F> struct RingTab {
     }
 };
 
-// 16-bit state at bit Q of a lane's window (MSB-first words); bits above 15 of the result are left as they are
-template <int NW1>
-__device__ __forceinline__ uint32_t win_state(const uint32_t (&W)[NW1], int q)
+// 16-bit state at bit q of a lane's window (MSB-first words: prev, own[0], own[1], ...); bits above 15 of the result
+// are left as they are
+template <int NW>
+__device__ __forceinline__ uint32_t win_state(uint32_t prev, const uint32_t (&own)[NW], int q)
 {
     const int d = q >> 5, o = q & 31;
-    if (o <= 16) return W[d] >> (16 - o);
-    return __builtin_amdgcn_alignbit(W[d], W[d + 1], 48 - o);
+    const uint32_t hi = d == 0 ? prev : own[d - 1];
+    if (o <= 16) return hi >> (16 - o);
+    return __builtin_amdgcn_alignbit(hi, own[d], 48 - o);
 }
 
 // One tile-row strip for this lane: 64 weights (stream positions 64 s .. 64 s + 63 of its tile) decoded and multiplied
 // with MR token rows. xr: LDS fp16 pairs of the strip's 16 input rows, 8 dwords per token row, token stride xstride.
 template <int F, int MR>
-__device__ __forceinline__ void strip(const uint32_t (&W)[Fmt<F>::TB / 16 + 1], const uint32_t* xr, int xstride,
+__device__ __forceinline__ void strip(const uint32_t (&own)[Fmt<F>::TB / 16], const uint32_t* xr, int xstride,
                                       float (&acc)[4][MR])
 {
+    constexpr int NW = Fmt<F>::TB / 16;
     constexpr RingTab<F> tab;
+    // previous lane's last word (quad_perm [3,0,1,2]: lane 0 of the tile takes lane 3's, the ring wraps)
+    const uint32_t prev = __builtin_amdgcn_mov_dpp(own[NW - 1], 0x93, 0xf, 0xf, false);
     uint32_t X[MR][8];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
@@ -78,7 +83,7 @@ __device__ __forceinline__ void strip(const uint32_t (&W)[Fmt<F>::TB / 16 + 1], 
 #pragma unroll
     for (int jj = 0; jj < 64; jj += 2)
     {
-        const f16x2 w2 = cb_pair(cb_hash(win_state(W, tab.q[jj])), cb_hash(win_state(W, tab.q[jj + 1])));
+        const f16x2 w2 = cb_pair(cb_hash(win_state(prev, own, tab.q[jj])), cb_hash(win_state(prev, own, tab.q[jj + 1])));
         const int gg = jj >> 3, j = jj & 7;
         const int cidx = (gg >> 2) + (j >= 4 ? 2 : 0);
         const int dw = (gg & 3) + ((j & 2) ? 4 : 0);
@@ -88,8 +93,16 @@ __device__ __forceinline__ void strip(const uint32_t (&W)[Fmt<F>::TB / 16 + 1], 
     }
 }
 
+template <int NW>
+__device__ __forceinline__ void load_words(uint32_t (&w)[NW], const uint8_t* p)
+{
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = ldg_nt(p, i);
+}
+
 // A wave's GEMV over tile-rows [tr0, tr0 + ntr) (ntr even; the two half-waves take alternate rows) of the 128-column
-// block cb of a matrix with tn tiles per row. xs: LDS input rows, dword (tr - xtr0) * 8 of each token row.
+// block cb of a matrix with tn tiles per row. xs: LDS input rows, dword (tr - xtr0) * 8 of each token row. Two register
+// sets alternate so the next strip's words are in flight while the current one is decoded.
 template <int F, int MR>
 __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ mat, int tn, int cb, int tr0, int ntr,
                                           const uint32_t* xs, int xstride, int xtr0, float (&acc)[4][MR])
@@ -98,23 +111,19 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ mat, int t
     const int lane = threadIdx.x & 63, h = lane >> 5, t = (lane >> 2) & 7, s = lane & 3;
     const size_t row_bytes = (size_t)tn * TB;
     const uint8_t* p = mat + (size_t)(tr0 + h) * row_bytes + (size_t)(cb * 8 + t) * TB + s * (TB / 4);
-    uint32_t Wn[NW];
-#pragma unroll
-    for (int i = 0; i < NW; ++i) Wn[i] = ldg_nt(p, i);
-    for (int it = 0; it < ntr; it += 2)
+    const uint32_t* xb = xs + (tr0 + h - xtr0) * 8;
+    uint32_t wa[NW], wb[NW];
+    load_words(wa, p);
+    int it = 0;
+    for (; it + 4 <= ntr; it += 4)
     {
-        uint32_t W[NW + 1];
-#pragma unroll
-        for (int i = 0; i < NW; ++i) W[i + 1] = Wn[i];
-        W[0] = __builtin_amdgcn_mov_dpp(W[NW], 0x93, 0xf, 0xf, false);   // quad_perm [3,0,1,2]: previous lane's last word
-        if (it + 2 < ntr)
-        {
-            p += 2 * row_bytes;
-#pragma unroll
-            for (int i = 0; i < NW; ++i) Wn[i] = ldg_nt(p, i);
-        }
-        strip<F, MR>(W, xs + (tr0 + it + h - xtr0) * 8, xstride, acc);
+        load_words(wb, p + 2 * row_bytes);
+        strip<F, MR>(wa, xb + it * 8, xstride, acc);
+        p += 4 * row_bytes;
+        if (it + 4 < ntr) load_words(wa, p);
+        strip<F, MR>(wb, xb + (it + 2) * 8, xstride, acc);
     }
+    if (it < ntr) strip<F, MR>(wa, xb + it * 8, xstride, acc);
 }
 
 template <int MR>

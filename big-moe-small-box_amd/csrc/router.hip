@@ -30,7 +30,8 @@ struct RouterArgs {
 };
 
 struct RouteShared {
-    float ch[RT_MAXE], sc[RT_MAXE];
+    float ch[RT_MAXE] __attribute__((aligned(16)));
+    float sc[RT_MAXE];
     float gtop[RT_MAXG][2], gsc[RT_MAXG];
     int gok[RT_MAXG];
     int idx[RT_MAXK];
@@ -56,7 +57,7 @@ __device__ void route_token(const RouterArgs& a, int t, RouteShared& S)
         mx = S.wmax[0];
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, S.wmax[w]);
     }
-    if (e >= E && e < ((E + 3) & ~3)) S.ch[e] = -__builtin_huge_valf();     // padding never beats a real expert
+    if (e >= E && e < ((E + 31) & ~31)) S.ch[e] = -__builtin_huge_valf();   // padding never beats a real expert
     if (mine)
     {
         if (a.score_fn == BMX_SCORE_SOFTMAX) { S.sc[e] = exp_fixed(__fsub_rn(l, mx)); S.ch[e] = l; }
@@ -97,12 +98,19 @@ __device__ void route_token(const RouterArgs& a, int t, RouteShared& S)
         int r = 0;
         if (G <= 1)
         {
-#pragma unroll 4
-            for (int q = 0; q < E; q += 4)
+            // 32 candidates per step: eight independent 16-byte LDS reads in flight, then the compares
+            for (int q0 = 0; q0 < E; q0 += 32)
             {
-                const float4 v = *reinterpret_cast<const float4*>(&S.ch[q]);
-                r += (better(v.x, q, c, e) ? 1 : 0) + (better(v.y, q + 1, c, e) ? 1 : 0) +
-                     (better(v.z, q + 2, c, e) ? 1 : 0) + (better(v.w, q + 3, c, e) ? 1 : 0);
+                float4 v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const float4*>(&S.ch[q0 + 4 * i]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                {
+                    const int q = q0 + 4 * i;
+                    r += (better(v[i].x, q, c, e) ? 1 : 0) + (better(v[i].y, q + 1, c, e) ? 1 : 0) +
+                         (better(v[i].z, q + 2, c, e) ? 1 : 0) + (better(v[i].w, q + 3, c, e) ? 1 : 0);
+                }
             }
         }
         else
@@ -165,56 +173,80 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
         __syncthreads();
     }
     const int NE = E + (d.shared ? 1 : 0);
-    __shared__ int firstocc[SM_MAXN];
+    __shared__ int4 pe4[SM_MAXN / 4];        // the picks again, padded with -1 to a multiple of 4
+    __shared__ int4 gc4[SM_MAXN / 4];        // per pick: groups of its expert if it is the expert's first pick, else 0
+    const int n4 = (n + 3) >> 2;
+    int* pev = reinterpret_cast<int*>(pe4);
+    int* gcv = reinterpret_cast<int*>(gc4);
+    for (int p = tid; p < 4 * n4; p += blockDim.x) pev[p] = p < n ? pe[p] : -1;
+    __syncthreads();
     // counts and offsets per expert (the shared segment last)
     int nvalid = 0;
-    for (int p = 0; p < n; ++p) nvalid += pe[p] >= 0;
+    for (int q = 0; q < n4; ++q)
+    {
+        const int4 v = pe4[q];
+        nvalid += (v.x >= 0) + (v.y >= 0) + (v.z >= 0) + (v.w >= 0);
+    }
     for (int e = tid; e < NE; e += blockDim.x)
     {
         int c = 0, below = 0;
         if (e < E)
-            for (int p = 0; p < n; ++p) { const int q = pe[p]; c += q == e; below += q >= 0 && q < e; }
+            for (int q = 0; q < n4; ++q)
+            {
+                const int4 v = pe4[q];
+                c += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+                below += (v.x >= 0 && v.x < e) + (v.y >= 0 && v.y < e) + (v.z >= 0 && v.z < e) + (v.w >= 0 && v.w < e);
+            }
         else { c = a.T; below = nvalid; }
         cnt[e] = c;
         d.r.counts[e] = c;
         d.r.offsets[e] = below;
         if (e == NE - 1) d.r.offsets[NE] = below + c;
     }
-    for (int p = tid; p < n; p += blockDim.x)
+    __syncthreads();
+    for (int p = tid; p < 4 * n4; p += blockDim.x)
     {
-        const int e = pe[p];
-        int f = e >= 0;
-        for (int q = 0; q < p && f; ++q) f = pe[q] != e;
-        firstocc[p] = f;
+        const int e = pev[p];
+        int first = e >= 0;
+        for (int q = 0; q < p && first; ++q) first = pev[q] != e;
+        gcv[p] = first ? (cnt[e] + d.rpg - 1) / d.rpg : 0;
     }
     __syncthreads();
-    // rows: stable by (expert, pick); per used expert (its first pick): list position and groups of <= rpg rows
     int nu_r = 0, ng_r = 0;
-    for (int q = 0; q < n; ++q)
-        if (firstocc[q]) { ++nu_r; ng_r += (cnt[pe[q]] + d.rpg - 1) / d.rpg; }
+    for (int q = 0; q < n4; ++q)
+    {
+        const int4 g = gc4[q];
+        nu_r += (g.x > 0) + (g.y > 0) + (g.z > 0) + (g.w > 0);
+        ng_r += g.x + g.y + g.z + g.w;
+    }
+    // rows: stable by (expert, pick); the expert's first pick also places its groups and its uexp entry
     for (int p = tid; p < n; p += blockDim.x)
     {
-        const int e = pe[p];
+        const int e = pev[p];
         if (e < 0) { d.r.inv[p] = -1; continue; }
         int row = 0, ui = 0, g0 = 0;
-        for (int q = 0; q < n; ++q)
+        for (int q4 = 0; q4 < n4; ++q4)
         {
-            const int eq = pe[q];
-            row += eq >= 0 && (eq < e || (eq == e && q < p));
-            if (firstocc[q] && eq < e) { ++ui; g0 += (cnt[eq] + d.rpg - 1) / d.rpg; }
+            const int4 v = pe4[q4], g = gc4[q4];
+            const int q = 4 * q4;
+            row += (v.x >= 0 && (v.x < e || (v.x == e && q < p))) + (v.y >= 0 && (v.y < e || (v.y == e && q + 1 < p))) +
+                   (v.z >= 0 && (v.z < e || (v.z == e && q + 2 < p))) + (v.w >= 0 && (v.w < e || (v.w == e && q + 3 < p)));
+            ui += (g.x > 0 && v.x < e) + (g.y > 0 && v.y < e) + (g.z > 0 && v.z < e) + (g.w > 0 && v.w < e);
+            g0 += (v.x < e ? g.x : 0) + (v.y < e ? g.y : 0) + (v.z < e ? g.z : 0) + (v.w < e ? g.w : 0);
         }
         d.r.inv[p] = row;
         d.r.row_token[row] = p / a.topk;
         d.r.row_slot[row] = p % a.topk;
         d.r.row_expert[row] = e;
-        if (firstocc[p])
+        const int ng = gcv[p];
+        if (ng > 0)
         {
-            const int c = cnt[e], row0 = row;          // the expert's first row is its first pick's
+            const int c = cnt[e];
             d.r.uexp[ui] = e;
-            for (int q = 0; q * d.rpg < c; ++q)
+            for (int q = 0; q < ng; ++q)
             {
                 d.r.groups[3 * (g0 + q) + 0] = e;
-                d.r.groups[3 * (g0 + q) + 1] = row0 + q * d.rpg;
+                d.r.groups[3 * (g0 + q) + 1] = row + q * d.rpg;
                 d.r.groups[3 * (g0 + q) + 2] = min(d.rpg, c - q * d.rpg);
             }
         }
