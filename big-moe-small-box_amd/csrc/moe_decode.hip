@@ -149,7 +149,39 @@ __device__ __forceinline__ int lane_col(int lane, int c)
 // ---- split-K grouped GEMV -> partial sums ------------------------------------------------------------------------------
 // NM = 2: gate and up of the same expert on rotated x rows (the rotation is computed here, per matrix suh);
 // NM = 1: down on the rotated fp16 down-input rows. part[ks][row][cb][mat][128] (mat stride 128, cb stride NM * 128).
-template <int MR, int NM>
+// MX: the most rows a group can hold (LDS layout); the GEMV itself runs with the group's own row count rounded up to
+// 1, 2, 4 or 8, so a one-token group costs one row of dot products whatever the batch.
+template <int MR, int MX, int NM>
+__device__ __forceinline__ void gemv_rows(const GvArgs& a, const bmx_expert& ex, int cb, int k0, int KR, int N,
+                                          const uint32_t* xs, float* red)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, XW = KR / 2;
+    const int TRW = KR / 16 / GV_WAVES;
+    const int tr0 = k0 / 16 + wave * TRW;
+#pragma unroll
+    for (int mat = 0; mat < NM; ++mat)
+    {
+        const int mi = NM == 2 ? mat : 2;
+        float acc[4][MR];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[c][m] = 0.0f;
+        gemv_any<MR>(ex.fmt[mi], reinterpret_cast<const uint8_t*>(ex.tr[mi]), N / 16, cb, tr0, TRW, xs + mat * MX * XW,
+                     XW, k0 / 16, acc);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[c][m] = acc[c][m] + __shfl_xor(acc[c][m], 32);
+        if (lane < 32)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) red[((mat * GV_WAVES + wave) * MX + m) * 128 + lane_col(lane, c)] = acc[c][m];
+    }
+}
+
+template <int MX, int NM>
 __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
 {
     extern __shared__ uint32_t smem[];
@@ -163,74 +195,55 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const int K = NM == 2 ? a.H : a.I, N = NM == 2 ? a.I : a.H;
     const int KR = K / KS, k0 = ks * KR, XW = KR / 2;
-    uint32_t* xs = smem;                                           // [NM][MR][KR / 2] fp16 pairs
-    float* red = reinterpret_cast<float*>(smem + NM * MR * XW);    // [NM][GV_WAVES][MR][128]
+    uint32_t* xs = smem;                                           // [NM][MX][KR / 2] fp16 pairs
+    float* red = reinterpret_cast<float*>(smem + NM * MX * XW);    // [NM][GV_WAVES][MX][128]
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 
     if (NM == 2)
     {
         // input rotation of each token row for gate and up: xt = RN16(H128(x * suh) * R)
         const int nblk = KR / 128;
-        for (int u = wave; u < 2 * MR * nblk; u += GV_WAVES)
+        for (int u = wave; u < 2 * nr * nblk; u += GV_WAVES)
         {
-            const int mat = u / (MR * nblk), rem = u % (MR * nblk), m = rem / nblk, b = rem % nblk;
-            uint32_t val = 0;
-            if (m < nr)
-            {
-                const int tok = a.row_token[r0 + m];
-                const int k = k0 + b * 128 + 2 * lane;
-                const uint32_t xv = ldg(a.x + (size_t)tok * a.H + k, 0);
-                const uint32_t sv = ldg(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k, 0);
-                float v0 = h2f(xv & 0xffffu) * h2f(sv & 0xffffu), v1 = h2f(xv >> 16) * h2f(sv >> 16);
-                had128_wave(v0, v1);
-                val = (uint32_t)f2h(v0 * R_SCALE) | ((uint32_t)f2h(v1 * R_SCALE) << 16);
-            }
-            xs[(mat * MR + m) * XW + b * 64 + lane] = val;
+            const int mat = u / (nr * nblk), rem = u % (nr * nblk), m = rem / nblk, b = rem % nblk;
+            const int tok = a.row_token[r0 + m];
+            const int k = k0 + b * 128 + 2 * lane;
+            const uint32_t xv = ldg(a.x + (size_t)tok * a.H + k, 0);
+            const uint32_t sv = ldg(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k, 0);
+            float v0 = h2f(xv & 0xffffu) * h2f(sv & 0xffffu), v1 = h2f(xv >> 16) * h2f(sv >> 16);
+            had128_wave(v0, v1);
+            xs[(mat * MX + m) * XW + b * 64 + lane] = (uint32_t)f2h(v0 * R_SCALE) | ((uint32_t)f2h(v1 * R_SCALE) << 16);
         }
     }
     else
     {
-        for (int i = threadIdx.x; i < MR * XW; i += GV_THREADS)
+        for (int i = threadIdx.x; i < nr * XW; i += GV_THREADS)
         {
             const int m = i / XW, d = i % XW;
-            xs[i] = m < nr ? ldg(a.act_rows + (size_t)(r0 + m) * a.I + k0 + 2 * d, 0) : 0u;
+            xs[i] = ldg(a.act_rows + (size_t)(r0 + m) * a.I + k0 + 2 * d, 0);
         }
     }
-    __syncthreads();
-
-    const int TRW = KR / 16 / GV_WAVES;
-    const int tr0 = k0 / 16 + wave * TRW;
-#pragma unroll
-    for (int mat = 0; mat < NM; ++mat)
+    // rows nr .. (nr rounded up) of the staged input are read by the GEMV: zero them
+    const int mr = nr <= 1 ? 1 : nr <= 2 ? 2 : nr <= 4 ? 4 : 8;
+    for (int i = threadIdx.x; i < NM * (mr - nr) * XW; i += GV_THREADS)
     {
-        const int mi = NM == 2 ? mat : 2;
-        float acc[4][MR];
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) acc[c][m] = 0.0f;
-        gemv_any<MR>(ex.fmt[mi], reinterpret_cast<const uint8_t*>(ex.tr[mi]), N / 16, cb, tr0, TRW, xs + mat * MR * XW,
-                     XW, k0 / 16, acc);
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) acc[c][m] = acc[c][m] + __shfl_xor(acc[c][m], 32);
-        if (lane < 32)
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-#pragma unroll
-                for (int m = 0; m < MR; ++m) red[((mat * GV_WAVES + wave) * MR + m) * 128 + lane_col(lane, c)] = acc[c][m];
+        const int mat = i / ((mr - nr) * XW), rem = i % ((mr - nr) * XW);
+        xs[(mat * MX + nr) * XW + rem] = 0u;
     }
+    __syncthreads();
+    if (mr == 1) gemv_rows<1, MX, NM>(a, ex, cb, k0, KR, N, xs, red);
+    else if (mr == 2) { if constexpr (MX >= 2) gemv_rows<2, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
+    else if (mr == 4) { if constexpr (MX >= 4) gemv_rows<4, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
+    else { if constexpr (MX >= 8) gemv_rows<8, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
     __syncthreads();
     // the four waves in order, then one partial per (split, row, block)
     float* part = (NM == 2 ? a.part_gu : a.part_dn) + (((size_t)ks * a.R_max + r0) * NB + cb) * (NM * 128);
-    for (int i = threadIdx.x; i < NM * MR * 128; i += GV_THREADS)
+    for (int i = threadIdx.x; i < NM * nr * 128; i += GV_THREADS)
     {
-        const int mat = i / (MR * 128), m = (i / 128) % MR, c = i % 128;
-        if (m >= nr) continue;
+        const int mat = i / (nr * 128), m = (i / 128) % nr, c = i % 128;
         float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < GV_WAVES; ++w) s = s + red[((mat * GV_WAVES + w) * MR + m) * 128 + c];
+        for (int w = 0; w < GV_WAVES; ++w) s = s + red[((mat * GV_WAVES + w) * MX + m) * 128 + c];
         part[(size_t)m * NB * NM * 128 + mat * 128 + c] = s;
     }
 }

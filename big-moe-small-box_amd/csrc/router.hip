@@ -1,23 +1,64 @@
 // Router and decode-size route + dispatch.
 //
-// Selection by rank: every candidate counts the candidates that beat it under the strict total order (larger choice,
-// then lower index); rank < k selects it into slot `rank`. The group limit ranks the top-2 of each group the same way,
-// then the groups by their top-2 sums. All threads read the same LDS word at each step (broadcast), so a token costs
-// E LDS reads per thread and no serial reduction chain; the result is the order the oracle's sequential selection
-// produces, independent of scheduling.
+// One wavefront per token. Lane l holds experts l, l + 64, ...; each pick is a wave-wide argmax under the strict total
+// order (larger choice, then lower index): a DPP max of the order-preserving key of the value, then a DPP min of the
+// index among the lanes holding that value. The group limit picks each group's top-2 the same way, then the groups by
+// their top-2 sums. The order is the one the oracle's sequential selection produces, independent of scheduling.
 #include "bmx_common.hpp"
 #include "bmx_internal.hpp"
 
 namespace bmx {
 
-constexpr int RT_THREADS = 1024;
-constexpr int RT_MAXE = 1024;
+constexpr int RT_WAVES = 16;
+constexpr int RT_THREADS = RT_WAVES * 64;
+constexpr int RT_MAXJ = 16;        // experts per lane: E <= 1024
+constexpr int RT_MAXE = RT_MAXJ * 64;
 constexpr int RT_MAXG = 64;
 constexpr int RT_MAXK = 32;
 constexpr int SM_MAXN = 256;       // picks of the fused decode kernel
 
 __device__ __forceinline__ float canon(float v) { return v != v ? -__builtin_huge_valf() : __fadd_rn(v, 0.0f); }
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) { return va > vb || (va == vb && ia < ib); }
+
+// unsigned key with the order of the (canonical, non-NaN) float
+__device__ __forceinline__ uint32_t okey(float v)
+{
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// wave-wide max / min of a uint32, uniform result: xor 1 and xor 2 within quads, mirrors within half-rows and rows
+// (each lane then holds its row's result), then the four rows on the scalar unit
+__device__ __forceinline__ uint32_t wave_umax(uint32_t k)
+{
+    k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0xB1, 0xf, 0xf, false));
+    k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x4E, 0xf, 0xf, false));
+    k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x141, 0xf, 0xf, false));
+    k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x140, 0xf, 0xf, false));
+    const uint32_t a = __builtin_amdgcn_readlane(k, 0), b = __builtin_amdgcn_readlane(k, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(k, 32), d = __builtin_amdgcn_readlane(k, 48);
+    return max(max(a, b), max(c, d));
+}
+
+__device__ __forceinline__ uint32_t wave_umin(uint32_t k)
+{
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0xB1, 0xf, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x4E, 0xf, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x141, 0xf, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x140, 0xf, 0xf, false));
+    const uint32_t a = __builtin_amdgcn_readlane(k, 0), b = __builtin_amdgcn_readlane(k, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(k, 32), d = __builtin_amdgcn_readlane(k, 48);
+    return min(min(a, b), min(c, d));
+}
+
+// index of the best of (lane candidate v at index i; i < 0 = none) over the wave, -1 if none
+__device__ __forceinline__ int wave_argbest(float v, int i)
+{
+    const uint32_t k = i >= 0 ? okey(v) : 0u;
+    const uint32_t m = wave_umax(k);
+    if (m == 0u) return -1;
+    return (int)wave_umin((i >= 0 && k == m) ? (uint32_t)i : 0xffffffffu);
+}
 
 struct RouterArgs {
     const uint16_t* logits;
@@ -29,129 +70,138 @@ struct RouterArgs {
     uint16_t* w;
 };
 
-struct RouteShared {
-    float ch[RT_MAXE] __attribute__((aligned(16)));
-    float sc[RT_MAXE];
-    float gtop[RT_MAXG][2], gsc[RT_MAXG];
-    int gok[RT_MAXG];
-    int idx[RT_MAXK];
-    float wmax[RT_THREADS / 64];
-};
-
-// Route token t with threads [tid0, tid0 + E) of the workgroup (one thread per expert). Writes sel / w of the token and
-// leaves the local picks in S.idx. Every thread of the workgroup must call it (it synchronises).
-__device__ void route_token(const RouterArgs& a, int t, RouteShared& S)
+// Route token t with the calling wave. Writes sel / w of the token; returns the pick of slot `lane` (lanes < topk)
+// as a local expert id (-1 otherwise).
+template <int J>
+__device__ int route_token_wave(const RouterArgs& a, int t)
 {
-    const int e = threadIdx.x, E = a.E;
-    const bool mine = e < E;
+    const int lane = threadIdx.x & 63, E = a.E;
     const uint16_t* lg = a.logits + (size_t)t * E;
-    float l = mine ? canon(h2f(lg[e])) : -__builtin_huge_valf();
-    float mx = 0.0f;
+    float ch[J], sc[J];
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+    {
+        const int e = lane + 64 * j;
+        ch[j] = e < E ? canon(h2f(lg[e])) : -__builtin_huge_valf();
+        mx = fmaxf(mx, ch[j]);
+    }
     if (a.score_fn == BMX_SCORE_SOFTMAX)
     {
-        float v = l;
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
-        if ((threadIdx.x & 63) == 0) S.wmax[threadIdx.x >> 6] = v;
-        __syncthreads();
-        mx = S.wmax[0];
-        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, S.wmax[w]);
+        const uint32_t m = wave_umax(okey(mx));
+        mx = __builtin_bit_cast(float, (m & 0x80000000u) ? (m & 0x7fffffffu) : ~m);
     }
-    if (e >= E && e < ((E + 31) & ~31)) S.ch[e] = -__builtin_huge_valf();   // padding never beats a real expert
-    if (mine)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
     {
-        if (a.score_fn == BMX_SCORE_SOFTMAX) { S.sc[e] = exp_fixed(__fsub_rn(l, mx)); S.ch[e] = l; }
+        const int e = lane + 64 * j;
+        if (a.score_fn == BMX_SCORE_SOFTMAX) sc[j] = e < E ? exp_fixed(__fsub_rn(ch[j], mx)) : 0.0f;
         else
         {
-            const float s = sigmoid_fixed(l);
-            S.sc[e] = s;
-            S.ch[e] = canon(a.bias ? __fadd_rn(s, a.bias[e]) : s);
+            sc[j] = e < E ? sigmoid_fixed(ch[j]) : 0.0f;
+            if (e < E) ch[j] = canon(a.bias ? __fadd_rn(sc[j], a.bias[e]) : sc[j]);
         }
     }
-    __syncthreads();
+    // group limit
+    uint64_t gok = ~0ull;
     const int G = a.G, gs = E / G;
     if (G > 1)
     {
-        if (mine)
+        float gsc[RT_MAXG];
+        for (int g = 0; g < G; ++g)
         {
-            const int g = e / gs;
-            const float c = S.ch[e];
-            int r = 0;
-            for (int q = g * gs; q < (g + 1) * gs; ++q) r += better(S.ch[q], q, c, e) ? 1 : 0;
-            if (r < 2) S.gtop[g][r] = c;
-        }
-        __syncthreads();
-        if (e < G) S.gsc[e] = canon(gs >= 2 ? __fadd_rn(S.gtop[e][0], S.gtop[e][1]) : S.gtop[e][0]);
-        __syncthreads();
-        if (e < G)
-        {
-            int r = 0;
-            for (int q = 0; q < G; ++q) r += better(S.gsc[q], q, S.gsc[e], e) ? 1 : 0;
-            S.gok[e] = r < a.TG;
-        }
-        __syncthreads();
-    }
-    const bool allowed = mine && (G <= 1 || S.gok[e / gs]);
-    if (allowed)
-    {
-        const float c = S.ch[e];
-        int r = 0;
-        if (G <= 1)
-        {
-            // 32 candidates per step: eight independent 16-byte LDS reads in flight, then the compares
-            for (int q0 = 0; q0 < E; q0 += 32)
+            float v1 = 0.0f, v2 = 0.0f;
+            int i1 = -1, i2 = -1;
+#pragma unroll
+            for (int j = 0; j < J; ++j)
             {
-                float4 v[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const float4*>(&S.ch[q0 + 4 * i]);
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                {
-                    const int q = q0 + 4 * i;
-                    r += (better(v[i].x, q, c, e) ? 1 : 0) + (better(v[i].y, q + 1, c, e) ? 1 : 0) +
-                         (better(v[i].z, q + 2, c, e) ? 1 : 0) + (better(v[i].w, q + 3, c, e) ? 1 : 0);
-                }
+                const int e = lane + 64 * j;
+                if (e >= g * gs && e < (g + 1) * gs && (i1 < 0 || better(ch[j], e, v1, i1))) { v1 = ch[j]; i1 = e; }
             }
+            const int b1 = wave_argbest(v1, i1);
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+            {
+                const int e = lane + 64 * j;
+                if (e >= g * gs && e < (g + 1) * gs && e != b1 && (i2 < 0 || better(ch[j], e, v2, i2))) { v2 = ch[j]; i2 = e; }
+            }
+            const int b2 = wave_argbest(v2, i2);
+            float t1 = 0.0f, t2 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+            {
+                t1 = (lane + 64 * j == b1) ? ch[j] : t1;
+                t2 = (lane + 64 * j == b2) ? ch[j] : t2;
+            }
+            t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t1), b1 & 63));
+            t2 = b2 >= 0 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t2), b2 & 63)) : 0.0f;
+            gsc[g] = canon(b2 >= 0 ? __fadd_rn(t1, t2) : t1);
         }
-        else
+        gok = 0;
+        for (int r = 0; r < a.TG && r < G; ++r)
         {
+            int bg = -1;
             for (int g = 0; g < G; ++g)
-            {
-                if (!S.gok[g]) continue;
-#pragma unroll 4
-                for (int q = g * gs; q < (g + 1) * gs; ++q) r += better(S.ch[q], q, c, e) ? 1 : 0;
-            }
+                if (!((gok >> g) & 1ull) && (bg < 0 || better(gsc[g], g, gsc[bg], bg))) bg = g;
+            gok |= 1ull << bg;
         }
-        if (r < a.topk) S.idx[r] = e;
     }
-    __syncthreads();
-    if (threadIdx.x == 0)
+    // top-k: each lane keeps its best remaining candidate; the winner's lane drops it and rescans
+    uint32_t taken = 0;
+    auto local_best = [&](float& bv, int& bi, float& bs) {
+        bi = -1; bv = 0.0f; bs = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+        {
+            const int e = lane + 64 * j;
+            const bool ok = e < E && !((taken >> j) & 1u) && (G <= 1 || ((gok >> (e / gs)) & 1ull));
+            if (ok && (bi < 0 || better(ch[j], e, bv, bi))) { bv = ch[j]; bi = e; bs = sc[j]; }
+        }
+    };
+    float bv, bs;
+    int bi;
+    local_best(bv, bi, bs);
+    int mypick = -1;
+    float vsum = 0.0f, myscore = 0.0f;
+    for (int k = 0; k < a.topk; ++k)
     {
-        float vsum = 0.0f;
-        for (int k = 0; k < a.topk; ++k) vsum = __fadd_rn(vsum, S.sc[S.idx[k]]);
-        float den = 1.0f;
-        if (a.score_fn == BMX_SCORE_SOFTMAX && !a.renorm)
+        const int win = wave_argbest(bv, bi);
+        const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bs), win & 63));
+        vsum = __fadd_rn(vsum, ws);
+        if (lane == k) { mypick = win; myscore = ws; }
+        if ((win & 63) == lane)
         {
-            den = 0.0f;
-            for (int q = 0; q < E; ++q) den = __fadd_rn(den, S.sc[q]);
-        }
-        else if (a.renorm) den = vsum;
-        for (int k = 0; k < a.topk; ++k)
-        {
-            const float v = S.sc[S.idx[k]];
-            const float qv = (a.score_fn == BMX_SCORE_SIGMOID && !a.renorm) ? v : __fdiv_rn(v, den);
-            a.sel[(size_t)t * a.topk + k] = (int64_t)S.idx[k] + a.first;
-            a.w[(size_t)t * a.topk + k] = f2h(__fmul_rn(qv, a.scale));
+            taken |= 1u << (win >> 6);
+            local_best(bv, bi, bs);
         }
     }
-    __syncthreads();
+    float den = 1.0f;
+    if (a.score_fn == BMX_SCORE_SOFTMAX && !a.renorm)
+    {
+        den = 0.0f;
+        for (int e = 0; e < E; ++e)
+        {
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < J; ++j) v = (j == (e >> 6)) ? sc[j] : v;
+            den = __fadd_rn(den, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), e & 63)));
+        }
+    }
+    else if (a.renorm) den = vsum;
+    if (lane < a.topk)
+    {
+        const float qv = (a.score_fn == BMX_SCORE_SIGMOID && !a.renorm) ? myscore : __fdiv_rn(myscore, den);
+        a.sel[(size_t)t * a.topk + lane] = (int64_t)mypick + a.first;
+        a.w[(size_t)t * a.topk + lane] = f2h(__fmul_rn(qv, a.scale));
+    }
+    return mypick;
 }
 
-// one workgroup per token
+template <int J>
 __global__ __launch_bounds__(RT_THREADS) void k_router(RouterArgs a)
 {
-    __shared__ RouteShared S;
-    route_token(a, blockIdx.x, S);
+    const int t = blockIdx.x * RT_WAVES + (threadIdx.x >> 6);
+    if (t < a.T) route_token_wave<J>(a, t);
 }
 
 // ---- fused decode kernel: route every token, then the counting sort of its picks, in one workgroup ------------------
@@ -160,18 +210,18 @@ struct SmallDispatch {
     bmx_routes r;
 };
 
+template <int J>
 __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs a, SmallDispatch d)
 {
-    __shared__ RouteShared S;
     __shared__ int pe[SM_MAXN];          // local expert of each pick (-1: dropped)
     __shared__ int cnt[RT_MAXE + 1];
-    const int E = a.E, n = a.T * a.topk, tid = threadIdx.x;
-    for (int t = 0; t < a.T; ++t)
+    const int E = a.E, n = a.T * a.topk, tid = threadIdx.x, lane = tid & 63;
+    for (int t = tid >> 6; t < a.T; t += RT_WAVES)
     {
-        route_token(a, t, S);
-        if (tid < a.topk) pe[t * a.topk + tid] = S.idx[tid];
-        __syncthreads();
+        const int pk = route_token_wave<J>(a, t);
+        if (lane < a.topk) pe[t * a.topk + lane] = pk;
     }
+    __syncthreads();
     const int NE = E + (d.shared ? 1 : 0);
     __shared__ int4 pe4[SM_MAXN / 4];        // the picks again, padded with -1 to a multiple of 4
     __shared__ int4 gc4[SM_MAXN / 4];        // per pick: groups of its expert if it is the expert's first pick, else 0
@@ -299,7 +349,6 @@ static RouterArgs router_args(const void* logits, const float* bias, int T, int 
     return a;
 }
 
-static unsigned router_threads(int E) { return (unsigned)((E + 63) / 64 * 64); }
 
 int launch_router(const void* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,
                   int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w, hipStream_t s)
@@ -307,7 +356,13 @@ int launch_router(const void* logits, const float* bias, int T, int E, int topk,
     int rc = check_router(T, E, topk, n_group, topk_group, score_fn, logits, sel, w);
     if (rc || T == 0) return rc;
     const RouterArgs a = router_args(logits, bias, T, E, topk, n_group, topk_group, score_fn, renorm, scale, first, sel, w);
-    hipLaunchKernelGGL(k_router, dim3((unsigned)T), dim3(router_threads(E)), 0, s, a);
+    const dim3 grid((unsigned)((T + RT_WAVES - 1) / RT_WAVES)), block(RT_THREADS);
+    const int J = (E + 63) / 64;
+    if (J <= 1) hipLaunchKernelGGL(k_router<1>, grid, block, 0, s, a);
+    else if (J <= 2) hipLaunchKernelGGL(k_router<2>, grid, block, 0, s, a);
+    else if (J <= 4) hipLaunchKernelGGL(k_router<4>, grid, block, 0, s, a);
+    else if (J <= 8) hipLaunchKernelGGL(k_router<8>, grid, block, 0, s, a);
+    else hipLaunchKernelGGL(k_router<16>, grid, block, 0, s, a);
     return check_launch("bmx_router_topk");
 }
 
@@ -325,8 +380,13 @@ int launch_route_dispatch_small(const void* logits, const float* bias, int T, in
     d.shared = shared ? 1 : 0;
     d.rpg = rpg;
     d.r = *routes;
-    const unsigned nt = router_threads(E) > 256 ? router_threads(E) : 256;
-    hipLaunchKernelGGL(k_route_dispatch_small, dim3(1), dim3(nt), 0, s, a, d);
+    const int J = (E + 63) / 64;
+    const dim3 grid(1), block(RT_THREADS);
+    if (J <= 1) hipLaunchKernelGGL(k_route_dispatch_small<1>, grid, block, 0, s, a, d);
+    else if (J <= 2) hipLaunchKernelGGL(k_route_dispatch_small<2>, grid, block, 0, s, a, d);
+    else if (J <= 4) hipLaunchKernelGGL(k_route_dispatch_small<4>, grid, block, 0, s, a, d);
+    else if (J <= 8) hipLaunchKernelGGL(k_route_dispatch_small<8>, grid, block, 0, s, a, d);
+    else hipLaunchKernelGGL(k_route_dispatch_small<16>, grid, block, 0, s, a, d);
     return check_launch("route + dispatch");
 }
 
