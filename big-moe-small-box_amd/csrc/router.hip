@@ -107,7 +107,7 @@ __device__ int route_token_wave(const RouterArgs& a, int t)
     const int G = a.G, gs = E / G;
     if (G > 1)
     {
-        float gsc[RT_MAXG];
+        float mygsc = 0.0f;                      // lane g holds group g's score
         for (int g = 0; g < G; ++g)
         {
             float v1 = 0.0f, v2 = 0.0f;
@@ -135,14 +135,12 @@ __device__ int route_token_wave(const RouterArgs& a, int t)
             }
             t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t1), b1 & 63));
             t2 = b2 >= 0 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t2), b2 & 63)) : 0.0f;
-            gsc[g] = canon(b2 >= 0 ? __fadd_rn(t1, t2) : t1);
+            if (lane == g) mygsc = canon(b2 >= 0 ? __fadd_rn(t1, t2) : t1);
         }
         gok = 0;
         for (int r = 0; r < a.TG && r < G; ++r)
         {
-            int bg = -1;
-            for (int g = 0; g < G; ++g)
-                if (!((gok >> g) & 1ull) && (bg < 0 || better(gsc[g], g, gsc[bg], bg))) bg = g;
+            const int bg = wave_argbest(mygsc, (lane < G && !((gok >> lane) & 1ull)) ? lane : -1);
             gok |= 1ull << bg;
         }
     }
