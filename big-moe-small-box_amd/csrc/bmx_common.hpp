@@ -76,6 +76,14 @@ __device__ __forceinline__ uint32_t ldg(const void* p, int i)
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, (f16)v); }
+// RN16 of an fp32 value that is first materialised as fp32: the empty asm keeps the compiler from fusing the producing
+// multiply or add with the conversion into one mixed-precision instruction (one rounding instead of the two the
+// reference performs: fp32 result, then fp16)
+__device__ __forceinline__ uint16_t f2h_r(float v)
+{
+    asm("" : "+v"(v));
+    return f2h(v);
+}
 
 // Codebook hash of one 16-bit state (only the low 16 bits of `st` are read; the bits above may hold anything):
 //   x = st * MUL1 mod 2^32 = st * 0xD12D + ((st * 0x83DC mod 2^16) << 16)

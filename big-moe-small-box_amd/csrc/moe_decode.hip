@@ -212,7 +212,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
             const uint32_t sv = ldg(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k, 0);
             float v0 = h2f(xv & 0xffffu) * h2f(sv & 0xffffu), v1 = h2f(xv >> 16) * h2f(sv >> 16);
             had128_wave(v0, v1);
-            xs[(mat * MX + m) * XW + b * 64 + lane] = (uint32_t)f2h(v0 * R_SCALE) | ((uint32_t)f2h(v1 * R_SCALE) << 16);
+            xs[(mat * MX + m) * XW + b * 64 + lane] = (uint32_t)f2h_r(v0 * R_SCALE) | ((uint32_t)f2h_r(v1 * R_SCALE) << 16);
         }
     }
     else
@@ -269,8 +269,8 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
         g0 = g0 + gv.x; g1 = g1 + gv.y;
         u0 = u0 + uv.x; u1 = u1 + uv.y;
     }
-    g0 = h2f(f2h(g0)); g1 = h2f(f2h(g1));
-    u0 = h2f(f2h(u0)); u1 = h2f(f2h(u1));
+    g0 = h2f(f2h_r(g0)); g1 = h2f(f2h_r(g1));
+    u0 = h2f(f2h_r(u0)); u1 = h2f(f2h_r(u1));
     had128_wave(g0, g1);
     had128_wave(u0, u1);
     const uint32_t svg = ldg(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col, 0);
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     float a0 = act_gate(a.act, a.gated, g0, u0, a.limit) * h2f(sud & 0xffffu);
     float a1 = act_gate(a.act, a.gated, g1, u1, a.limit) * h2f(sud >> 16);
     had128_wave(a0, a1);
-    const uint32_t pk = (uint32_t)f2h(a0 * R_SCALE) | ((uint32_t)f2h(a1 * R_SCALE) << 16);
+    const uint32_t pk = (uint32_t)f2h_r(a0 * R_SCALE) | ((uint32_t)f2h_r(a1 * R_SCALE) << 16);
     *reinterpret_cast<uint32_t*>(a.act_rows + (size_t)r * a.I + col) = pk;
 }
 

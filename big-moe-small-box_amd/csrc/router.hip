@@ -190,7 +190,7 @@ __device__ int route_token_wave(const RouterArgs& a, int t)
     {
         const float qv = (a.score_fn == BMX_SCORE_SIGMOID && !a.renorm) ? myscore : __fdiv_rn(myscore, den);
         a.sel[(size_t)t * a.topk + lane] = (int64_t)mypick + a.first;
-        a.w[(size_t)t * a.topk + lane] = f2h(__fmul_rn(qv, a.scale));
+        a.w[(size_t)t * a.topk + lane] = f2h_r(__fmul_rn(qv, a.scale));
     }
     return mypick;
 }
