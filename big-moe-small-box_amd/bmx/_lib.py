@@ -11,6 +11,7 @@ TILE_BYTES = {TF_K2: 64, TF_K25: 80, TF_K3: 96, TF_K4: 128}
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
+STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT = 0, 1, 2, 3, 4
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -54,8 +55,7 @@ SIGNATURES = {
     "bmx_rows_per_group": (_I, [_I, _I]),
     "bmx_experts_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_experts": (_I, [ctypes.POINTER(MoeDesc), _P, _I, ctypes.POINTER(Routes), _P, _P, _P, _SZ, _I, _P]),
-    "bmx_moe_gate_up": (_I, [ctypes.POINTER(MoeDesc), _P, _I, ctypes.POINTER(Routes), _P, _P, _SZ, _I, _P]),
-    "bmx_moe_down": (_I, [ctypes.POINTER(MoeDesc), _I, ctypes.POINTER(Routes), _P, _P, _P, _P, _P, _SZ, _I, _P]),
+    "bmx_moe_stage": (_I, [ctypes.POINTER(MoeDesc), _I, _P, _I, ctypes.POINTER(Routes), _P, _P, _P, _P, _P, _SZ, _I, _P]),
     "bmx_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "bmx_moe_layer_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_layer": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),

@@ -88,6 +88,8 @@ static bmx_routes routes_at(char* base, const RoutesLayout& L)
     return r;
 }
 
+constexpr int STAGES_LAYER = (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) | (1 << BMX_STAGE_COMBINE);
+
 static int resolve_path(int path, int T)
 {
     (void)T;
@@ -160,31 +162,25 @@ int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const b
     if (T == 0) return BMX_OK;
     if (!x_fp16 || !routes || !y_rows || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_experts: null pointer");
     return launch_decode_experts(shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
-                                 nullptr, nullptr, static_cast<hipStream_t>(stream), 3);
+                                 nullptr, nullptr, static_cast<hipStream_t>(stream),
+                                 (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) | (1 << BMX_STAGE_DOWN_OUT));
 }
 
-int bmx_moe_gate_up(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, void* act_rows_fp16,
-                    void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream)
+int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T, const bmx_routes* routes,
+                  void* act_rows_fp16, float* y_rows, const void* w_fp16, float* out, void* workspace,
+                  size_t workspace_bytes, int path, bmx_stream_t stream)
 {
-    int rc = check_desc(desc, "bmx_moe_gate_up");
+    int rc = check_desc(desc, "bmx_moe_stage");
     if (rc) return rc;
-    if (resolve_path(path, T) < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_gate_up: bad path or T");
+    if (resolve_path(path, T) < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_stage: bad path or T");
+    if (stage < BMX_STAGE_GATE_UP || stage > BMX_STAGE_DOWN_OUT) return set_error(BMX_ERR_ARG, "bmx_moe_stage: unknown stage %d", stage);
     if (T == 0) return BMX_OK;
-    if (!x_fp16 || !routes || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_gate_up: null pointer");
-    return launch_decode_experts(shape_of(desc, T), x_fp16, routes, nullptr, act_rows_fp16, workspace, workspace_bytes,
-                                 nullptr, nullptr, static_cast<hipStream_t>(stream), 1);
-}
-
-int bmx_moe_down(const bmx_moe_desc* desc, int T, const bmx_routes* routes, const void* act_rows_fp16, float* y_rows,
-                 const void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream)
-{
-    int rc = check_desc(desc, "bmx_moe_down");
-    if (rc) return rc;
-    if (resolve_path(path, T) < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_down: bad path or T");
-    if (T == 0) return BMX_OK;
-    if (!routes || !y_rows || !workspace || (out && !w_fp16)) return set_error(BMX_ERR_ARG, "bmx_moe_down: null pointer");
-    return launch_decode_experts(shape_of(desc, T), nullptr, routes, y_rows, const_cast<void*>(act_rows_fp16), workspace,
-                                 workspace_bytes, out, w_fp16, static_cast<hipStream_t>(stream), 2);
+    if (!routes || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_stage: null pointer");
+    if (stage == BMX_STAGE_GATE_UP && !x_fp16) return set_error(BMX_ERR_ARG, "bmx_moe_stage: gate/up needs x");
+    if (stage == BMX_STAGE_COMBINE && (!out || !w_fp16)) return set_error(BMX_ERR_ARG, "bmx_moe_stage: combine needs out and w");
+    if (stage == BMX_STAGE_DOWN_OUT && !y_rows) return set_error(BMX_ERR_ARG, "bmx_moe_stage: down_out needs y_rows");
+    return launch_decode_experts(shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
+                                 out, w_fp16, static_cast<hipStream_t>(stream), 1 << stage);
 }
 
 int bmx_combine(const float* y_rows, const int32_t* inv, const void* w_fp16, const int32_t* offsets, int T, int topk,
@@ -230,7 +226,7 @@ int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const i
     const size_t ews_bytes = align_up(decode_ws_bytes(m), 256);
     rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr, 0, s);
     if (rc) return rc;
-    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, 3);
+    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
 }
 
 size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path) { return bmx_moe_workspace(desc, T, path); }
@@ -270,7 +266,7 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
         if (!rc) rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr, 0, s);
     }
     if (rc) return rc;
-    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, 3);
+    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
 }
 
 }  // extern "C"

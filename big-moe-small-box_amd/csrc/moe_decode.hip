@@ -468,25 +468,22 @@ size_t decode_ws_bytes(const MoeShape& m)
     return align_up(p.part_gu_bytes, 256) + align_up(p.part_dn_bytes, 256) + align_up((size_t)p.R_max * m.I * 2, 256);
 }
 
+// stages: bit i = BMX_STAGE i (GATE_UP, ACT, DOWN, COMBINE, DOWN_OUT)
 template <int MR>
 static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStream_t s)
 {
     const size_t lds_gu = (size_t)2 * MR * (a.H / p.KS_gu) / 2 * 4 + (size_t)2 * GV_WAVES * MR * 128 * 4;
     const size_t lds_dn = (size_t)MR * (a.I / p.KS_dn) / 2 * 4 + (size_t)GV_WAVES * MR * 128 * 4;
-    const unsigned epi_gu = (unsigned)((p.R_max * p.NB + GV_WAVES - 1) / GV_WAVES);
-    if (stages & 1)
-    {
+    if (stages & (1 << BMX_STAGE_GATE_UP))
         hipLaunchKernelGGL((k_gemv_part<MR, 2>), dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds_gu, s, a);
-        hipLaunchKernelGGL(k_gu_epi, dim3(epi_gu), dim3(GV_THREADS), 0, s, a);
-    }
-    if (stages & 2)
-    {
+    if (stages & (1 << BMX_STAGE_ACT))
+        hipLaunchKernelGGL(k_gu_epi, dim3((unsigned)((p.R_max * p.NB + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+    if (stages & (1 << BMX_STAGE_DOWN))
         hipLaunchKernelGGL((k_gemv_part<MR, 1>), dim3((unsigned)(p.G_max * p.NBH * p.KS_dn)), dim3(GV_THREADS), lds_dn, s, a);
-        if (a.out)
-            hipLaunchKernelGGL(k_dn_combine, dim3((unsigned)(a.T * p.NBH)), dim3(GV_THREADS), 0, s, a);
-        else
-            hipLaunchKernelGGL(k_dn_epi, dim3((unsigned)((p.R_max * p.NBH + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
-    }
+    if (stages & (1 << BMX_STAGE_COMBINE))
+        hipLaunchKernelGGL(k_dn_combine, dim3((unsigned)(a.T * p.NBH)), dim3(GV_THREADS), 0, s, a);
+    if (stages & (1 << BMX_STAGE_DOWN_OUT))
+        hipLaunchKernelGGL(k_dn_epi, dim3((unsigned)((p.R_max * p.NBH + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
 }
 
 int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,

@@ -148,14 +148,17 @@ size_t bmx_experts_workspace(const bmx_moe_desc* desc, int T, int path);
 int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, float* y_rows,
                     void* act_rows_fp16, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
 
-/* The two halves of bmx_moe_experts, for callers that schedule or time them apart (exllamav3's kernel A and kernel B,
- * docs/x16.md:38-54): gate_up writes the rotated fp16 down-input rows (act_rows, or the workspace's own copy when
- * NULL); down reads them, writes y_rows and, when out != NULL, also combines into out with the routing weights w. Use
- * the same workspace for both, gate_up first. */
-int bmx_moe_gate_up(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, void* act_rows_fp16,
-                    void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
-int bmx_moe_down(const bmx_moe_desc* desc, int T, const bmx_routes* routes, const void* act_rows_fp16, float* y_rows,
-                 const void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
+/* bmx_moe_experts one kernel at a time, for callers that schedule or time the stages apart (exllamav3's kernel A /
+ * kernel B split, docs/x16.md:38-54). Stages, in order, on the same workspace (bmx_experts_workspace):
+ *   BMX_STAGE_GATE_UP  gate / up split-K GEMV partial sums                         (reads x, routes)
+ *   BMX_STAGE_ACT      gate / up epilogue -> fp16 down-input rows (act_rows, or the workspace's copy when NULL)
+ *   BMX_STAGE_DOWN     down split-K GEMV partial sums                              (reads act rows)
+ *   BMX_STAGE_COMBINE  down epilogue + slot-ordered combine into out with weights w (y_rows also written if not NULL)
+ *   BMX_STAGE_DOWN_OUT down epilogue into y_rows for every row (instead of COMBINE) */
+enum bmx_stage { BMX_STAGE_GATE_UP = 0, BMX_STAGE_ACT = 1, BMX_STAGE_DOWN = 2, BMX_STAGE_COMBINE = 3, BMX_STAGE_DOWN_OUT = 4 };
+int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T, const bmx_routes* routes,
+                  void* act_rows_fp16, float* y_rows, const void* w_fp16, float* out, void* workspace,
+                  size_t workspace_bytes, int path, bmx_stream_t stream);
 
 /* Combine: out[t] = sum over k ascending of w[t, k] * y_rows[inv[t, k]] (picks with inv < 0 or w = 0 skipped), then
  * + y_rows[offsets[E] + t] when has_shared (x16_red_k order, engine/kernels/x16/x16_dev.cu:354-384). */
