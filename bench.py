@@ -227,6 +227,11 @@ def main():
     layer_gbps = q_bytes / (ms * 1e-3) / 1e9
 
     cpu = None if args.no_cpu else cpu_baseline(tab, sel, w)
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", f"decode_{args.config}_t{T}.json")
+    if os.path.exists(tpath):
+        tr = json.load(open(tpath))
+        traffic = tr["read_bytes"] + tr["write_bytes"]
     res = {
         "metric": METRIC,
         "value": round(T * 1e3 / ms, 2),
@@ -257,7 +262,9 @@ def main():
         "roofline": {"kernel": "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)",
                      "bound": "hbm", "achieved": round(gu_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "algorithmic_bytes": gu_bytes},
+                     "traffic": traffic, "algorithmic_bytes": gu_bytes,
+                     "traffic_source": "rocprofv3 FETCH_SIZE / WRITE_SIZE passes, calibrated by a 256 MiB copy "
+                                       f"(profiles/decode_{args.config}_t{T}.md)" if traffic else None},
         "cpu_baseline": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()} if cpu else None),
     }
     print(json.dumps(res), flush=True)
