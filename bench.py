@@ -1,12 +1,14 @@
 #!/usr/bin/env python3
 """MoE layer benchmark on one MI355X.
 
-A step is one pass of the hot path over one batch of synthetic input: router (fp16 logits -> top-k), dispatch, fused
-gate/up GEMV + epilogue, down GEMV + combine, for the GLM-shaped layer (288 routed experts, top-8 sigmoid + bias, one
-shared expert, H 4096, I 1536, EXL3 3 bpw; decode batch of 1 token by default). Inputs and all 289 experts are resident
-in HBM before the timed region. Prints one JSON line.
+A step is one pass of the hot path over one batch of synthetic input: router (fp16 logits -> top-k), dispatch, gate/up
+products + epilogue, down products + combine. Default workload: the GLM-shaped layer (288 routed experts, top-8
+sigmoid + bias, one shared expert, H 4096, I 1536, EXL3 3 bpw) on a decode batch of 1 token (bandwidth-bound GEMV
+path). --config c3 runs the DeepSeek-shaped 8192-token prefill layer (384 experts, group-limited top-6, H 4096, I 2048,
+EXL3 2 / 3 bpw, Zipf routing) on the MFMA path. Inputs and all experts are resident in HBM before the timed region.
+Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--no-cpu]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--tokens T] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -23,6 +25,7 @@ for _p in (REPO, os.path.join(REPO, "big-moe-small-box_amd")):
 
 METRIC = "MoE layer µs/token (decode) + prefill tok/s; HBM GB/s & MFMA util vs peak"
 HBM_PEAK_GBPS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
 
 
 def log(*a):
@@ -58,6 +61,7 @@ def cpu_model():
 
 
 def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
+    # sel / w: the routes of the bounded sample (the first tokens of the timed batch)
     """The reference's CPU lane (ft_n135.h moe_forward4, built from the reference sources into oracle/_ref) on the same
     routes, driven as the reference's cpu_forward drives it (nv2_host.cpp:1974-2003): experts in RAM, routes given (no
     router), mode auto, the shared expert as a weight-1 job. Median of warm calls, whole-call wall time."""
@@ -105,8 +109,9 @@ def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
     finally:
         R.ref_lane_destroy()
     return {"value": T / med, "unit": "tokens/s", "cores": len(cpus), "kind": "reference",
-            "sample": f"{len(times)} calls of the same {T}-token layer call ({k} jobs per token incl. the shared "
-                      f"expert), median wall time {med * 1e6:.0f} us; moe_forward4 mode auto, {len(cpus)} threads "
+            "sample": f"{len(times)} calls of one {T}-token layer call (the routes of the first {T} tokens of the timed "
+                      f"batch, {k} jobs per token{' incl. the shared expert' if tab.has_shared else ''}), median wall "
+                      f"time {med * 1e6:.0f} us; moe_forward4 mode auto, {len(cpus)} threads "
                       f"pinned one per physical core ({ncores} physical cores available), {cpu_model()}",
             "us_per_layer": med * 1e6}
 
@@ -116,7 +121,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--tokens", type=int, default=None, help="tokens per step (default: the config's batch)")
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
@@ -133,7 +138,7 @@ def main():
 
     dev = torch.device("cuda:0")
     c = synth.CONFIGS[args.config]
-    T = args.tokens
+    T = args.tokens or c["T"]
     log(f"bench: building {args.config} table (E={c['E']}, H={c['H']}, I={c['I']})")
     tab = synth.table(args.config, seed=0, device=dev)
     x, lg, bias = synth.inputs(args.config, T=T, seed=0, device=dev)
@@ -194,20 +199,24 @@ def main():
         raise RuntimeError("graph replay output differs from the eager call")
     ms = min(ms_eager, ms_graph)
 
-    # per-stage timing with events on the launch stream (torch's current stream): gate/up (dominant) and down+combine
+    # per-stage timing with events on the launch stream (torch's current stream)
+    L = bmx.lib()
+    topk = layer.num_experts_per_tok
+    path = L.bmx_resolve_path(T, topk, 0)
+    prefill = path == bmx._lib.PATH_PREFILL
     sel, w = sel_b.clone(), w_b.clone()
-    rpg = bmx.lib().bmx_rows_per_group(T, 0)
-    routes = bmx.ops.dispatch(sel, tab.E, 0, tab.has_shared, rpg)
+    routes = bmx.ops.dispatch(sel, tab.E, 0, tab.has_shared, L.bmx_rows_per_group(T, topk, 0))
     desc = layer.desc
-    need = bmx.lib().bmx_experts_workspace(ctypes.byref(desc), T, 0)
+    need = L.bmx_experts_workspace(ctypes.byref(desc), T, 0)
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
-    y = torch.empty((routes.R, tab.H), dtype=torch.float32, device=dev)
     out = torch.empty((T, tab.H), dtype=torch.float32, device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    stages = [("gate_up", bmx._lib.STAGE_GATE_UP), ("act", bmx._lib.STAGE_ACT), ("down", bmx._lib.STAGE_DOWN),
-              ("combine", bmx._lib.STAGE_COMBINE)]
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(args.steps)]
-    for i in range(args.steps + args.warmup):
+    stages = ([("prep", bmx._lib.STAGE_PREP)] if prefill else []) + [
+        ("gate_up", bmx._lib.STAGE_GATE_UP), ("act", bmx._lib.STAGE_ACT), ("down", bmx._lib.STAGE_DOWN),
+        ("combine", bmx._lib.STAGE_COMBINE)]
+    nst = min(args.steps, 50) if prefill else args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(nst)]
+    for i in range(nst + args.warmup):
         e = evs[i - args.warmup] if i >= args.warmup else None
         for j, (_, st) in enumerate(stages):
             if e: e[j].record()
@@ -217,21 +226,44 @@ def main():
     torch.cuda.synchronize()
     stage_ms = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j, (name, _) in enumerate(stages)}
     gu_ms = stage_ms["gate_up"]
-    experts = set(sel.cpu().numpy().ravel().tolist())
+    sel_np = sel.cpu().numpy()
+    experts = set(int(e) for e in sel_np.ravel() if 0 <= e < tab.E)
     if tab.has_shared:
         experts.add(tab.E)
     gu_bytes = sum(tab.mat_bytes(e, 0) + tab.mat_bytes(e, 1) for e in experts)
     dn_bytes = sum(tab.mat_bytes(e, 2) for e in experts)
     q_bytes = gu_bytes + dn_bytes
-    gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
-    layer_gbps = q_bytes / (ms * 1e-3) / 1e9
+    rows = routes.rows()
+    layer_flops = synth.flops(tab.H, tab.I, rows)
+    gu_flops = 4.0 * tab.H * tab.I * rows
 
-    cpu = None if args.no_cpu else cpu_baseline(tab, sel, w)
+    n_cpu = T if T <= 64 else 64
+    cpu = None if args.no_cpu else cpu_baseline(tab, sel[:n_cpu], w[:n_cpu])
     traffic = None
-    tpath = os.path.join(REPO, "profiles", f"decode_{args.config}_t{T}.json")
+    kind = "prefill" if prefill else "decode"
+    tpath = os.path.join(REPO, "profiles", f"{kind}_{args.config}_t{T}.json")
     if os.path.exists(tpath):
         tr = json.load(open(tpath))
         traffic = tr["read_bytes"] + tr["write_bytes"]
+    traffic_src = (f"rocprofv3 FETCH_SIZE / WRITE_SIZE passes, calibrated by a 256 MiB copy "
+                   f"(profiles/{kind}_{args.config}_t{T}.md)") if traffic else None
+    if prefill:
+        ach = gu_flops / (gu_ms * 1e-3) / 1e12
+        roofline = {"kernel": "k_pf_gemm<2> (BMX_STAGE_GATE_UP: trellis decode to LDS + gate/up MFMA grouped GEMM)",
+                    "bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(ach / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": traffic, "algorithmic_flops": gu_flops,
+                    "traffic_source": traffic_src}
+    else:
+        gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
+        roofline = {"kernel": "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)",
+                    "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "algorithmic_bytes": gu_bytes,
+                    "traffic_source": traffic_src}
+    layer_gbps = q_bytes / (ms * 1e-3) / 1e9
+    scores = {0: "softmax", 1: "sigmoid"}[c["score"]] + ("+bias" if c["bias"] else "")
+    if c["n_group"] > 1:
+        scores = f"group-limited ({c['n_group']} groups, top-{c['topk_group']}) {scores}"
+    bpw = {"c1": "4", "c2": "3", "c3": "2/3 mixed", "c4": "3", "c5": "2/2.5 mixed"}[args.config]
     res = {
         "metric": METRIC,
         "value": round(T * 1e3 / ms, 2),
@@ -245,12 +277,11 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic: random EXL3 trellis codes, suh ~ U(0.5,1.5), svh ~ U(0.5,1.5)/sqrt(k), x ~ N(0,1) fp16, "
-                "router logits ~ N(0,1) fp16, bias ~ N(0,0.1); seed 0",
-        "config": {"workload": f"{args.config} decode layer: {c['E']} routed experts top-{c['topk']} "
-                               f"{'sigmoid+bias' if c['bias'] else 'softmax' if c['score'] == 0 else 'sigmoid'}"
-                               f"{' + 1 shared' if c['shared'] else ''}, H {c['H']}, I {c['I']}, EXL3 "
-                               f"{ {'c1': '4', 'c2': '3', 'c4': '3'}.get(args.config, 'mixed') } bpw",
-                   "tokens": T, "step": "router + dispatch + gate/up + down + combine"},
+                + ("router logits = Zipf(1.1) log-popularity + Gumbel noise" if args.config in ("c3", "c4") else
+                   "router logits ~ N(0,1) fp16") + (", bias ~ N(0,0.1)" if c["bias"] else "") + "; seed 0",
+        "config": {"workload": f"{args.config} {kind} layer: {c['E']} routed experts top-{c['topk']} {scores}"
+                               f"{' + 1 shared' if c['shared'] else ''}, H {c['H']}, I {c['I']}, EXL3 {bpw} bpw",
+                   "tokens": T, "path": kind, "step": "router + dispatch + gate/up + down + combine"},
         "timing": "min of eager launches and HIP-graph replay of the same bmx_moe_layer call",
         "us_per_layer_eager": round(ms_eager * 1e3, 3),
         "us_per_layer_graph": round(ms_graph * 1e3, 3),
@@ -258,13 +289,10 @@ def main():
         "us_per_layer": round(ms * 1e3, 3),
         "quantized_bytes_per_layer": q_bytes,
         "layer_hbm_gbps": round(layer_gbps, 1),
+        "layer_tflops": round(layer_flops / (ms * 1e-3) / 1e12, 1),
+        "layer_mfma_frac": round(layer_flops / (ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
         "stage_us": {k: round(v * 1e3, 3) for k, v in stage_ms.items()},
-        "roofline": {"kernel": "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)",
-                     "bound": "hbm", "achieved": round(gu_gbps, 1),
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "algorithmic_bytes": gu_bytes,
-                     "traffic_source": "rocprofv3 FETCH_SIZE / WRITE_SIZE passes, calibrated by a 256 MiB copy "
-                                       f"(profiles/decode_{args.config}_t{T}.md)" if traffic else None},
+        "roofline": roofline,
         "cpu_baseline": ({k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()} if cpu else None),
     }
     print(json.dumps(res), flush=True)

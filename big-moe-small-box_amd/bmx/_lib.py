@@ -11,7 +11,7 @@ TILE_BYTES = {TF_K2: 64, TF_K25: 80, TF_K3: 96, TF_K4: 128}
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
-STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT = 0, 1, 2, 3, 4
+STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT, STAGE_PREP = 0, 1, 2, 3, 4, 5
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -52,7 +52,8 @@ SIGNATURES = {
     "bmx_dispatch": (_I, [_P, _I, _I, _I, _I64, _I, _I, ctypes.POINTER(Routes), _P, _SZ, _P]),
     "bmx_moe_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_forward": (_I, [ctypes.POINTER(MoeDesc), _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
-    "bmx_rows_per_group": (_I, [_I, _I]),
+    "bmx_rows_per_group": (_I, [_I, _I, _I]),
+    "bmx_resolve_path": (_I, [_I, _I, _I]),
     "bmx_experts_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_experts": (_I, [ctypes.POINTER(MoeDesc), _P, _I, ctypes.POINTER(Routes), _P, _P, _P, _SZ, _I, _P]),
     "bmx_moe_stage": (_I, [ctypes.POINTER(MoeDesc), _I, _P, _I, ctypes.POINTER(Routes), _P, _P, _P, _P, _P, _SZ, _I, _P]),

@@ -64,9 +64,15 @@ class RoutesBuf:
         self.ngroups = torch.zeros(1, **i32)
         self.row_expert = torch.full((max(R, 1),), -1, **i32)
         self.T, self.topk, self.E, self.shared, self.R = T, topk, E, bool(shared), R
+        self.NE = E + (1 if shared else 0)       # segments written: offsets[0 .. NE]
         self.struct = L.Routes(*[t.data_ptr() for t in (self.counts, self.offsets, self.row_token, self.row_slot,
                                                           self.inv, self.uexp, self.nuniq, self.groups, self.ngroups,
                                                           self.row_expert)])
+
+
+    def rows(self):
+        """Dispatch rows in use (synchronises)."""
+        return int(self.offsets[self.NE].item())
 
 
 def dispatch(sel, E, first=0, shared=False, rows_per_group=8):

@@ -58,4 +58,11 @@ int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const
                    int H, int E, int has_shared, float* out, hipStream_t s);
 int launch_zero_i32(int32_t* p, int n, hipStream_t s);
 
+// moe_prefill.hip (same ws / stage conventions; ws layout [xt][part_gu][act rows][part_dn])
+int prefill_rows_per_group();
+size_t prefill_ws_bytes(const MoeShape& m);
+int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
+                           void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s,
+                           int stages);
+
 }  // namespace bmx

@@ -4,6 +4,7 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 namespace bmx {
@@ -88,13 +89,35 @@ static bmx_routes routes_at(char* base, const RoutesLayout& L)
     return r;
 }
 
-constexpr int STAGES_LAYER = (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) | (1 << BMX_STAGE_COMBINE);
+constexpr int STAGES_LAYER = (1 << BMX_STAGE_PREP) | (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) | (1 << BMX_STAGE_COMBINE);
 
-static int resolve_path(int path, int T)
+// AUTO takes the MFMA path from this many routed rows (T * topk) up, the GEMV path below
+static long prefill_min_rows()
 {
-    (void)T;
-    if (path == BMX_PATH_AUTO || path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL) return BMX_PATH_DECODE;
+    const char* v = getenv("BMX_PREFILL_MIN_ROWS");
+    return (v && *v) ? atol(v) : 512;
+}
+
+static int resolve_path(int path, int T, int topk)
+{
+    if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL) return path;
+    if (path == BMX_PATH_AUTO) return (long)T * topk >= prefill_min_rows() ? BMX_PATH_PREFILL : BMX_PATH_DECODE;
     return -1;
+}
+
+static int path_rows_per_group(int path, int T) { return path == BMX_PATH_PREFILL ? prefill_rows_per_group() : decode_rows_per_group(T); }
+
+static size_t experts_ws_bytes(int path, const MoeShape& m)
+{
+    return path == BMX_PATH_PREFILL ? prefill_ws_bytes(m) : decode_ws_bytes(m);
+}
+
+static int launch_experts(int path, const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
+                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages)
+{
+    if (path == BMX_PATH_PREFILL)
+        return launch_prefill_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
+    return launch_decode_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
 }
 
 }  // namespace bmx
@@ -140,16 +163,21 @@ int bmx_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int 
                            static_cast<hipStream_t>(stream));
 }
 
-int bmx_rows_per_group(int T, int path)
+int bmx_rows_per_group(int T, int topk, int path)
 {
-    if (resolve_path(path, T) < 0 || T < 0) return -1;
-    return decode_rows_per_group(T);
+    const int p = resolve_path(path, T, topk);
+    if (p < 0 || T < 0 || topk <= 0) return -1;
+    return path_rows_per_group(p, T);
 }
+
+int bmx_resolve_path(int T, int topk, int path) { return T < 0 || topk <= 0 ? -1 : resolve_path(path, T, topk); }
 
 size_t bmx_experts_workspace(const bmx_moe_desc* desc, int T, int path)
 {
-    if (check_desc(desc, "bmx_experts_workspace") || resolve_path(path, T) < 0 || T < 0) return 0;
-    return decode_ws_bytes(shape_of(desc, T));
+    if (check_desc(desc, "bmx_experts_workspace") || T < 0) return 0;
+    const int p = resolve_path(path, T, desc->topk);
+    if (p < 0) return 0;
+    return experts_ws_bytes(p, shape_of(desc, T));
 }
 
 int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, float* y_rows,
@@ -157,13 +185,15 @@ int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const b
 {
     int rc = check_desc(desc, "bmx_moe_experts");
     if (rc) return rc;
-    if (resolve_path(path, T) < 0) return set_error(BMX_ERR_ARG, "bmx_moe_experts: unknown path %d", path);
+    const int p = resolve_path(path, T, desc->topk);
+    if (p < 0) return set_error(BMX_ERR_ARG, "bmx_moe_experts: unknown path %d", path);
     if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_experts: T < 0");
     if (T == 0) return BMX_OK;
     if (!x_fp16 || !routes || !y_rows || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_experts: null pointer");
-    return launch_decode_experts(shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
+    return launch_experts(p, shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
                                  nullptr, nullptr, static_cast<hipStream_t>(stream),
-                                 (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) | (1 << BMX_STAGE_DOWN_OUT));
+                                 (1 << BMX_STAGE_PREP) | (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) |
+                                 (1 << BMX_STAGE_DOWN_OUT));
 }
 
 int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T, const bmx_routes* routes,
@@ -172,15 +202,17 @@ int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T
 {
     int rc = check_desc(desc, "bmx_moe_stage");
     if (rc) return rc;
-    if (resolve_path(path, T) < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_stage: bad path or T");
-    if (stage < BMX_STAGE_GATE_UP || stage > BMX_STAGE_DOWN_OUT) return set_error(BMX_ERR_ARG, "bmx_moe_stage: unknown stage %d", stage);
+    const int p = resolve_path(path, T, desc->topk);
+    if (p < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_stage: bad path or T");
+    if (stage < BMX_STAGE_GATE_UP || stage > BMX_STAGE_PREP) return set_error(BMX_ERR_ARG, "bmx_moe_stage: unknown stage %d", stage);
     if (T == 0) return BMX_OK;
     if (!routes || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_stage: null pointer");
-    if (stage == BMX_STAGE_GATE_UP && !x_fp16) return set_error(BMX_ERR_ARG, "bmx_moe_stage: gate/up needs x");
+    if ((stage == BMX_STAGE_GATE_UP || stage == BMX_STAGE_PREP) && !x_fp16)
+        return set_error(BMX_ERR_ARG, "bmx_moe_stage: gate/up needs x");
     if (stage == BMX_STAGE_COMBINE && (!out || !w_fp16)) return set_error(BMX_ERR_ARG, "bmx_moe_stage: combine needs out and w");
     if (stage == BMX_STAGE_DOWN_OUT && !y_rows) return set_error(BMX_ERR_ARG, "bmx_moe_stage: down_out needs y_rows");
-    return launch_decode_experts(shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
-                                 out, w_fp16, static_cast<hipStream_t>(stream), 1 << stage);
+    return launch_experts(p, shape_of(desc, T), x_fp16, routes, y_rows, act_rows_fp16, workspace, workspace_bytes,
+                          out, w_fp16, static_cast<hipStream_t>(stream), 1 << stage);
 }
 
 int bmx_combine(const float* y_rows, const int32_t* inv, const void* w_fp16, const int32_t* offsets, int T, int topk,
@@ -194,13 +226,12 @@ int bmx_combine(const float* y_rows, const int32_t* inv, const void* w_fp16, con
 
 size_t bmx_moe_workspace(const bmx_moe_desc* desc, int T, int path)
 {
-    if (check_desc(desc, "bmx_moe_workspace") || resolve_path(path, T) < 0 || T < 0) return 0;
+    if (check_desc(desc, "bmx_moe_workspace") || T < 0) return 0;
+    const int p = resolve_path(path, T, desc->topk);
+    if (p < 0) return 0;
     const MoeShape m = shape_of(desc, T);
-    const int rpg = decode_rows_per_group(T);
-    const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
-    const size_t R = (size_t)T * desc->topk + (m.shared ? T : 0);
-    (void)R;
-    return L.total + align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256) + align_up(decode_ws_bytes(m), 256);
+    const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, path_rows_per_group(p, T));
+    return L.total + align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256) + align_up(experts_ws_bytes(p, m), 256);
 }
 
 int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const int64_t* sel, const void* w_fp16,
@@ -208,7 +239,8 @@ int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const i
 {
     int rc = check_desc(desc, "bmx_moe_forward");
     if (rc) return rc;
-    if (resolve_path(path, T) < 0) return set_error(BMX_ERR_ARG, "bmx_moe_forward: unknown path %d", path);
+    const int p = resolve_path(path, T, desc->topk);
+    if (p < 0) return set_error(BMX_ERR_ARG, "bmx_moe_forward: unknown path %d", path);
     if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_forward: T < 0");
     if (T == 0) return BMX_OK;
     if (!x_fp16 || !sel || !w_fp16 || !out || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_forward: null pointer");
@@ -216,17 +248,17 @@ int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const i
     if (workspace_bytes < need) return set_error(BMX_ERR_WORKSPACE, "bmx_moe_forward: workspace %zu < %zu", workspace_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const MoeShape m = shape_of(desc, T);
-    const int rpg = decode_rows_per_group(T);
+    const int rpg = path_rows_per_group(p, T);
     const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
     char* base = static_cast<char*>(workspace);
     const bmx_routes r = routes_at(base, L);
     char* dws = base + L.total;
     const size_t dws_bytes = align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256);
     char* ews = dws + dws_bytes;
-    const size_t ews_bytes = align_up(decode_ws_bytes(m), 256);
+    const size_t ews_bytes = align_up(experts_ws_bytes(p, m), 256);
     rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr, 0, s);
     if (rc) return rc;
-    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
+    return launch_experts(p, m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
 }
 
 size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path) { return bmx_moe_workspace(desc, T, path); }
@@ -238,7 +270,8 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
     int rc = check_desc(desc, "bmx_moe_layer");
     if (rc) return rc;
     if (!router) return set_error(BMX_ERR_ARG, "bmx_moe_layer: null router descriptor");
-    if (resolve_path(path, T) < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: unknown path %d", path);
+    const int p = resolve_path(path, T, desc->topk);
+    if (p < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: unknown path %d", path);
     if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: T < 0");
     if (T == 0) return BMX_OK;
     if (!x_fp16 || !logits_fp16 || !sel || !w_fp16 || !out || !workspace)
@@ -247,14 +280,14 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
     if (workspace_bytes < need) return set_error(BMX_ERR_WORKSPACE, "bmx_moe_layer: workspace %zu < %zu", workspace_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const MoeShape m = shape_of(desc, T);
-    const int rpg = decode_rows_per_group(T);
+    const int rpg = path_rows_per_group(p, T);
     const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
     char* base = static_cast<char*>(workspace);
     const bmx_routes r = routes_at(base, L);
     char* dws = base + L.total;
     const size_t dws_bytes = align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256);
     char* ews = dws + dws_bytes;
-    const size_t ews_bytes = align_up(decode_ws_bytes(m), 256);
+    const size_t ews_bytes = align_up(experts_ws_bytes(p, m), 256);
     if (route_dispatch_small_fits(T, desc->E, desc->topk))
         rc = launch_route_dispatch_small(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group,
                                          router->topk_group, router->score_fn, router->renorm, router->scale,
@@ -266,7 +299,7 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
         if (!rc) rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr, 0, s);
     }
     if (rc) return rc;
-    return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
+    return launch_experts(p, m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
 }
 
 }  // extern "C"

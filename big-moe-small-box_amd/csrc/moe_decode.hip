@@ -13,8 +13,7 @@
 //   k_dn_combine       : splits summed in order -> rotation * svh -> every token's slots summed in slot order, + the
 //                        shared expert                                     (exllamav3 kernel B, x16_red_k order)
 // The kernels hand data over only at kernel boundaries (no inter-workgroup flags or fences inside a kernel).
-#include "bmx_common.hpp"
-#include "bmx_internal.hpp"
+#include "moe_kernels.hpp"
 
 #include <stdlib.h>
 
@@ -23,47 +22,6 @@ namespace bmx {
 constexpr int GV_WAVES = 4;
 constexpr int GV_THREADS = GV_WAVES * 64;
 constexpr int GV_LDS_X = 32768;       // bytes of staged input rows per workgroup
-
-struct GvArgs {
-    const bmx_expert* experts;
-    const bmx_expert* shared;
-    int E, H, I, act, gated;
-    float limit;
-    const uint16_t* x;
-    const int32_t* row_token;
-    const int32_t* groups;
-    const int32_t* ngroups;
-    uint16_t* act_rows;
-    float* y_rows;
-    const int32_t* row_expert;
-    float* part_gu;
-    float* part_dn;
-    int KS_gu, KS_dn, NB, NBH, R_max, NE;
-    float* out;
-    const uint16_t* w;
-    const int32_t* inv;
-    const int32_t* offsets;
-    int T, topk, has_shared;
-};
-
-template <int F> struct RingTab {
-    int q[64];
-    constexpr RingTab() : q()
-    {
-        for (int i = 0; i < 64; ++i) q[i] = ring_end<F>(i) + 16;
-    }
-};
-
-// 16-bit state at bit q of a lane's window (MSB-first words: prev, own[0], own[1], ...); bits above 15 of the result
-// are left as they are
-template <int NW>
-__device__ __forceinline__ uint32_t win_state(uint32_t prev, const uint32_t (&own)[NW], int q)
-{
-    const int d = q >> 5, o = q & 31;
-    const uint32_t hi = d == 0 ? prev : own[d - 1];
-    if (o <= 16) return hi >> (16 - o);
-    return __builtin_amdgcn_alignbit(hi, own[d], 48 - o);
-}
 
 // One tile-row strip for this lane: 64 weights (stream positions 64 s .. 64 s + 63 of its tile) decoded and multiplied
 // with MR token rows. xr: LDS fp16 pairs of the strip's 16 input rows, 8 dwords per token row, token stride xstride.
@@ -84,20 +42,11 @@ __device__ __forceinline__ void strip(const uint32_t (&own)[Fmt<F>::TB / 16], co
     for (int jj = 0; jj < 64; jj += 2)
     {
         const f16x2 w2 = cb_pair(cb_hash(win_state(prev, own, tab.q[jj])), cb_hash(win_state(prev, own, tab.q[jj + 1])));
-        const int gg = jj >> 3, j = jj & 7;
-        const int cidx = (gg >> 2) + (j >= 4 ? 2 : 0);
-        const int dw = (gg & 3) + ((j & 2) ? 4 : 0);
+        const int cidx = strip_cidx(jj), dw = strip_dw(jj);
 #pragma unroll
         for (int m = 0; m < MR; ++m)
             acc[cidx][m] = __builtin_amdgcn_fdot2(w2, __builtin_bit_cast(f16x2, X[m][dw]), acc[cidx][m], false);
     }
-}
-
-template <int NW>
-__device__ __forceinline__ void load_words(uint32_t (&w)[NW], const uint8_t* p)
-{
-#pragma unroll
-    for (int i = 0; i < NW; ++i) w[i] = ldg_nt(p, i);
 }
 
 // A wave's GEMV over tile-rows [tr0, tr0 + ntr) (ntr even; the two half-waves take alternate rows) of the 128-column
@@ -137,13 +86,6 @@ __device__ __forceinline__ void gemv_any(int fmt, const uint8_t* mat, int tn, in
         case BMX_TF_K3: gemv_wave<BMX_TF_K3, MR>(mat, tn, cb, tr0, ntr, xs, xstride, xtr0, acc); break;
         default: gemv_wave<BMX_TF_K4, MR>(mat, tn, cb, tr0, ntr, xs, xstride, xtr0, acc); break;
     }
-}
-
-// lane's 4 columns inside the 128-column block
-__device__ __forceinline__ int lane_col(int lane, int c)
-{
-    const int t = (lane >> 2) & 7, s = lane & 3;
-    return t * 16 + 2 * s + (c & 1) + ((c & 2) ? 8 : 0);
 }
 
 // ---- split-K grouped GEMV -> partial sums ------------------------------------------------------------------------------
@@ -409,6 +351,24 @@ int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const
     return check_launch("bmx_combine");
 }
 
+int launch_epilogue(const GvArgs& a, int stage, hipStream_t s)
+{
+    switch (stage)
+    {
+        case BMX_STAGE_ACT:
+            hipLaunchKernelGGL(k_gu_epi, dim3((unsigned)((a.R_max * a.NB + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+            break;
+        case BMX_STAGE_COMBINE:
+            hipLaunchKernelGGL(k_dn_combine, dim3((unsigned)(a.T * a.NBH)), dim3(GV_THREADS), 0, s, a);
+            break;
+        case BMX_STAGE_DOWN_OUT:
+            hipLaunchKernelGGL(k_dn_epi, dim3((unsigned)((a.R_max * a.NBH + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+            break;
+        default: return set_error(BMX_ERR_ARG, "unknown epilogue stage %d", stage);
+    }
+    return BMX_OK;
+}
+
 // ---- plan ------------------------------------------------------------------------------------------------------------
 static int rows_per_group_of(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
 
@@ -468,7 +428,7 @@ size_t decode_ws_bytes(const MoeShape& m)
     return align_up(p.part_gu_bytes, 256) + align_up(p.part_dn_bytes, 256) + align_up((size_t)p.R_max * m.I * 2, 256);
 }
 
-// stages: bit i = BMX_STAGE i (GATE_UP, ACT, DOWN, COMBINE, DOWN_OUT)
+// stages: bit i = BMX_STAGE i (GATE_UP, ACT, DOWN, COMBINE, DOWN_OUT; PREP launches nothing here: the GEMV rotates)
 template <int MR>
 static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStream_t s)
 {
@@ -476,14 +436,11 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
     const size_t lds_dn = (size_t)MR * (a.I / p.KS_dn) / 2 * 4 + (size_t)GV_WAVES * MR * 128 * 4;
     if (stages & (1 << BMX_STAGE_GATE_UP))
         hipLaunchKernelGGL((k_gemv_part<MR, 2>), dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds_gu, s, a);
-    if (stages & (1 << BMX_STAGE_ACT))
-        hipLaunchKernelGGL(k_gu_epi, dim3((unsigned)((p.R_max * p.NB + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+    if (stages & (1 << BMX_STAGE_ACT)) launch_epilogue(a, BMX_STAGE_ACT, s);
     if (stages & (1 << BMX_STAGE_DOWN))
         hipLaunchKernelGGL((k_gemv_part<MR, 1>), dim3((unsigned)(p.G_max * p.NBH * p.KS_dn)), dim3(GV_THREADS), lds_dn, s, a);
-    if (stages & (1 << BMX_STAGE_COMBINE))
-        hipLaunchKernelGGL(k_dn_combine, dim3((unsigned)(a.T * p.NBH)), dim3(GV_THREADS), 0, s, a);
-    if (stages & (1 << BMX_STAGE_DOWN_OUT))
-        hipLaunchKernelGGL(k_dn_epi, dim3((unsigned)((p.R_max * p.NBH + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+    if (stages & (1 << BMX_STAGE_COMBINE)) launch_epilogue(a, BMX_STAGE_COMBINE, s);
+    if (stages & (1 << BMX_STAGE_DOWN_OUT)) launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
 }
 
 int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
@@ -511,6 +468,7 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
     a.NE = m.E + (m.shared ? 1 : 0);
     a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
+    a.xt = nullptr;
     switch (rows_per_group_of(m.T))
     {
         case 1: launch_mr<1>(a, p, stages, s); break;

@@ -1,0 +1,77 @@
+// Pieces shared by the decode (GEMV) and prefill (MFMA) expert-product kernels: the kernel argument block, the
+// in-register trellis window, and the epilogue kernels both paths hand their fp32 products to.
+#pragma once
+#include "bmx_common.hpp"
+#include "bmx_internal.hpp"
+
+namespace bmx {
+
+// Arguments of the expert-product kernels. Rows are dispatch rows (expert-major); `part_gu` / `part_dn` hold fp32 products
+// as [k-split][row][128-column block][matrix][128] (gate / up) and [k-split][row][128-column block][128] (down).
+struct GvArgs {
+    const bmx_expert* experts;
+    const bmx_expert* shared;
+    int E, H, I, act, gated;
+    float limit;
+    const uint16_t* x;
+    const int32_t* row_token;
+    const int32_t* groups;
+    const int32_t* ngroups;
+    uint16_t* act_rows;
+    float* y_rows;
+    const int32_t* row_expert;
+    float* part_gu;
+    float* part_dn;
+    int KS_gu, KS_dn, NB, NBH, R_max, NE;
+    float* out;
+    const uint16_t* w;
+    const int32_t* inv;
+    const int32_t* offsets;
+    int T, topk, has_shared;
+    uint16_t* xt;              // prefill: rotated gate / up input rows [2][R_max][H]
+};
+
+// S(i) + 16 for the 64 stream positions of a 64-weight strip (a strip starts on a 64-position boundary, where the ring
+// position is a whole number of 32-bit words for every format)
+template <int F> struct RingTab {
+    int q[64];
+    constexpr RingTab() : q()
+    {
+        for (int i = 0; i < 64; ++i) q[i] = ring_end<F>(i) + 16;
+    }
+};
+
+// 16-bit state at bit q of a lane's window (MSB-first words: prev, own[0], own[1], ...); bits above 15 of the result
+// are left as they are
+template <int NW>
+__device__ __forceinline__ uint32_t win_state(uint32_t prev, const uint32_t (&own)[NW], int q)
+{
+    const int d = q >> 5, o = q & 31;
+    const uint32_t hi = d == 0 ? prev : own[d - 1];
+    if (o <= 16) return hi >> (16 - o);
+    return __builtin_amdgcn_alignbit(hi, own[d], 48 - o);
+}
+
+template <int NW>
+__device__ __forceinline__ void load_words(uint32_t (&w)[NW], const uint8_t* p)
+{
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = ldg_nt(p, i);
+}
+
+// The strip of lane s (= lane & 3) of a tile: stream positions 64 s .. 64 s + 63, i.e. output columns
+// 2 s, 2 s + 1, 2 s + 8, 2 s + 9 of the tile, all 16 input rows. Pair jj (positions jj, jj + 1) is rows 2 dw, 2 dw + 1 of
+// column index cidx (make_tc_perm, engine/kernels/nv2/ft_core.h:49-62):
+__device__ __forceinline__ constexpr int strip_cidx(int jj) { return ((jj >> 3) >> 2) + ((jj & 7) >= 4 ? 2 : 0); }
+__device__ __forceinline__ constexpr int strip_dw(int jj) { return ((jj >> 3) & 3) + ((jj & 2) ? 4 : 0); }
+// the column (0..127) inside a 128-column block of strip column index c for lane `lane` (tile (lane >> 2) & 7)
+__device__ __forceinline__ int lane_col(int lane, int c)
+{
+    const int t = (lane >> 2) & 7, s = lane & 3;
+    return t * 16 + 2 * s + (c & 1) + ((c & 2) ? 8 : 0);
+}
+
+// epilogue kernels of moe_decode.hip, launched with the partial layout above (any k-split count)
+int launch_epilogue(const GvArgs& a, int stage, hipStream_t s);
+
+}  // namespace bmx

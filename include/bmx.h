@@ -43,7 +43,10 @@ enum bmx_score { BMX_SCORE_SOFTMAX = 0, BMX_SCORE_SIGMOID = 1 };
 /* expert activations, exllamav3's MOE_COOP_ACT_* numbering (engine/kernels/x16/x16_dev.cu:21-24) */
 enum bmx_act { BMX_ACT_SILU = 0, BMX_ACT_GELU = 1, BMX_ACT_RELU2 = 2, BMX_ACT_SILU_OAI = 3 };
 
-/* expert-products path */
+/* expert-products path: DECODE = bandwidth-bound grouped GEMVs (the reference's bsz-N decode kernel,
+ * engine/kernels/x16/x16_dev.cu:205-392), PREFILL = grouped GEMMs on MFMA (the reference's staged prefill call,
+ * engine/tiers.py:673-700). AUTO picks PREFILL from 512 routed rows (T * topk) up; the environment variable
+ * BMX_PREFILL_MIN_ROWS moves that threshold. */
 enum bmx_path { BMX_PATH_AUTO = 0, BMX_PATH_DECODE = 1, BMX_PATH_PREFILL = 2 };
 
 /* One expert: three EXL3 linears (gate [H->I], up [H->I], down [I->H]). Device-resident array, one entry per expert.
@@ -141,21 +144,27 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
                   int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
                   bmx_stream_t stream);
 
-/* Expert products only, on given routes (from bmx_dispatch with rows_per_group = bmx_rows_per_group(path)):
- * y_rows fp32 [R, H] (expert output of each dispatch row), act_rows fp16 [R, I] (the rotated down input) or NULL. */
-int bmx_rows_per_group(int T, int path);
+/* Expert products only, on given routes (from bmx_dispatch with rows_per_group = bmx_rows_per_group(T, topk, path)):
+ * y_rows fp32 [R, H] (expert output of each dispatch row), act_rows fp16 [R, I] (the rotated down input) or NULL.
+ * bmx_resolve_path: the path (DECODE or PREFILL) that `path` selects for T tokens of topk picks, -1 if invalid. */
+int bmx_rows_per_group(int T, int topk, int path);
+int bmx_resolve_path(int T, int topk, int path);
 size_t bmx_experts_workspace(const bmx_moe_desc* desc, int T, int path);
 int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const bmx_routes* routes, float* y_rows,
                     void* act_rows_fp16, void* workspace, size_t workspace_bytes, int path, bmx_stream_t stream);
 
 /* bmx_moe_experts one kernel at a time, for callers that schedule or time the stages apart (exllamav3's kernel A /
  * kernel B split, docs/x16.md:38-54). Stages, in order, on the same workspace (bmx_experts_workspace):
- *   BMX_STAGE_GATE_UP  gate / up split-K GEMV partial sums                         (reads x, routes)
+ *   BMX_STAGE_PREP     rotated gate / up inputs of every row (PREFILL path; nothing on DECODE, whose GEMV rotates)
+ *   BMX_STAGE_GATE_UP  gate / up products (DECODE: split-K GEMV partials; PREFILL: MFMA GEMM on the PREP rows)
  *   BMX_STAGE_ACT      gate / up epilogue -> fp16 down-input rows (act_rows, or the workspace's copy when NULL)
- *   BMX_STAGE_DOWN     down split-K GEMV partial sums                              (reads act rows)
+ *   BMX_STAGE_DOWN     down products                                               (reads act rows)
  *   BMX_STAGE_COMBINE  down epilogue + slot-ordered combine into out with weights w (y_rows also written if not NULL)
  *   BMX_STAGE_DOWN_OUT down epilogue into y_rows for every row (instead of COMBINE) */
-enum bmx_stage { BMX_STAGE_GATE_UP = 0, BMX_STAGE_ACT = 1, BMX_STAGE_DOWN = 2, BMX_STAGE_COMBINE = 3, BMX_STAGE_DOWN_OUT = 4 };
+enum bmx_stage {
+    BMX_STAGE_GATE_UP = 0, BMX_STAGE_ACT = 1, BMX_STAGE_DOWN = 2, BMX_STAGE_COMBINE = 3, BMX_STAGE_DOWN_OUT = 4,
+    BMX_STAGE_PREP = 5
+};
 int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T, const bmx_routes* routes,
                   void* act_rows_fp16, float* y_rows, const void* w_fp16, float* out, void* workspace,
                   size_t workspace_bytes, int path, bmx_stream_t stream);

@@ -200,7 +200,7 @@ def test_act_rows_match_oracle(cuda, oracle):
     tab = synth.table("c2", seed=4, device=cuda, E=16)
     x, lg, bias = synth.inputs("c2", T=2, seed=5, device=cuda)
     sel, w = bmx.ops.router_topk(lg[:, :16].contiguous(), 8, bias[:16].contiguous(), 1, 1, 1, True, 2.5)
-    rpg = bmx.lib().bmx_rows_per_group(2, 0)
+    rpg = bmx.lib().bmx_rows_per_group(2, 8, 0)
     routes = bmx.ops.dispatch(sel, 16, 0, True, rpg)
     y, act = bmx.ops.moe_experts(tab.desc(8), x, routes, with_act=True)
     torch.cuda.synchronize()
@@ -230,7 +230,7 @@ def test_combine_matches_standalone(cuda):
     sel, w = bmx.ops.router_topk(lg[:, :24].contiguous(), 8, bias[:24].contiguous(), 1, 1, 1, True, 2.5)
     d = tab.desc(8)
     out = bmx.ops.moe_forward(d, x, sel, w)
-    routes = bmx.ops.dispatch(sel, 24, 0, True, bmx.lib().bmx_rows_per_group(5, 0))
+    routes = bmx.ops.dispatch(sel, 24, 0, True, bmx.lib().bmx_rows_per_group(5, 8, 0))
     y, _ = bmx.ops.moe_experts(d, x, routes)
     out2 = bmx.ops.combine(y, routes, w, tab.H)
     assert torch.equal(out, out2)
