@@ -9,17 +9,15 @@
 // element is one fixed sum (k ascending in MFMA blocks), independent of scheduling.
 //
 //   k_pf_prep     : rotated gate / up inputs of every dispatch row, xt = RN16(H128(x * suh) * R)
-//   k_pf_gemm<2>  : gate and up products of one 128-column block -> fp32 [row][block][gate | up][128]
+//   k_pf_gemm<false> : gate or up products of one 256-column block -> fp32 [row][128-block][gate | up][128]
 //   (k_gu_epi)    : fp16 gate / up -> epilogue -> fp16 down-input rows (shared with the decode path)
-//   k_pf_gemm<1>  : down products of two 128-column blocks -> fp32 [row][block][128]
+//   k_pf_gemm<true>  : down products of one 256-column block -> fp32 [row][128-block][128]
 //   (k_dn_combine): rotation * svh, slots summed in slot order (shared with the decode path)
 #include "moe_kernels.hpp"
 
 namespace bmx {
 
-constexpr int PF_THREADS = 256;
 constexpr int PF_M = 128;                    // rows per group
-constexpr int PF_STAGE_U4 = 2 * 4 * 4 * 64;  // one LDS stage: [matrix 2][tile-row 4][32-column block 4][lane 64] x 16 B
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) u32x4* gptr_u32x4;
@@ -60,189 +58,281 @@ __global__ __launch_bounds__(256) void k_pf_prep(GvArgs a)
     }
 }
 
-// ---- B operand: one strip decoded into fragments ----------------------------------------------------------------------
-// Fragment (matrix, tile-row kt, 32-column block nb) holds, for MFMA lane L, the 8 input rows 8 (L / 32) .. + 7 of column
-// 32 nb + L % 32 as 4 dwords (rows 2d, 2d + 1 in dword d). A strip's column c supplies two fragments' worth (rows 0-7 and
-// 8-15); they are written as soon as the column is complete.
-template <int F>
-__device__ __forceinline__ void decode_to_lds(const uint32_t (&own)[Fmt<F>::TB / 16], u32x4* stage, int mat, int kt)
+// ---- LDS stages ------------------------------------------------------------------------------------------------------
+// A stage: [row 128][8 chunks of 16 B] = the k-step's 64 inputs of every row; chunk c of row r sits at slot
+//          c ^ ((r >> 1) & 7) of the row, so that the 16 lanes an LDS cycle serves (16 rows, one chunk) hit 16 different
+//          16-byte bank groups. Copied by the decode waves (each lane 32 B of one row) from registers loaded two steps
+//          ahead.
+// B stage: fragment f = tile-row * 8 + 32-column block (of the 256), 64 lanes x 16 B; lane L's 16 B at slot
+//          f * 64 + bsw(f, L), bsw(f, L) = L ^ ((L >> 4) & 1) ^ ((f & 1) << 3): a bijection on each 16-lane block (the
+//          MFMA reads stay conflict-free) that spreads the 16 lanes of a decode store over 16 bank groups.
+constexpr int PF_A_U4 = 128 * 8;
+constexpr int PF_B_U4 = 4 * 8 * 64;
+__shared__ u32x4 pf_a0[PF_A_U4];
+__shared__ u32x4 pf_a1[PF_A_U4];
+__shared__ u32x4 pf_b0[PF_B_U4];
+__shared__ u32x4 pf_b1[PF_B_U4];
+
+__device__ __forceinline__ u32x4* a_stage(int s) { return s == 0 ? pf_a0 : pf_a1; }
+__device__ __forceinline__ u32x4* b_stage(int s) { return s == 0 ? pf_b0 : pf_b1; }
+__device__ __forceinline__ int bsw(int f, int L) { return L ^ ((L >> 4) & 1) ^ ((f & 1) << 3); }
+
+// Step barrier: the wave's LDS operations are done (its global loads, register prefetches for later steps, may still be in
+// flight; the compiler waits for those where their registers are used).
+__device__ __forceinline__ void step_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0); vmcnt (63) and expcnt (7) at their maxima: no wait
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ---- B operand: half a strip decoded into fragments -------------------------------------------------------------------
+// Fragment (tile-row kt, 32-column block nb) holds, for MFMA lane L, the 8 input rows 8 (L / 32) .. + 7 of column
+// 32 nb + L % 32 as 4 dwords (rows 2d, 2d + 1 in dword d). Stream positions 32 HALF .. 32 HALF + 31 of a lane's strip are
+// columns HALF and HALF + 2 of its four, all 16 rows: two columns' worth of fragments. col0: the first column of the
+// lane's 128-column half of the block.
+template <int F, int HALF>
+__device__ __forceinline__ void decode_half(const uint32_t (&own)[Fmt<F>::TB / 16], u32x4* __restrict__ stage, int kt,
+                                            int col0)
 {
     constexpr int NW = Fmt<F>::TB / 16;
     constexpr RingTab<F> tab;
     const int lane = threadIdx.x & 63;
+    // every word of the window is consumed here (a half strip reads only some of them): keeps the prefetched registers
+    // allocated until now instead of reused while their load is in flight, which would force a wait on it
+#pragma unroll
+    for (int k = 0; k < NW; ++k) asm volatile("" :: "v"(own[k]));
     const uint32_t prev = __builtin_amdgcn_mov_dpp(own[NW - 1], 0x93, 0xf, 0xf, false);
+    uint32_t fr[2][8];
 #pragma unroll
-    for (int half = 0; half < 2; ++half)
+    for (int jj = 32 * HALF; jj < 32 * HALF + 32; jj += 2)
     {
-        // positions 32 half .. 32 half + 31 complete columns c = half and half + 2
-        uint32_t fr[2][8];
+        const f16x2 w2 = cb_pair(cb_hash(win_state(prev, own, tab.q[jj])), cb_hash(win_state(prev, own, tab.q[jj + 1])));
+        fr[strip_cidx(jj) >> 1][strip_dw(jj)] = __builtin_bit_cast(uint32_t, w2);
+    }
 #pragma unroll
-        for (int jj = 32 * half; jj < 32 * half + 32; jj += 2)
-        {
-            const f16x2 w2 = cb_pair(cb_hash(win_state(prev, own, tab.q[jj])), cb_hash(win_state(prev, own, tab.q[jj + 1])));
-            fr[strip_cidx(jj) >> 1][strip_dw(jj)] = __builtin_bit_cast(uint32_t, w2);
-        }
-#pragma unroll
-        for (int ci = 0; ci < 2; ++ci)
-        {
-            const int col = lane_col(lane, half + 2 * ci);
-            u32x4* f = stage + ((mat * 4 + kt) * 4 + (col >> 5)) * 64 + (col & 31);
-            f[0] = u32x4{fr[ci][0], fr[ci][1], fr[ci][2], fr[ci][3]};
-            f[32] = u32x4{fr[ci][4], fr[ci][5], fr[ci][6], fr[ci][7]};
-        }
+    for (int ci = 0; ci < 2; ++ci)
+    {
+        const int col = col0 + lane_col(lane, HALF + 2 * ci);
+        const int f = kt * 8 + (col >> 5);
+        u32x4* fp = stage + f * 64;
+        fp[bsw(f, col & 31)] = u32x4{fr[ci][0], fr[ci][1], fr[ci][2], fr[ci][3]};
+        fp[bsw(f, (col & 31) + 32)] = u32x4{fr[ci][4], fr[ci][5], fr[ci][6], fr[ci][7]};
     }
 }
 
 // ---- grouped GEMM ----------------------------------------------------------------------------------------------------
-// NM = 2: gate and up of 128-column block cb (A = the matrix's rotated rows); NM = 1: down, 128-column blocks 2 cb and
-// 2 cb + 1 (A = the down-input rows for both). Wave w: MFMA rows 64 (w & 1) .. + 63 and 32-column blocks 2 (w >> 1),
-// 2 (w >> 1) + 1 of both matrices; decode of matrix w >> 1, tile-rows 2 (w & 1) + (lane >> 5) of each step.
-struct PfWave {
-    const uint16_t* arow[2][2];   // [A source][row block] lane's A row (+ its k offset)
-    bool mvalid[2];               // row block has rows
-    bool bvalid;                  // second matrix exists (down with an odd block count: the last one does not)
+// Work unit: (group of <= 128 rows, matrix, 256-column block); 12 waves, one barrier per k-step (64 k). While waves 0-3
+// run the MFMAs of step i from A / B stage i % 2, waves 4-11 stage step i + 1: they store the A rows loaded two steps
+// earlier and the B fragments decoded from trellis words loaded two steps earlier, and issue the loads of step i + 3.
+// Each SIMD holds one MFMA wave and two decode waves, so the decode (VALU; two waves hide its latency) overlaps the MFMAs.
+//   MFMA wave w: rows 64 (w & 1) .. + 63 (2 row blocks) x columns 128 (w >> 1) .. + 127 (4 column blocks).
+//   decode wave 4 + d: tile-rows 2 (d >> 2) + (lane >> 5), 128-column half (d >> 1) & 1, strip half d & 1; A rows
+//     16 d .. 16 d + 15, 32 B per lane.
+// DOWN = false: gate (matrix 0) or up (1) of the rotated input rows; DOWN = true: down of the down-input rows.
+constexpr int PF_WAVES = 12;
+
+struct PfJob {
+    int g, mat, cb, e, r0, nr, K, N, nb128;
+    const bmx_expert* ex;
 };
 
-template <int NM>
-__device__ __forceinline__ void mfma_step(const u32x4* stage, const PfWave& wv, int k0, f32x16 (&acc)[2][2][2])
+// Every MFMA wave runs all its rows and columns: rows past the group's end hold copies of its last row and a missing
+// second 128-column half holds stale LDS, and neither is stored. (On a small group the MFMAs cost nothing: the step's
+// decode takes longer.)
+struct PfFrag {
+    f16x8 a[2];      // [row block]
+    f16x8 b[4];      // [column block]
+};
+
+__device__ __forceinline__ void pf_frag_load(PfFrag& f, const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, int ks)
 {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wn = wave >> 1;
-    constexpr int NA = NM == 2 ? 2 : 1;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave & 1, wn = wave >> 1;
+    const int slot = (2 * ks + (lane >> 5)) ^ ((lane >> 1) & 7);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int mb = 0; mb < 2; ++mb) f.a[mb] = __builtin_bit_cast(f16x8, sa[(64 * wm + 32 * mb + (lane & 31)) * 8 + slot]);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
     {
-        f16x8 af[NA][2];
-#pragma unroll
-        for (int m = 0; m < NA; ++m)
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) af[m][mb] = __builtin_bit_cast(f16x8, ldg4(wv.arow[m][mb] + k0 + 16 * ks));
-#pragma unroll
-        for (int mat = 0; mat < 2; ++mat)
-        {
-            if (mat == 1 && !wv.bvalid) continue;
-#pragma unroll
-            for (int nb2 = 0; nb2 < 2; ++nb2)
-            {
-                const f16x8 bf = __builtin_bit_cast(f16x8, stage[((mat * 4 + ks) * 4 + 2 * wn + nb2) * 64 + lane]);
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-                    if (wv.mvalid[mb])
-                        acc[mat][mb][nb2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[NM == 2 ? mat : 0][mb], bf,
-                                                                                   acc[mat][mb][nb2], 0, 0, 0);
-            }
-        }
+        const int fi = ks * 8 + 4 * wn + nb;
+        f.b[nb] = __builtin_bit_cast(f16x8, sb[fi * 64 + bsw(fi, lane)]);
     }
 }
 
-template <int F, int NM>
-__device__ __forceinline__ void pf_loop(u32x4 (*stages)[PF_STAGE_U4], const uint8_t* mat_base, int tn, int dcb,
-                                        bool dvalid, int K, const PfWave& wv, f32x16 (&acc)[2][2][2])
+__device__ __forceinline__ void pf_frag_mfma(const PfFrag& f, f32x16 (&acc)[2][4])
+{
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+            acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[mb], f.b[nb], acc[mb][nb], 0, 0, 0);
+}
+
+// one k-step of an MFMA wave: 4 sub-steps of 16 k, the fragments of sub-step ks + 1 read while those of ks feed the MFMAs
+__device__ __forceinline__ void pf_mfma_step(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb,
+                                             f32x16 (&acc)[2][4])
+{
+    PfFrag f0, f1;
+    pf_frag_load(f0, sa, sb, 0);
+    pf_frag_load(f1, sa, sb, 1);
+    pf_frag_mfma(f0, acc);
+    pf_frag_load(f0, sa, sb, 2);
+    pf_frag_mfma(f1, acc);
+    pf_frag_load(f1, sa, sb, 3);
+    pf_frag_mfma(f0, acc);
+    pf_frag_mfma(f1, acc);
+}
+
+// A rows of one k-step: lane's 32 bytes (chunks 2 (lane & 3), + 1) of row 16 d + (lane >> 2)
+struct PfArow {
+    u32x4 c[2];
+};
+
+__device__ __forceinline__ void a_fetch(PfArow& r, const uint16_t* rowp, int k0)
+{
+    const int lane = threadIdx.x & 63;
+    const uint16_t* p = rowp + k0 + 16 * (lane & 3);
+    r.c[0] = ldg4(p);
+    r.c[1] = ldg4(p + 8);
+}
+
+__device__ __forceinline__ void a_store(const PfArow& r, u32x4* __restrict__ stage, int row)
+{
+    const int lane = threadIdx.x & 63, x = (row >> 1) & 7;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) stage[row * 8 + ((2 * (lane & 3) + j) ^ x)] = r.c[j];
+}
+
+// The loop is straight-line code (every step issues the same loads, past-the-end steps re-read the last one, a missing
+// second 128-column half decodes the first one's tiles again), so the compiler's wait counts for the prefetched
+// registers stay exact and the waits land only where the data is two steps old.
+template <int F, int HALF>
+__device__ __forceinline__ void pf_decoder(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int d)
 {
     constexpr int TB = Fmt<F>::TB, NW = TB / 16;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63;
     const int h = lane >> 5, t = (lane >> 2) & 7, s = lane & 3;
-    const int dmat = wave >> 1, kt = 2 * (wave & 1) + h;
-    const size_t row_bytes = (size_t)tn * TB;
-    const uint8_t* p = mat_base + (size_t)kt * row_bytes + (size_t)(dcb * 8 + t) * TB + s * (TB / 4);
-    const int KT = K / 64;
-    uint32_t wa[NW], wb[NW];
-    if (dvalid) load_words(wa, p);
-    for (int it = 0; it < KT; it += 2)
+    const int kt = 2 * (d >> 2) + h, th = (d >> 1) & 1;
+    const int tcol = min(2 * jb.cb + th, jb.nb128 - 1);
+    const size_t row_bytes = (size_t)(jb.N / 16) * TB, step_bytes = 4 * row_bytes;
+    const uint8_t* p = mat_base + (size_t)kt * row_bytes + (size_t)(tcol * 8 + t) * TB + s * (TB / 4);
+    const int KT = jb.K / 64;
+    // this lane's A row (rows past the group's end read its last row; their products are not stored)
+    const int arow = 16 * d + (lane >> 2);
+    const uint16_t* rowp = asrc + (size_t)(jb.r0 + min(arow, jb.nr - 1)) * jb.K;
+    auto wp = [&](int step) { return p + (size_t)min(step, KT - 1) * step_bytes; };
+    auto ak = [&](int step) { return 64 * min(step, KT - 1); };
+    uint32_t w0[NW], w1[NW], w2[NW];
+    PfArow a0, a1, a2;
+    a_fetch(a0, rowp, ak(0));
+    a_fetch(a1, rowp, ak(1));
+    a_fetch(a2, rowp, ak(2));
+    load_words(w0, wp(0));
+    load_words(w1, wp(1));
+    load_words(w2, wp(2));
+    decode_half<F, HALF>(w0, pf_b0, kt, 128 * th);
+    a_store(a0, pf_a0, arow);
+    step_barrier();
+    // step i: stage step i + 1 (A rows, B fragments) into stage (i + 1) % 2, fetch step i + 3 into the sets step i used
+    for (int i = 0; i < KT; i += 3)
     {
-        if (dvalid && it + 1 < KT) load_words(wb, p + 4 * row_bytes);
-        if (dvalid) decode_to_lds<F>(wa, stages[0], dmat, kt);
-        __syncthreads();
-        mfma_step<NM>(stages[0], wv, it * 64, acc);
-        if (it + 1 < KT)
-        {
-            if (dvalid && it + 2 < KT) load_words(wa, p + 8 * row_bytes);
-            if (dvalid) decode_to_lds<F>(wb, stages[1], dmat, kt);
-            __syncthreads();
-            mfma_step<NM>(stages[1], wv, (it + 1) * 64, acc);
-        }
-        p += 8 * row_bytes;
+        a_fetch(a0, rowp, ak(i + 3));
+        load_words(w0, wp(i + 3));
+        decode_half<F, HALF>(w1, b_stage((i + 1) & 1), kt, 128 * th);
+        a_store(a1, a_stage((i + 1) & 1), arow);
+        step_barrier();
+        if (i + 1 >= KT) break;
+        a_fetch(a1, rowp, ak(i + 4));
+        load_words(w1, wp(i + 4));
+        decode_half<F, HALF>(w2, b_stage(i & 1), kt, 128 * th);
+        a_store(a2, a_stage(i & 1), arow);
+        step_barrier();
+        if (i + 2 >= KT) break;
+        a_fetch(a2, rowp, ak(i + 5));
+        load_words(w2, wp(i + 5));
+        decode_half<F, HALF>(w0, b_stage((i + 1) & 1), kt, 128 * th);
+        a_store(a0, a_stage((i + 1) & 1), arow);
+        step_barrier();
     }
 }
 
-template <int NM>
-__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm(GvArgs a)
+template <int F>
+__device__ __forceinline__ void pf_decoder_any(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc)
 {
-    __shared__ u32x4 stages[2][PF_STAGE_U4];
-    const int NBX = NM == 2 ? a.NB : (a.NBH + 1) / 2;
+    const int d = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) - 4);
+    if (d & 1) pf_decoder<F, 1>(jb, mat_base, asrc, d);
+    else pf_decoder<F, 0>(jb, mat_base, asrc, d);
+}
+
+template <bool DOWN>
+__global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
+{
+    const int nb128 = DOWN ? a.NBH : a.NB;     // 128-column blocks of the output
+    const int NB2 = (nb128 + 1) / 2;
     const int lid = xcd_block(blockIdx.x, gridDim.x);
-    const int g = lid / NBX, cb = lid % NBX;
-    if (g >= *a.ngroups) return;
-    const int e = a.groups[3 * g], r0 = a.groups[3 * g + 1], nr = a.groups[3 * g + 2];
-    const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-    const int K = NM == 2 ? a.H : a.I, N = NM == 2 ? a.I : a.H;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave & 1, wn = wave >> 1;
+    PfJob jb;
+    jb.nb128 = nb128;
+    if (DOWN) { jb.g = lid / NB2; jb.mat = 2; jb.cb = lid % NB2; }
+    else { jb.g = lid / (2 * NB2); jb.mat = (lid / NB2) & 1; jb.cb = lid % NB2; }
+    if (jb.g >= *a.ngroups) return;
+    jb.e = a.groups[3 * jb.g];
+    jb.r0 = a.groups[3 * jb.g + 1];
+    jb.nr = a.groups[3 * jb.g + 2];
+    jb.ex = jb.e == a.E ? a.shared : a.experts + jb.e;
+    jb.K = DOWN ? a.I : a.H;
+    jb.N = DOWN ? a.H : a.I;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int KT = jb.K / 64;
 
-    PfWave wv;
-    const int lk = (lane >> 5) * 8;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    const uint16_t* asrc = DOWN ? a.act_rows : a.xt + (size_t)jb.mat * a.R_max * a.H;
+    if (wave >= 4)
     {
-        const int row0 = 64 * wm + 32 * mb;
-        wv.mvalid[mb] = row0 < nr;
-        // rows past the group's end read its last row (their products are not stored)
-        const int row = r0 + min(row0 + (lane & 31), nr - 1);
-        if (NM == 2)
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(jb.ex->tr[jb.mat]);
+        switch (jb.ex->fmt[jb.mat])
         {
-            wv.arow[0][mb] = a.xt + (size_t)row * a.H + lk;
-            wv.arow[1][mb] = a.xt + ((size_t)a.R_max + row) * a.H + lk;
+            case BMX_TF_K2: pf_decoder_any<BMX_TF_K2>(jb, base, asrc); break;
+            case BMX_TF_K25: pf_decoder_any<BMX_TF_K25>(jb, base, asrc); break;
+            case BMX_TF_K3: pf_decoder_any<BMX_TF_K3>(jb, base, asrc); break;
+            default: pf_decoder_any<BMX_TF_K4>(jb, base, asrc); break;
         }
-        else
-        {
-            wv.arow[0][mb] = a.act_rows + (size_t)row * a.I + lk;
-            wv.arow[1][mb] = wv.arow[0][mb];
-        }
+        return;
     }
-    wv.bvalid = NM == 2 || 2 * cb + 1 < a.NBH;
 
-    // decode role
-    const int dmat = wave >> 1;
-    const int mi = NM == 2 ? dmat : 2;
-    const int dcb = NM == 2 ? cb : 2 * cb + dmat;
-    const bool dvalid = dcb < N / 128;
-    const uint8_t* base = reinterpret_cast<const uint8_t*>(ex.tr[mi]);
-
-    f32x16 acc[2][2][2];
+    // MFMA waves
+    f32x16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int k = 0; k < 2; ++k) acc[i][j][k] = f32x16{};
-    switch (ex.fmt[mi])
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    step_barrier();
+    for (int i = 0; i < KT; ++i)
     {
-        case BMX_TF_K2: pf_loop<BMX_TF_K2, NM>(stages, base, N / 16, dcb, dvalid, K, wv, acc); break;
-        case BMX_TF_K25: pf_loop<BMX_TF_K25, NM>(stages, base, N / 16, dcb, dvalid, K, wv, acc); break;
-        case BMX_TF_K3: pf_loop<BMX_TF_K3, NM>(stages, base, N / 16, dcb, dvalid, K, wv, acc); break;
-        default: pf_loop<BMX_TF_K4, NM>(stages, base, N / 16, dcb, dvalid, K, wv, acc); break;
+        pf_mfma_step(a_stage(i & 1), b_stage(i & 1), acc);
+        step_barrier();
     }
 
     // accumulator element v of lane L: row 8 (v / 4) + 4 (L / 32) + v % 4, column L % 32 of its 32 x 32 block
+    const int wm = wave & 1, wn = wave >> 1;
+    const int r0 = jb.r0, nr = jb.nr;
+    const int cbo = 2 * jb.cb + wn;                 // this wave's 128-column output block
+    if (cbo >= nb128) return;
 #pragma unroll
-    for (int mat = 0; mat < 2; ++mat)
+    for (int mb = 0; mb < 2; ++mb)
     {
-        if (mat == 1 && !wv.bvalid) continue;
+        if (64 * wm + 32 * mb >= nr) continue;
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int nb = 0; nb < 4; ++nb)
         {
-            if (!wv.mvalid[mb]) continue;
+            const int col = 32 * nb + (lane & 31);
 #pragma unroll
-            for (int nb2 = 0; nb2 < 2; ++nb2)
+            for (int v = 0; v < 16; ++v)
             {
-                const int col = 32 * (2 * wn + nb2) + (lane & 31);
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                {
-                    const int row = 64 * wm + 32 * mb + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                    if (row >= nr) continue;
-                    const size_t r = (size_t)(r0 + row);
-                    if (NM == 2) a.part_gu[(r * a.NB + cb) * 256 + mat * 128 + col] = acc[mat][mb][nb2][v];
-                    else a.part_dn[(r * a.NBH + 2 * cb + mat) * 128 + col] = acc[mat][mb][nb2][v];
-                }
+                const int row = 64 * wm + 32 * mb + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (row >= nr) continue;
+                const size_t r = (size_t)(r0 + row);
+                if (DOWN) a.part_dn[(r * a.NBH + cbo) * 128 + col] = acc[mb][nb][v];
+                else a.part_gu[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] = acc[mb][nb][v];
             }
         }
     }
@@ -250,7 +340,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 
 // ---- plan and launch -------------------------------------------------------------------------------------------------
 struct PrefillPlan {
-    int NB, NBH, NBX_dn, G_max, R_max;
+    int NB, NBH, G_max, R_max;
     size_t xt_bytes, part_gu_bytes, act_bytes, part_dn_bytes;
 };
 
@@ -259,7 +349,6 @@ static PrefillPlan prefill_plan(const MoeShape& m)
     PrefillPlan p;
     p.NB = m.I / 128;
     p.NBH = m.H / 128;
-    p.NBX_dn = (p.NBH + 1) / 2;
     p.G_max = groups_max(m.T, m.topk, m.E, m.shared, PF_M);
     p.R_max = m.T * m.topk + (m.shared ? m.T : 0);
     p.xt_bytes = (size_t)2 * p.R_max * m.H * 2;
@@ -310,10 +399,10 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, dim3((unsigned)((2 * p.R_max + 3) / 4)), dim3(256), 0, s, a);
     if (stages & (1 << BMX_STAGE_GATE_UP))
-        hipLaunchKernelGGL(k_pf_gemm<2>, dim3((unsigned)(p.G_max * p.NB)), dim3(PF_THREADS), 0, s, a);
+        hipLaunchKernelGGL(k_pf_gemm<false>, dim3((unsigned)(p.G_max * 2 * ((p.NB + 1) / 2))), dim3(PF_WAVES * 64), 0, s, a);
     if (stages & (1 << BMX_STAGE_ACT)) rc = launch_epilogue(a, BMX_STAGE_ACT, s);
     if (!rc && (stages & (1 << BMX_STAGE_DOWN)))
-        hipLaunchKernelGGL(k_pf_gemm<1>, dim3((unsigned)(p.G_max * p.NBX_dn)), dim3(PF_THREADS), 0, s, a);
+        hipLaunchKernelGGL(k_pf_gemm<true>, dim3((unsigned)(p.G_max * ((p.NBH + 1) / 2))), dim3(PF_WAVES * 64), 0, s, a);
     if (!rc && (stages & (1 << BMX_STAGE_COMBINE))) rc = launch_epilogue(a, BMX_STAGE_COMBINE, s);
     if (!rc && (stages & (1 << BMX_STAGE_DOWN_OUT))) rc = launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
     if (rc) return rc;
