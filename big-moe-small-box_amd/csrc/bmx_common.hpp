@@ -130,6 +130,82 @@ __device__ __forceinline__ void had128_wave(float& v0, float& v1)
     }
 }
 
+// ---- 128-point Hadamard over 16 lanes, 8 elements per lane -------------------------------------------------------------
+// Lane j of a 16-lane row holds elements 8 j .. 8 j + 7. Same transform and rounding as had128_wave: spans 1, 2, 4 inside
+// the lane, spans 8, 16, 32, 64 between lanes j ^ 1, ^ 2, ^ 4, ^ 8 of the row (DPP, no LDS traffic). A cross-lane stage is
+// fma(sgn, v, partner), sgn = -1 on the upper lane: sgn * v is exact, so the single rounding equals the reference's
+// a + b (lower) and a - b (upper).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float dpp_xor4(float v)
+{
+    // banks 0, 2 (lane bit 2 clear) read lane + 4 (row_shl:4), banks 1, 3 read lane - 4 (row_shr:4)
+    const int b = __builtin_bit_cast(int, v);
+    int p = __builtin_amdgcn_update_dpp(b, b, 0x104, 0xf, 0x5, false);
+    p = __builtin_amdgcn_update_dpp(p, b, 0x114, 0xf, 0xa, false);
+    return __builtin_bit_cast(float, p);
+}
+
+__device__ __forceinline__ void had128_x8(float (&v)[8])
+{
+#pragma unroll
+    for (int s = 1; s < 8; s <<= 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (!(e & s))
+            {
+                const float a = v[e], b = v[e + s];
+                v[e] = a + b;
+                v[e + s] = a - b;
+            }
+    const int lane = threadIdx.x & 63;
+    const float s1 = (lane & 1) ? -1.0f : 1.0f, s2 = (lane & 2) ? -1.0f : 1.0f;
+    const float s4 = (lane & 4) ? -1.0f : 1.0f, s8 = (lane & 8) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s1, v[e], dpp_f<0xB1>(v[e]));   // quad_perm [1,0,3,2]
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s2, v[e], dpp_f<0x4E>(v[e]));   // quad_perm [2,3,0,1]
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s4, v[e], dpp_xor4(v[e]));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s8, v[e], dpp_f<0x128>(v[e]));  // row_ror:8
+}
+
+// 16-byte global loads / stores and 8 fp16 <-> 16 bytes
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4* gptr_u32x4;
+__device__ __forceinline__ u32x4 ldg4(const void* p)
+{
+    return *reinterpret_cast<gptr_u32x4>(reinterpret_cast<uintptr_t>(p));
+}
+// 4 floats (read as a float vector: __builtin_bit_cast of a single element of an integer vector is miscompiled by this
+// compiler, every element reads element 0)
+typedef const __attribute__((address_space(1))) f32x4* gptr_f32x4;
+__device__ __forceinline__ f32x4 ldg4f(const float* p)
+{
+    return *reinterpret_cast<gptr_f32x4>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ void unpack8(const u32x4 w, float (&v)[8])
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        v[2 * i] = h2f(w[i] & 0xffffu);
+        v[2 * i + 1] = h2f(w[i] >> 16);
+    }
+}
+__device__ __forceinline__ u32x4 pack8_r(const float (&v)[8])
+{
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f2h_r(v[2 * i]) | ((uint32_t)f2h_r(v[2 * i + 1]) << 16);
+    return w;
+}
+
 // ---- fixed-sequence fp32 exp (the router's; the oracle evaluates the same sequence) ----------------------------------
 __device__ __forceinline__ float exp_fixed(float x)
 {

@@ -190,121 +190,197 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
     }
 }
 
-// ---- gate / up epilogue: one wave per (row, 128-column block) ----------------------------------------------------------
-// sum of the splits in split order -> fp16 gate / up (the stored GEMV results) -> H128 * R * svh -> activation -> * down
-// suh -> H128 * R -> fp16 down-input row (exllamav3 kernel A epilogue order, engine/kernels/x16/x16_dev.cu:245-283)
+// ---- epilogues: 16 lanes per (row or token, 128-column block), 8 consecutive columns per lane -----------------------------
+// UPW work units per wave: 4 (every lane busy) for large launches, 1 (lanes 16-63 idle; four times the waves, so a
+// decode-size launch spreads over more CUs) for small ones.
+template <int UPW>
+__device__ __forceinline__ int ep_unit()
+{
+    return (blockIdx.x * GV_WAVES + (threadIdx.x >> 6)) * UPW + ((threadIdx.x & 63) >> 4);
+}
+constexpr long EP_SMALL = 16384;              // launches with fewer units use UPW = 1
+
+// gate / up epilogue: sum of the splits in split order -> fp16 gate / up (the stored GEMV / GEMM results) -> H128 * R * svh
+// -> activation -> * down suh -> H128 * R -> fp16 down-input row (exllamav3 kernel A epilogue order,
+// engine/kernels/x16/x16_dev.cu:245-283)
+template <int UPW>
 __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
 {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int u = blockIdx.x * GV_WAVES + wave;
+    if (UPW == 1 && (threadIdx.x & 63) >= 16) return;
+    const int u = ep_unit<UPW>(), j = threadIdx.x & 15;
     const int r = u / a.NB, cb = u % a.NB;
     if (r >= a.offsets[a.NE]) return;
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-    const int col = cb * 128 + 2 * lane;
-    float g0 = 0.0f, g1 = 0.0f, u0 = 0.0f, u1 = 0.0f;
+    const int col = cb * 128 + 8 * j;
+    float g[8], v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { g[i] = 0.0f; v[i] = 0.0f; }
     for (int s = 0; s < a.KS_gu; ++s)
     {
-        const float* p = a.part_gu + (((size_t)s * a.R_max + r) * a.NB + cb) * 256 + 2 * lane;
-        const float2 gv = *reinterpret_cast<const float2*>(p);
-        const float2 uv = *reinterpret_cast<const float2*>(p + 128);
-        g0 = g0 + gv.x; g1 = g1 + gv.y;
-        u0 = u0 + uv.x; u1 = u1 + uv.y;
+        const float* p = a.part_gu + (((size_t)s * a.R_max + r) * a.NB + cb) * 256 + 8 * j;
+        const f32x4 g0 = ldg4f(p), g1 = ldg4f(p + 4), u0 = ldg4f(p + 128), u1 = ldg4f(p + 132);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            g[i] = g[i] + g0[i];
+            g[i + 4] = g[i + 4] + g1[i];
+            v[i] = v[i] + u0[i];
+            v[i + 4] = v[i + 4] + u1[i];
+        }
     }
-    g0 = h2f(f2h_r(g0)); g1 = h2f(f2h_r(g1));
-    u0 = h2f(f2h_r(u0)); u1 = h2f(f2h_r(u1));
-    had128_wave(g0, g1);
-    had128_wave(u0, u1);
-    const uint32_t svg = ldg(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col, 0);
-    const uint32_t svu = ldg(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col, 0);
-    const uint32_t sud = ldg(reinterpret_cast<const uint16_t*>(ex.suh[2]) + col, 0);
-    g0 = (g0 * R_SCALE) * h2f(svg & 0xffffu);
-    g1 = (g1 * R_SCALE) * h2f(svg >> 16);
-    u0 = (u0 * R_SCALE) * h2f(svu & 0xffffu);
-    u1 = (u1 * R_SCALE) * h2f(svu >> 16);
-    float a0 = act_gate(a.act, a.gated, g0, u0, a.limit) * h2f(sud & 0xffffu);
-    float a1 = act_gate(a.act, a.gated, g1, u1, a.limit) * h2f(sud >> 16);
-    had128_wave(a0, a1);
-    const uint32_t pk = (uint32_t)f2h_r(a0 * R_SCALE) | ((uint32_t)f2h_r(a1 * R_SCALE) << 16);
-    *reinterpret_cast<uint32_t*>(a.act_rows + (size_t)r * a.I + col) = pk;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(g[i])); v[i] = h2f(f2h_r(v[i])); }
+    had128_x8(g);
+    had128_x8(v);
+    float svg[8], svu[8], sud[8];
+    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col), svg);
+    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col), svu);
+    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.suh[2]) + col), sud);
+    float act[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+    {
+        const float gi = (g[i] * R_SCALE) * svg[i], ui = (v[i] * R_SCALE) * svu[i];
+        act[i] = act_gate(a.act, a.gated, gi, ui, a.limit) * sud[i];
+    }
+    had128_x8(act);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) act[i] = act[i] * R_SCALE;
+    *reinterpret_cast<u32x4*>(a.act_rows + (size_t)r * a.I + col) = pack8_r(act);
 }
 
-// down output of row r, block cb, lane's two columns: sum of the splits -> H128 * R * svh
-__device__ __forceinline__ void down_out(const GvArgs& a, int r, int cb, float& v0, float& v1)
+// down output of row r, block cb, lane's 8 columns: sum of the splits -> H128 * R * svh
+__device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float (&y)[8])
 {
-    const int lane = threadIdx.x & 63;
+    const int j = threadIdx.x & 15;
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-    v0 = 0.0f;
-    v1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = 0.0f;
     for (int s = 0; s < a.KS_dn; ++s)
     {
-        const float2 d = *reinterpret_cast<const float2*>(a.part_dn + (((size_t)s * a.R_max + r) * a.NBH + cb) * 128 + 2 * lane);
-        v0 = v0 + d.x;
-        v1 = v1 + d.y;
+        const float* p = a.part_dn + (((size_t)s * a.R_max + r) * a.NBH + cb) * 128 + 8 * j;
+        const f32x4 d0 = ldg4f(p), d1 = ldg4f(p + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            y[i] = y[i] + d0[i];
+            y[i + 4] = y[i + 4] + d1[i];
+        }
     }
-    had128_wave(v0, v1);
-    const uint32_t svd = ldg(reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 2 * lane, 0);
-    v0 = (v0 * R_SCALE) * h2f(svd & 0xffffu);
-    v1 = (v1 * R_SCALE) * h2f(svd >> 16);
+    had128_x8(y);
+    float sv[8];
+    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 8 * j), sv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = (y[i] * R_SCALE) * sv[i];
+}
+
+__device__ __forceinline__ void store8f(float* p, const float (&y)[8])
+{
+    *reinterpret_cast<float4*>(p) = make_float4(y[0], y[1], y[2], y[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(y[4], y[5], y[6], y[7]);
 }
 
 // ---- down epilogue over rows (expert outputs only) -----------------------------------------------------------------------
+template <int UPW>
 __global__ __launch_bounds__(GV_THREADS) void k_dn_epi(GvArgs a)
 {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int u = blockIdx.x * GV_WAVES + wave;
+    if (UPW == 1 && (threadIdx.x & 63) >= 16) return;
+    const int u = ep_unit<UPW>(), j = threadIdx.x & 15;
     const int r = u / a.NBH, cb = u % a.NBH;
     if (r >= a.offsets[a.NE]) return;
-    float v0, v1;
-    down_out(a, r, cb, v0, v1);
-    *reinterpret_cast<float2*>(a.y_rows + (size_t)r * a.H + cb * 128 + 2 * lane) = make_float2(v0, v1);
+    float y[8];
+    down_out8(a, r, cb, y);
+    store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
 }
 
-// ---- down epilogue + combine: one workgroup per (token, 128-column block) ---------------------------------------------
-// the slots' expert outputs are computed in parallel (wave w takes slots w, w + 4, ...), then wave 0 sums them:
+// ---- down epilogue + combine -----------------------------------------------------------------------------------------
 // out[t] = sum over k ascending of w[t, k] * y(inv[t, k]) (picks with inv < 0 or w = 0 skipped), then + y(shared row)
-// (engine/kernels/x16/x16_dev.cu:354-384)
-constexpr int CB_MAXK = 33;
+// (engine/kernels/x16/x16_dev.cu:354-384). Large launches: 16 lanes per (token, 128-column block), the slots in turn.
 __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
 {
-    __shared__ float ys[CB_MAXK][128];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = blockIdx.x / a.NBH, cb = blockIdx.x % a.NBH;
-    const int ns = a.topk + (a.has_shared ? 1 : 0);
-    for (int k = wave; k < ns; k += GV_WAVES)
-    {
-        int r;
-        if (k < a.topk)
-        {
-            r = a.inv[t * a.topk + k];
-            if (r < 0 || h2f(a.w[t * a.topk + k]) == 0.0f) continue;
-        }
-        else r = a.offsets[a.E] + t;
-        float v0, v1;
-        down_out(a, r, cb, v0, v1);
-        if (a.y_rows) *reinterpret_cast<float2*>(a.y_rows + (size_t)r * a.H + cb * 128 + 2 * lane) = make_float2(v0, v1);
-        ys[k][2 * lane] = v0;
-        ys[k][2 * lane + 1] = v1;
-    }
-    __syncthreads();
-    if (wave) return;
-    float o0 = 0.0f, o1 = 0.0f;
+    const int u = ep_unit<4>(), j = threadIdx.x & 15;
+    const int t = u / a.NBH, cb = u % a.NBH;
+    if (t >= a.T) return;
+    float o[8], y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = 0.0f;
     for (int k = 0; k < a.topk; ++k)
     {
         const int r = a.inv[t * a.topk + k];
         const float wk = h2f(a.w[t * a.topk + k]);
         if (r < 0 || wk == 0.0f) continue;
-        const float p0 = wk * ys[k][2 * lane], p1 = wk * ys[k][2 * lane + 1];
-        o0 = o0 + p0;
-        o1 = o1 + p1;
+        down_out8(a, r, cb, y);
+        if (a.y_rows) store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            const float p = wk * y[i];
+            o[i] = o[i] + p;
+        }
     }
     if (a.has_shared)
     {
-        o0 = o0 + ys[a.topk][2 * lane];
-        o1 = o1 + ys[a.topk][2 * lane + 1];
+        const int r = a.offsets[a.E] + t;
+        down_out8(a, r, cb, y);
+        if (a.y_rows) store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = o[i] + y[i];
     }
-    *reinterpret_cast<float2*>(a.out + (size_t)t * a.H + cb * 128 + 2 * lane) = make_float2(o0, o1);
+    store8f(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
+}
+
+// Small launches: one workgroup per (token, 128-column block); 16-lane group k computes slot k (the shared expert's row
+// is slot topk), then group 0 sums them in slot order: the same sums in the same order as k_dn_combine.
+constexpr int CB_MAXS = 33;
+__global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
+{
+    __shared__ float ys[CB_MAXS][128];
+    __shared__ int live[CB_MAXS];
+    const int t = blockIdx.x / a.NBH, cb = blockIdx.x % a.NBH;
+    const int k0 = threadIdx.x >> 4, j = threadIdx.x & 15;
+    const int ns = a.topk + (a.has_shared ? 1 : 0);
+    for (int k = k0; k < ns; k += GV_THREADS / 16)
+    {
+        int r;
+        if (k < a.topk)
+        {
+            r = a.inv[t * a.topk + k];
+            if (r < 0 || h2f(a.w[t * a.topk + k]) == 0.0f)
+            {
+                if (j == 0) live[k] = 0;
+                continue;
+            }
+        }
+        else r = a.offsets[a.E] + t;
+        float y[8];
+        down_out8(a, r, cb, y);
+        if (a.y_rows) store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ys[k][8 * j + i] = y[i];
+        if (j == 0) live[k] = 1;
+    }
+    __syncthreads();
+    if (k0) return;
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = 0.0f;
+    for (int k = 0; k < a.topk; ++k)
+    {
+        if (!live[k]) continue;
+        const float wk = h2f(a.w[t * a.topk + k]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            const float p = wk * ys[k][8 * j + i];
+            o[i] = o[i] + p;
+        }
+    }
+    if (a.has_shared)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = o[i] + ys[a.topk][8 * j + i];
+    store8f(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
 }
 
 // ---- standalone combine ----------------------------------------------------------------------------------------------
@@ -353,16 +429,22 @@ int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const
 
 int launch_epilogue(const GvArgs& a, int stage, hipStream_t s)
 {
+    // units -> workgroups of GV_WAVES waves with UPW units each
+    auto wgs = [](long units, int upw) { return dim3((unsigned)((units + GV_WAVES * upw - 1) / (GV_WAVES * upw))); };
+    const long gu = (long)a.R_max * a.NB, dn = (long)a.R_max * a.NBH, cmb = (long)a.T * a.NBH;
     switch (stage)
     {
         case BMX_STAGE_ACT:
-            hipLaunchKernelGGL(k_gu_epi, dim3((unsigned)((a.R_max * a.NB + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+            if (gu >= EP_SMALL) hipLaunchKernelGGL(k_gu_epi<4>, wgs(gu, 4), dim3(GV_THREADS), 0, s, a);
+            else hipLaunchKernelGGL(k_gu_epi<1>, wgs(gu, 1), dim3(GV_THREADS), 0, s, a);
             break;
         case BMX_STAGE_COMBINE:
-            hipLaunchKernelGGL(k_dn_combine, dim3((unsigned)(a.T * a.NBH)), dim3(GV_THREADS), 0, s, a);
+            if (cmb >= EP_SMALL) hipLaunchKernelGGL(k_dn_combine, wgs(cmb, 4), dim3(GV_THREADS), 0, s, a);
+            else hipLaunchKernelGGL(k_dn_combine_par, dim3((unsigned)cmb), dim3(GV_THREADS), 0, s, a);
             break;
         case BMX_STAGE_DOWN_OUT:
-            hipLaunchKernelGGL(k_dn_epi, dim3((unsigned)((a.R_max * a.NBH + GV_WAVES - 1) / GV_WAVES)), dim3(GV_THREADS), 0, s, a);
+            if (dn >= EP_SMALL) hipLaunchKernelGGL(k_dn_epi<4>, wgs(dn, 4), dim3(GV_THREADS), 0, s, a);
+            else hipLaunchKernelGGL(k_dn_epi<1>, wgs(dn, 1), dim3(GV_THREADS), 0, s, a);
             break;
         default: return set_error(BMX_ERR_ARG, "unknown epilogue stage %d", stage);
     }

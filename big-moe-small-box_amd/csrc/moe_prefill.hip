@@ -19,14 +19,6 @@ namespace bmx {
 
 constexpr int PF_M = 128;                    // rows per group
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef const __attribute__((address_space(1))) u32x4* gptr_u32x4;
-
-__device__ __forceinline__ u32x4 ldg4(const void* p)
-{
-    return *reinterpret_cast<gptr_u32x4>(reinterpret_cast<uintptr_t>(p));
-}
-
 // Workgroups are handed to the 8 XCDs round-robin (block b runs on XCD b % 8). Renumber so that consecutive logical
 // blocks share an XCD: the column blocks of one row group then read the group's A rows through the same L2.
 __device__ __forceinline__ int xcd_block(int bid, int nblk)
@@ -35,26 +27,28 @@ __device__ __forceinline__ int xcd_block(int bid, int nblk)
     return (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + i;
 }
 
-// ---- rotated inputs: one wave per (row, matrix) ----------------------------------------------------------------------
+// ---- rotated inputs: 16 lanes per (row, matrix), 8 consecutive inputs per lane -----------------------------------------
 __global__ __launch_bounds__(256) void k_pf_prep(GvArgs a)
 {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int u = blockIdx.x * 4 + wave;
+    const int u = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
     const int r = u >> 1, mat = u & 1;
     if (r >= a.offsets[a.NE]) return;
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-    const uint16_t* xr = a.x + (size_t)a.row_token[r] * a.H;
-    const uint16_t* su = reinterpret_cast<const uint16_t*>(ex.suh[mat]);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(a.xt + ((size_t)mat * a.R_max + r) * a.H);
+    const uint16_t* xr = a.x + (size_t)a.row_token[r] * a.H + 8 * j;
+    const uint16_t* su = reinterpret_cast<const uint16_t*>(ex.suh[mat]) + 8 * j;
+    uint16_t* dst = a.xt + ((size_t)mat * a.R_max + r) * a.H + 8 * j;
     for (int b = 0; b < a.H / 128; ++b)
     {
-        const int k = b * 128 + 2 * lane;
-        const uint32_t xv = ldg(xr + k, 0);
-        const uint32_t sv = ldg(su + k, 0);
-        float v0 = h2f(xv & 0xffffu) * h2f(sv & 0xffffu), v1 = h2f(xv >> 16) * h2f(sv >> 16);
-        had128_wave(v0, v1);
-        dst[b * 64 + lane] = (uint32_t)f2h_r(v0 * R_SCALE) | ((uint32_t)f2h_r(v1 * R_SCALE) << 16);
+        float v[8], s[8];
+        unpack8(ldg4(xr + 128 * b), v);
+        unpack8(ldg4(su + 128 * b), s);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] * s[i];
+        had128_x8(v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] * R_SCALE;
+        *reinterpret_cast<u32x4*>(dst + 128 * b) = pack8_r(v);
     }
 }
 
@@ -397,7 +391,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
-        hipLaunchKernelGGL(k_pf_prep, dim3((unsigned)((2 * p.R_max + 3) / 4)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_pf_prep, dim3((unsigned)((2 * p.R_max + 15) / 16)), dim3(256), 0, s, a);
     if (stages & (1 << BMX_STAGE_GATE_UP))
         hipLaunchKernelGGL(k_pf_gemm<false>, dim3((unsigned)(p.G_max * 2 * ((p.NB + 1) / 2))), dim3(PF_WAVES * 64), 0, s, a);
     if (stages & (1 << BMX_STAGE_ACT)) rc = launch_epilogue(a, BMX_STAGE_ACT, s);
