@@ -4,8 +4,9 @@ from ._lib import (ACT_GELU, ACT_RELU2, ACT_SILU, ACT_SILU_OAI, PATH_AUTO, PATH_
                    SCORE_SOFTMAX, TF_K2, TF_K3, TF_K4, TF_K25, TILE_BYTES, BmxError, lib)
 from .experts import ExpertTable
 from .layer import MoELayer
+from .slots import ExpertSlots
 from . import ops
 
-__all__ = ["ExpertTable", "MoELayer", "ops", "lib", "BmxError", "TF_K2", "TF_K25", "TF_K3", "TF_K4", "TILE_BYTES",
+__all__ = ["ExpertTable", "ExpertSlots", "MoELayer", "ops", "lib", "BmxError", "TF_K2", "TF_K25", "TF_K3", "TF_K4", "TILE_BYTES",
            "SCORE_SIGMOID", "SCORE_SOFTMAX", "ACT_SILU", "ACT_GELU", "ACT_RELU2", "ACT_SILU_OAI", "PATH_AUTO",
            "PATH_DECODE", "PATH_PREFILL", "_lib"]

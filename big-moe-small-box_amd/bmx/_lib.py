@@ -12,6 +12,7 @@ SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
 STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT, STAGE_PREP = 0, 1, 2, 3, 4, 5
+STAGE_GATE_UP_RESIDENT, STAGE_GATE_UP_STAGED = 6, 7
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -27,7 +28,15 @@ class Expert(ctypes.Structure):
 class MoeDesc(ctypes.Structure):
     _fields_ = [("H", ctypes.c_int32), ("I", ctypes.c_int32), ("E", ctypes.c_int32), ("topk", ctypes.c_int32),
                 ("first", ctypes.c_int64), ("act", ctypes.c_int32), ("gated", ctypes.c_int32),
-                ("act_limit", ctypes.c_float), ("experts", _P), ("shared", _P)]
+                ("act_limit", ctypes.c_float), ("experts", _P), ("shared", _P), ("fresh", _P)]
+
+
+class SlotTable(ctypes.Structure):
+    _fields_ = [("L", ctypes.c_int32), ("E", ctypes.c_int32), ("S", ctypes.c_int32), ("maxj", ctypes.c_int32),
+                ("H", ctypes.c_int32), ("I", ctypes.c_int32),
+                ("rec", ctypes.c_int64), ("off_u", ctypes.c_int64), ("off_d", ctypes.c_int64)] + \
+               [(n, _P) for n in ("slotof", "owner", "refb", "pin", "ctl", "jobs", "fresh", "stats", "home", "slot_base",
+                                  "tables")]
 
 
 class RouterDesc(ctypes.Structure):
@@ -60,6 +69,10 @@ SIGNATURES = {
     "bmx_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "bmx_moe_layer_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_layer": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
+    "bmx_slot_step": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, _I64, _I, _P]),
+    "bmx_slot_copy": (_I, [ctypes.POINTER(SlotTable), _I, _P]),
+    "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
+    "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }
 
 _lib = None

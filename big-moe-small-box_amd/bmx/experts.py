@@ -21,20 +21,35 @@ def matrix_bytes(k, n, fmt):
     return (k // 16) * (n // 16) * L.TILE_BYTES[fmt]
 
 
+def device_address(t):
+    """Address at which the GPU reads tensor t: its data pointer for device memory, the mapped address
+    (hipHostGetDevicePointer) for pinned host memory."""
+    if t.is_cuda:
+        return t.data_ptr()
+    if not t.is_pinned():
+        raise ValueError("expert homes in host memory must be pinned (allocated with pin_memory=True)")
+    out = ctypes.c_uint64(0)
+    L.check(L.lib().bmx_host_device_ptr(ctypes.c_void_p(t.data_ptr()), ctypes.byref(out)), "bmx_host_device_ptr")
+    return int(out.value)
+
+
 class ExpertTable:
     """E routed experts (+ optional shared expert at index E) of one layer.
 
-    arena uint8 [E + shared, rec]; suh / svh: lists of three fp16 tensors [E + shared, k] / [E + shared, n];
-    fmt int [E + shared, 3]. Build with ExpertTable.random(...) or from existing tensors."""
+    arena uint8 [E + shared, rec] (device memory, or pinned host memory the kernels read over PCIe: the home of experts
+    an expert-slot table stages into VRAM); suh / svh: lists of three fp16 device tensors [E + shared, k] /
+    [E + shared, n]; fmt int [E + shared, 3]. Build with ExpertTable.random(...) or from existing tensors."""
 
     def __init__(self, H, I, arena, fmt, suh, svh, off_u, off_d, n_routed, has_shared):
         self.H, self.I = H, I
         self.arena, self.fmt, self.suh, self.svh = arena, fmt, suh, svh
         self.off_u, self.off_d, self.rec = off_u, off_d, arena.shape[1]
         self.E, self.has_shared = n_routed, has_shared
-        self.device = arena.device
+        self.device = suh[0].device
         self._table = None
-        self.addr = [self._addr(e) for e in range(n_routed + (1 if has_shared else 0))]   # home trellis addresses
+        base = device_address(arena)
+        self.addr = [(base + e * self.rec, base + e * self.rec + off_u, base + e * self.rec + off_d)
+                     for e in range(n_routed + (1 if has_shared else 0))]   # home trellis addresses
 
     @staticmethod
     def geometry(H, I, fmts):
@@ -47,10 +62,11 @@ class ExpertTable:
         return off_u, off_d, off_d + _al(sd)
 
     @classmethod
-    def random(cls, H, I, E, fmts, shared=False, seed=0, device="cuda", svh_norm=True):
+    def random(cls, H, I, E, fmts, shared=False, seed=0, device="cuda", svh_norm=True, home="device"):
         """Random trellis bytes (every bit string is a valid code), suh ~ U(0.5, 1.5), svh ~ U(0.5, 1.5) / sqrt(k) when
         svh_norm (each linear then keeps the norm of its input, so layer outputs are O(1)). fmts: one (fg, fu, fd) for
-        every expert (E + shared entries) or a single tuple for all."""
+        every expert (E + shared entries) or a single tuple for all. home = "host": the trellis arena in pinned host
+        memory (drawn on the device and copied, the same bytes as a device arena of the same seed)."""
         n = E + (1 if shared else 0)
         if isinstance(fmts, tuple):
             fmts = [fmts] * n
@@ -60,6 +76,10 @@ class ExpertTable:
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
         arena = torch.randint(0, 256, (n, rec), dtype=torch.uint8, device=dev, generator=g)
+        if home == "host":
+            pinned = torch.empty((n, rec), dtype=torch.uint8, pin_memory=True)
+            pinned.copy_(arena)
+            arena = pinned
         dims = ((H, I), (H, I), (I, H))
         suh, svh = [], []
         for k, nn in dims:
@@ -68,10 +88,6 @@ class ExpertTable:
             svh.append((s / (k ** 0.5) if svh_norm else s).half())
         fmt = torch.tensor(fmts, dtype=torch.int32)
         return cls(H, I, arena, fmt, suh, svh, off_u, off_d, E, shared)
-
-    def _addr(self, e):
-        base = self.arena[e].data_ptr()
-        return (base, base + self.off_u, base + self.off_d)
 
     def mat_bytes(self, e, m):
         k, n = ((self.H, self.I), (self.H, self.I), (self.I, self.H))[m]
@@ -101,11 +117,12 @@ class ExpertTable:
             self._table = raw.to(self.device)
         return self._table
 
-    def desc(self, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0):
+    def desc(self, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0, fresh=None):
         t = self.table()
         es = ctypes.sizeof(L.Expert)
         shared = t.data_ptr() + self.E * es if self.has_shared else None
-        return L.MoeDesc(self.H, self.I, self.E, topk, first, act, int(gated), act_limit, t.data_ptr(), shared)
+        return L.MoeDesc(self.H, self.I, self.E, topk, first, act, int(gated), act_limit, t.data_ptr(), shared,
+                         fresh.data_ptr() if fresh is not None else None)
 
     def host_expert(self, e):
         """numpy copies of one expert (trellis per matrix, scales, formats) for the oracle."""

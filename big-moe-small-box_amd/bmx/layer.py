@@ -9,6 +9,8 @@ Names and argument meaning follow the reference:
   combine(fhs) -> fhs                                                           engine/nv2.py:489-493 (Nv2.combine)
 Every call enqueues on torch's current stream; nothing synchronises the host.
 """
+import ctypes
+
 import torch
 
 from . import _lib as L
@@ -29,6 +31,7 @@ class MoELayer:
         self.router_weight = router_weight        # fp16 [H, E] or None (logits passed in params["logits"])
         self.slots, self.li = slots, li           # optional ExpertSlots (expert-slot table) and this layer's index
         self.desc = table.desc(topk, first, act, gated, act_limit)
+        self.slot_desc = slots.desc(li, topk, first, act, gated, act_limit) if slots is not None else None
         self.router = L.RouterDesc(score, int(renorm), n_group, topk_group, scale, 0,
                                    bias.data_ptr() if bias is not None else None)
         self._ws = None
@@ -51,7 +54,7 @@ class MoELayer:
     # ---- engine hook: residency before the experts run ----
     def layer(self, li, sel, w, z, bsz):
         if self.slots is not None:
-            self.slots.step(li, sel)
+            self.slots.step(li, sel, self.routing_first)
         return sel, w, False
 
     # ---- experts + combine ----
@@ -65,12 +68,40 @@ class MoELayer:
         rw = rw.view(x.shape[0], -1)
         if rw.dtype != torch.float16 or not rw.is_contiguous():
             rw = rw.half().contiguous()
-        desc = self.slots.desc(self.li) if self.slots is not None else self.desc
-        need = L.lib().bmx_moe_workspace(desc, x.shape[0], path)
+        if self.slots is not None:
+            self.out_bszn = self._run_slots(x, sel, rw, path)
+            return self.out_bszn
+        need = L.lib().bmx_moe_workspace(self.desc, x.shape[0], path)
         if self._ws is None or self._ws.numel() < need:
             self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
-        self.out_bszn = ops.moe_forward(desc, x, sel, rw, path, self._ws)
+        self.out_bszn = ops.moe_forward(self.desc, x, sel, rw, path, self._ws)
         return self.out_bszn
+
+    def _run_slots(self, x, sel, rw, path):
+        """Expert products with the slot table: gate / up of the experts resident before this layer's step, then (after
+        the side stream's copies of the experts it admitted) the admitted ones, then the rest of the layer."""
+        T, lib = x.shape[0], L.lib()
+        desc = self.slot_desc
+        routes = ops.dispatch(sel, self.num_local_experts, self.routing_first, self.table.has_shared,
+                              lib.bmx_rows_per_group(T, self.num_experts_per_tok, path))
+        need = lib.bmx_experts_workspace(ctypes.byref(desc), T, path)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        out = torch.empty((T, self.hidden_size), dtype=torch.float32, device=x.device)
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+
+        def stage(st):
+            L.check(lib.bmx_moe_stage(ctypes.byref(desc), st, P(x), T, ctypes.byref(routes.struct), None, None, P(rw),
+                                      P(out), P(self._ws), self._ws.numel(), path, s), "bmx_moe_stage")
+
+        stage(L.STAGE_PREP)
+        stage(L.STAGE_GATE_UP_RESIDENT)
+        self.slots.wait_copies(self.li)
+        for st in (L.STAGE_GATE_UP_STAGED, L.STAGE_ACT, L.STAGE_DOWN, L.STAGE_COMBINE):
+            stage(st)
+        self._routes = routes
+        return out
 
     def cpu_split_combine(self, fhs, cpu_partial=None, cpu_pending=False, shape=None):
         if cpu_pending and cpu_partial is not None:

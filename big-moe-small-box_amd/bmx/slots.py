@@ -1,0 +1,94 @@
+"""ExpertSlots: the VRAM expert-slot table over a stack of MoE layers (the reference's Pool: slot geometry, slotof /
+owner / reference bits / pins, per-layer pointer tables and homes; engine/tiers.py:275-373, step kernel ec_step_k at
+engine/ec.py:16-76, copies ec_copy_k engine/ec.py:78-105 and stage_layer engine/kernels/nv2/nv2_host.cpp:1558-1593).
+
+Every layer keeps its experts' trellis at home (an ExpertTable, typically with its arena in pinned host memory); S
+uniform slots of the layers' record size live in VRAM. step(li, sel) runs the CLOCK step of layer li on the current
+stream (hits pinned, misses admitted, table pointers rewritten) and the copies of its admissions on a side stream;
+the layer's expert products wait for those copies only in their staged part (MoELayer.run_bszN). No host
+synchronisation anywhere."""
+import ctypes
+
+import torch
+
+from . import _lib as L
+
+
+class ExpertSlots:
+    def __init__(self, layers, S, maxj=32, disabled=()):
+        """layers: one ExpertTable per layer (same H, I, E and record geometry); S slots; maxj admissions per step;
+        disabled: slot indices never used."""
+        t0 = layers[0]
+        for t in layers:
+            if (t.H, t.I, t.E, t.rec, t.off_u, t.off_d) != (t0.H, t0.I, t0.E, t0.rec, t0.off_u, t0.off_d):
+                raise ValueError("ExpertSlots: layers must share H, I, E and the record geometry")
+        self.layers, self.L, self.E, self.S, self.maxj = layers, len(layers), t0.E, S, maxj
+        dev = t0.device
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.arena = torch.empty((max(S, 1), t0.rec), dtype=torch.uint8, device=dev)
+        self.slotof = torch.full((self.L * self.E,), -1, **i32)
+        self.owner = torch.full((max(S, 1),), -1, **i32)
+        self.refb = torch.zeros(max(S, 1), **i32)
+        self.pin = torch.zeros(max(S, 1), **i32)
+        for s in disabled:
+            self.pin[s] = -1
+        self.ctl = torch.zeros(4, **i32)
+        self.jobs = torch.zeros(2 * max(maxj, 1), **i32)
+        self.fresh = torch.zeros(self.E, **i32)
+        self.stats_t = torch.zeros(5, dtype=torch.int64, device=dev)
+        home = [a for t in layers for e in range(t.E) for a in t.addr[e]]
+        self.home = torch.tensor(home, dtype=torch.int64, device=dev)       # uint64 addresses, int64 storage
+        base = self.arena.data_ptr()
+        self.slot_base = torch.tensor([base + s * t0.rec for s in range(max(S, 1))], dtype=torch.int64, device=dev)
+        self.tables = torch.tensor([t.table().data_ptr() for t in layers], dtype=torch.int64, device=dev)
+        P = lambda x: x.data_ptr()
+        self.struct = L.SlotTable(self.L, self.E, S, maxj, t0.H, t0.I, t0.rec, t0.off_u, t0.off_d,
+                                  P(self.slotof), P(self.owner), P(self.refb), P(self.pin), P(self.ctl), P(self.jobs),
+                                  P(self.fresh), P(self.stats_t), P(self.home), P(self.slot_base), P(self.tables))
+        self.side = torch.cuda.Stream(device=dev)
+        self.copied = [None] * self.L        # event: copies of the layer's last step done
+
+    def step(self, li, sel, first=0, admit=True):
+        """CLOCK step of layer li over the picks sel (int64 device tensor) on the current stream, then the copies of
+        its admissions on the side stream."""
+        if sel.dtype != torch.int64 or not sel.is_contiguous():
+            sel = sel.long().contiguous()
+        cur = torch.cuda.current_stream()
+        L.check(L.lib().bmx_slot_step(ctypes.byref(self.struct), li, ctypes.c_void_p(sel.data_ptr()), sel.numel(),
+                                      int(first), int(admit), ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_step")
+        stepped = torch.cuda.Event()
+        stepped.record(cur)
+        self.side.wait_event(stepped)
+        L.check(L.lib().bmx_slot_copy(ctypes.byref(self.struct), li, ctypes.c_void_p(self.side.cuda_stream)),
+                "bmx_slot_copy")
+        ev = torch.cuda.Event()
+        ev.record(self.side)
+        self.copied[li] = ev
+        return ev
+
+    def wait_copies(self, li, stream=None):
+        """Order `stream` (default: current) after the copies of layer li's last step."""
+        if self.copied[li] is not None:
+            (stream or torch.cuda.current_stream()).wait_event(self.copied[li])
+
+    def desc(self, li, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0):
+        return self.layers[li].desc(topk, first, act, gated, act_limit, fresh=self.fresh)
+
+    def warm(self, li, experts, first=0):
+        """Admit the given local experts of layer li (a step over them) and wait for their copies."""
+        sel = torch.as_tensor(list(experts), dtype=torch.int64, device=self.arena.device) + first
+        self.step(li, sel, first)
+        self.wait_copies(li)
+
+    def stage_async(self, src, dst, nbytes, stream=None):
+        """Host-planned staging: copies src[i] -> dst[i] of nbytes[i] bytes (addresses) with hipMemcpyAsync."""
+        n = len(src)
+        a = (ctypes.c_void_p * n)(*src)
+        b = (ctypes.c_void_p * n)(*dst)
+        c = (ctypes.c_size_t * n)(*nbytes)
+        s = stream or torch.cuda.current_stream()
+        L.check(L.lib().bmx_slot_stage_async(a, b, c, n, ctypes.c_void_p(s.cuda_stream)), "bmx_slot_stage_async")
+
+    def stats(self):
+        """(hits, misses, admissions, steps without a victim, evictions) (synchronises)."""
+        return tuple(int(v) for v in self.stats_t.cpu())

@@ -43,6 +43,7 @@ struct MoeShape {
     int64_t first;
     const bmx_expert* experts;
     const bmx_expert* shared_ex;
+    const int32_t* fresh;
 };
 struct DecodePlan {
     int KS_gu, KS_dn, NB, NBH, G_max, R_max;
@@ -57,6 +58,10 @@ int decode_rows_per_group(int T);
 int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const int32_t* offsets, int T, int topk,
                    int H, int E, int has_shared, float* out, hipStream_t s);
 int launch_zero_i32(int32_t* p, int n, hipStream_t s);
+
+// slots.hip
+int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s);
+int launch_slot_copy(const bmx_slot_table* t, int li, hipStream_t s);
 
 // moe_prefill.hip (same ws / stage conventions; ws layout [xt][part_gu][act rows][part_dn])
 int prefill_rows_per_group();

@@ -44,7 +44,7 @@ static MoeShape shape_of(const bmx_moe_desc* d, int T)
     MoeShape m;
     m.H = d->H; m.I = d->I; m.E = d->E; m.topk = d->topk; m.T = T; m.shared = d->shared ? 1 : 0;
     m.act = d->act; m.gated = d->gated; m.limit = d->act_limit; m.first = d->first;
-    m.experts = d->experts; m.shared_ex = d->shared;
+    m.experts = d->experts; m.shared_ex = d->shared; m.fresh = d->fresh;
     return m;
 }
 
@@ -204,10 +204,14 @@ int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T
     if (rc) return rc;
     const int p = resolve_path(path, T, desc->topk);
     if (p < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_stage: bad path or T");
-    if (stage < BMX_STAGE_GATE_UP || stage > BMX_STAGE_PREP) return set_error(BMX_ERR_ARG, "bmx_moe_stage: unknown stage %d", stage);
+    if (stage < BMX_STAGE_GATE_UP || stage > BMX_STAGE_GATE_UP_STAGED)
+        return set_error(BMX_ERR_ARG, "bmx_moe_stage: unknown stage %d", stage);
+    if ((stage == BMX_STAGE_GATE_UP_RESIDENT || stage == BMX_STAGE_GATE_UP_STAGED) && !desc->fresh)
+        return set_error(BMX_ERR_ARG, "bmx_moe_stage: split gate / up stages need desc->fresh");
     if (T == 0) return BMX_OK;
     if (!routes || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_stage: null pointer");
-    if ((stage == BMX_STAGE_GATE_UP || stage == BMX_STAGE_PREP) && !x_fp16)
+    if ((stage == BMX_STAGE_GATE_UP || stage == BMX_STAGE_PREP || stage == BMX_STAGE_GATE_UP_RESIDENT ||
+         stage == BMX_STAGE_GATE_UP_STAGED) && !x_fp16)
         return set_error(BMX_ERR_ARG, "bmx_moe_stage: gate/up needs x");
     if (stage == BMX_STAGE_COMBINE && (!out || !w_fp16)) return set_error(BMX_ERR_ARG, "bmx_moe_stage: combine needs out and w");
     if (stage == BMX_STAGE_DOWN_OUT && !y_rows) return set_error(BMX_ERR_ARG, "bmx_moe_stage: down_out needs y_rows");

@@ -134,6 +134,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
     const int cb = bid % NB, g = bid / NB;
     if (g >= *a.ngroups) return;
     const int e = a.groups[3 * g], r0 = a.groups[3 * g + 1], nr = a.groups[3 * g + 2];
+    if (NM == 2 && group_skipped(a, e)) return;
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const int K = NM == 2 ? a.H : a.I, N = NM == 2 ? a.I : a.H;
     const int KR = K / KS, k0 = ks * KR, XW = KR / 2;
@@ -516,8 +517,14 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
 {
     const size_t lds_gu = (size_t)2 * MR * (a.H / p.KS_gu) / 2 * 4 + (size_t)2 * GV_WAVES * MR * 128 * 4;
     const size_t lds_dn = (size_t)MR * (a.I / p.KS_dn) / 2 * 4 + (size_t)GV_WAVES * MR * 128 * 4;
-    if (stages & (1 << BMX_STAGE_GATE_UP))
-        hipLaunchKernelGGL((k_gemv_part<MR, 2>), dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds_gu, s, a);
+    for (int f = 0; f < 3; ++f)
+    {
+        const int st = f == 0 ? BMX_STAGE_GATE_UP : f == 1 ? BMX_STAGE_GATE_UP_RESIDENT : BMX_STAGE_GATE_UP_STAGED;
+        if (!(stages & (1 << st))) continue;
+        GvArgs b = a;
+        b.filter = f;
+        hipLaunchKernelGGL((k_gemv_part<MR, 2>), dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds_gu, s, b);
+    }
     if (stages & (1 << BMX_STAGE_ACT)) launch_epilogue(a, BMX_STAGE_ACT, s);
     if (stages & (1 << BMX_STAGE_DOWN))
         hipLaunchKernelGGL((k_gemv_part<MR, 1>), dim3((unsigned)(p.G_max * p.NBH * p.KS_dn)), dim3(GV_THREADS), lds_dn, s, a);
@@ -551,6 +558,8 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
     a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
     a.xt = nullptr;
+    a.fresh = m.fresh;
+    a.filter = 0;
     switch (rows_per_group_of(m.T))
     {
         case 1: launch_mr<1>(a, p, stages, s); break;

@@ -29,7 +29,17 @@ struct GvArgs {
     const int32_t* offsets;
     int T, topk, has_shared;
     uint16_t* xt;              // prefill: rotated gate / up input rows [2][R_max][H]
+    const int32_t* fresh;      // [E] admitted-this-step flags of the expert-slot table, or null
+    int filter;                // gate / up groups: 0 all, 1 experts not fresh, 2 fresh experts only
 };
+
+// group filter of the split gate / up stages (the shared expert, index E, is never fresh)
+__device__ __forceinline__ bool group_skipped(const GvArgs& a, int e)
+{
+    if (!a.filter) return false;
+    const bool fr = e < a.E && a.fresh && a.fresh[e];
+    return fr != (a.filter == 2);
+}
 
 // S(i) + 16 for the 64 stream positions of a 64-weight strip (a strip starts on a 64-position boundary, where the ring
 // position is a whole number of 32-bit words for every format)

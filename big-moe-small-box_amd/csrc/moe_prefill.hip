@@ -271,6 +271,7 @@ __global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
     else { jb.g = lid / (2 * NB2); jb.mat = (lid / NB2) & 1; jb.cb = lid % NB2; }
     if (jb.g >= *a.ngroups) return;
     jb.e = a.groups[3 * jb.g];
+    if (!DOWN && group_skipped(a, jb.e)) return;
     jb.r0 = a.groups[3 * jb.g + 1];
     jb.nr = a.groups[3 * jb.g + 2];
     jb.ex = jb.e == a.E ? a.shared : a.experts + jb.e;
@@ -389,11 +390,19 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.NE = m.E + (m.shared ? 1 : 0);
     a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
+    a.fresh = m.fresh;
+    a.filter = 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, dim3((unsigned)((2 * p.R_max + 15) / 16)), dim3(256), 0, s, a);
-    if (stages & (1 << BMX_STAGE_GATE_UP))
-        hipLaunchKernelGGL(k_pf_gemm<false>, dim3((unsigned)(p.G_max * 2 * ((p.NB + 1) / 2))), dim3(PF_WAVES * 64), 0, s, a);
+    for (int f = 0; f < 3; ++f)
+    {
+        const int st = f == 0 ? BMX_STAGE_GATE_UP : f == 1 ? BMX_STAGE_GATE_UP_RESIDENT : BMX_STAGE_GATE_UP_STAGED;
+        if (!(stages & (1 << st))) continue;
+        GvArgs b = a;
+        b.filter = f;
+        hipLaunchKernelGGL(k_pf_gemm<false>, dim3((unsigned)(p.G_max * 2 * ((p.NB + 1) / 2))), dim3(PF_WAVES * 64), 0, s, b);
+    }
     if (stages & (1 << BMX_STAGE_ACT)) rc = launch_epilogue(a, BMX_STAGE_ACT, s);
     if (!rc && (stages & (1 << BMX_STAGE_DOWN)))
         hipLaunchKernelGGL(k_pf_gemm<true>, dim3((unsigned)(p.G_max * ((p.NBH + 1) / 2))), dim3(PF_WAVES * 64), 0, s, a);

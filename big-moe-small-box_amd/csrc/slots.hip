@@ -1,0 +1,282 @@
+// Expert-slot table: the CLOCK step of one layer (one workgroup) and the home -> slot copies of its admissions.
+//
+// Semantics follow the reference's ec_step_k (engine/ec.py:16-76) with one contract fixed: misses are admitted in
+// ascending expert order (the reference collects them with atomics, in no fixed order).
+#include "bmx_common.hpp"
+#include "bmx_internal.hpp"
+
+namespace bmx {
+
+constexpr int SL_THREADS = 512;     // one thread per expert (E <= 512)
+constexpr int SL_MAXS = 8192;       // slots the step keeps in LDS (pin and reference bits)
+
+struct SlotArgs {
+    bmx_slot_table t;
+    const int64_t* sel;
+    int64_t first;
+    int li, n, admit;
+};
+
+__device__ __forceinline__ int tile_bytes_dev(int fmt)
+{
+    return fmt == BMX_TF_K2 ? 64 : fmt == BMX_TF_K25 ? 80 : fmt == BMX_TF_K3 ? 96 : 128;
+}
+
+__global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
+{
+    __shared__ int32_t pin[SL_MAXS];
+    __shared__ int32_t refb[SL_MAXS];
+    __shared__ uint32_t mark[16];
+    __shared__ int32_t miss[512];
+    __shared__ int wave_miss[SL_THREADS / 64], wave_hit[SL_THREADS / 64];
+    const bmx_slot_table& t = a.t;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int S = t.S, E = t.E;
+    const int epoch = t.ctl[1] + 1;
+    for (int s = tid; s < S; s += SL_THREADS)
+    {
+        pin[s] = t.pin[s];
+        refb[s] = t.refb[s];
+    }
+    if (tid < 16) mark[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < a.n; i += SL_THREADS)
+    {
+        const int64_t e = a.sel[i] - a.first;
+        if (e >= 0 && e < E) atomicOr(&mark[e >> 5], 1u << (e & 31));
+    }
+    __syncthreads();
+
+    // hits: reference bit, pinned for this step; misses: compacted in ascending expert order
+    int32_t* slotof = t.slotof + (size_t)a.li * E;
+    const int e = tid;
+    bool is_miss = false, is_hit = false;
+    if (e < E)
+    {
+        t.fresh[e] = 0;
+        if ((mark[e >> 5] >> (e & 31)) & 1u)
+        {
+            const int s = slotof[e];
+            if (s >= 0)
+            {
+                refb[s] = 1;
+                pin[s] = epoch;
+                is_hit = true;
+            }
+            else is_miss = true;
+        }
+    }
+    const uint64_t bm = __ballot(is_miss), bh = __ballot(is_hit);
+    if (lane == 0)
+    {
+        wave_miss[wave] = __popcll(bm);
+        wave_hit[wave] = __popcll(bh);
+    }
+    __syncthreads();
+    int base = 0, nmiss = 0, nhit = 0;
+    for (int w = 0; w < SL_THREADS / 64; ++w)
+    {
+        if (w < wave) base += wave_miss[w];
+        nmiss += wave_miss[w];
+        nhit += wave_hit[w];
+    }
+    if (is_miss) miss[base + __popcll(bm & ((1ull << lane) - 1ull))] = e;
+    __syncthreads();
+
+    // admissions: one wave sweeps the CLOCK hand 64 slots at a time. Within a chunk every slot is probed once, so taking
+    // the first candidate and clearing the reference bits of the unpinned slots before it is the sequential sweep.
+    if (wave == 0)
+    {
+        int hand = t.ctl[0], nj = 0, novictim = 0, evicted = 0;
+        const int chunk = S < 64 ? S : 64;
+        for (int k = 0; a.admit && S > 0 && k < nmiss && nj < t.maxj; ++k)
+        {
+            const int ex = miss[k];
+            int found = -1, probes = 0;
+            while (probes < 2 * S)
+            {
+                const int nv = min(chunk, 2 * S - probes);
+                int idx = hand + lane;
+                if (idx >= S) idx -= S;
+                const bool valid = lane < nv;
+                const int p = valid ? pin[idx] : 0, rb = valid ? refb[idx] : 0;
+                const bool skip = p == epoch || p < 0;
+                const bool cand = valid && !skip && !rb;
+                const uint64_t cb = __ballot(cand);
+                const int upto = cb ? (__ffsll((long long)cb) - 1) : nv;
+                if (valid && lane < upto && !skip && rb) refb[idx] = 0;
+                if (cb)
+                {
+                    found = hand + upto;
+                    if (found >= S) found -= S;
+                    hand = found + 1 == S ? 0 : found + 1;
+                    break;
+                }
+                hand += nv;
+                if (hand >= S) hand -= S;
+                probes += nv;
+            }
+            if (found < 0)
+            {
+                novictim = 1;
+                break;
+            }
+            if (lane == 0)
+            {
+                const int s = found, old = t.owner[s];
+                if (old >= 0)
+                {
+                    const int ol = old / E, oe = old % E;
+                    t.slotof[old] = -1;
+                    bmx_expert* tab = reinterpret_cast<bmx_expert*>(t.tables[ol]);
+                    const uint64_t* h = t.home + ((size_t)ol * E + oe) * 3;
+                    tab[oe].tr[0] = h[0];
+                    tab[oe].tr[1] = h[1];
+                    tab[oe].tr[2] = h[2];
+                    ++evicted;
+                }
+                t.owner[s] = a.li * E + ex;
+                slotof[ex] = s;
+                refb[s] = 1;
+                pin[s] = epoch;
+                bmx_expert* tab = reinterpret_cast<bmx_expert*>(t.tables[a.li]);
+                const uint64_t b = t.slot_base[s];
+                tab[ex].tr[0] = b;
+                tab[ex].tr[1] = b + (uint64_t)t.off_u;
+                tab[ex].tr[2] = b + (uint64_t)t.off_d;
+                t.jobs[2 * nj] = ex;
+                t.jobs[2 * nj + 1] = s;
+                t.fresh[ex] = 1;
+            }
+            ++nj;
+        }
+        if (lane == 0)
+        {
+            if (a.admit && S > 0) t.ctl[0] = hand;
+            t.ctl[1] = epoch;
+            t.ctl[2] = nj;
+            t.stats[0] += nhit;
+            t.stats[1] += nmiss;
+            t.stats[2] += nj;
+            t.stats[3] += novictim;
+            t.stats[4] += evicted;
+        }
+    }
+    __syncthreads();
+    for (int s = tid; s < S; s += SL_THREADS)
+    {
+        t.pin[s] = pin[s];
+        t.refb[s] = refb[s];
+    }
+}
+
+// copies of the last step's admissions: blockIdx.y = job; 16-byte chunks, grid-stride
+__global__ __launch_bounds__(256) void k_slot_copy(bmx_slot_table t, int li)
+{
+    const int j = blockIdx.y;
+    if (j >= t.ctl[2]) return;
+    const int e = t.jobs[2 * j], s = t.jobs[2 * j + 1];
+    const bmx_expert& ex = reinterpret_cast<const bmx_expert*>(t.tables[li])[e];
+    const size_t tiles = (size_t)t.H * t.I / 256;
+    const uint64_t b = t.slot_base[s];
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+#pragma unroll 1
+    for (int m = 0; m < 3; ++m)
+    {
+        const size_t n16 = tiles * tile_bytes_dev(ex.fmt[m]) / 16;
+        const u32x4* src = reinterpret_cast<const u32x4*>(t.home[((size_t)li * t.E + e) * 3 + m]);
+        u32x4* dst = reinterpret_cast<u32x4*>(b + (m == 0 ? 0 : m == 1 ? (uint64_t)t.off_u : (uint64_t)t.off_d));
+        size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+        for (; i + 3 * stride < n16; i += 4 * stride)
+        {
+            const u32x4 v0 = __builtin_nontemporal_load(src + i), v1 = __builtin_nontemporal_load(src + i + stride);
+            const u32x4 v2 = __builtin_nontemporal_load(src + i + 2 * stride);
+            const u32x4 v3 = __builtin_nontemporal_load(src + i + 3 * stride);
+            dst[i] = v0;
+            dst[i + stride] = v1;
+            dst[i + 2 * stride] = v2;
+            dst[i + 3 * stride] = v3;
+        }
+        for (; i < n16; i += stride) dst[i] = __builtin_nontemporal_load(src + i);
+    }
+}
+
+static int check_table(const bmx_slot_table* t, const char* who)
+{
+    if (!t) return set_error(BMX_ERR_ARG, "%s: null table", who);
+    if (t->L <= 0 || t->E <= 0 || t->E > 512 || t->S < 0 || t->S > SL_MAXS || t->maxj < 0 || t->maxj > 64)
+        return set_error(BMX_ERR_ARG, "%s: unsupported L=%d E=%d S=%d maxj=%d (E <= 512, S <= %d, maxj <= 64)", who, t->L,
+                         t->E, t->S, t->maxj, SL_MAXS);
+    if (t->H <= 0 || t->I <= 0 || t->H % 16 || t->I % 16 || t->rec <= 0 || t->rec % 16 || t->off_u % 16 || t->off_d % 16)
+        return set_error(BMX_ERR_ARG, "%s: bad geometry", who);
+    if (!t->slotof || !t->owner || !t->refb || !t->pin || !t->ctl || !t->jobs || !t->fresh || !t->stats || !t->home ||
+        !t->slot_base || !t->tables)
+        return set_error(BMX_ERR_ARG, "%s: null table array", who);
+    return BMX_OK;
+}
+
+int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s)
+{
+    int rc = check_table(t, "bmx_slot_step");
+    if (rc) return rc;
+    if (li < 0 || li >= t->L || n < 0 || (n && !sel)) return set_error(BMX_ERR_ARG, "bmx_slot_step: bad layer or picks");
+    SlotArgs a;
+    a.t = *t;
+    a.sel = sel;
+    a.first = first;
+    a.li = li;
+    a.n = n;
+    a.admit = admit ? 1 : 0;
+    hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
+    return check_launch("bmx_slot_step");
+}
+
+int launch_slot_copy(const bmx_slot_table* t, int li, hipStream_t s)
+{
+    int rc = check_table(t, "bmx_slot_copy");
+    if (rc) return rc;
+    if (li < 0 || li >= t->L) return set_error(BMX_ERR_ARG, "bmx_slot_copy: bad layer");
+    if (t->maxj == 0) return BMX_OK;
+    hipLaunchKernelGGL(k_slot_copy, dim3(64, (unsigned)t->maxj), dim3(256), 0, s, *t, li);
+    return check_launch("bmx_slot_copy");
+}
+
+}  // namespace bmx
+
+using namespace bmx;
+
+extern "C" {
+
+int bmx_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit,
+                  bmx_stream_t stream)
+{
+    return launch_slot_step(t, li, sel, n, first, admit, static_cast<hipStream_t>(stream));
+}
+
+int bmx_slot_copy(const bmx_slot_table* t, int li, bmx_stream_t stream)
+{
+    return launch_slot_copy(t, li, static_cast<hipStream_t>(stream));
+}
+
+int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream)
+{
+    if (n < 0 || (n && (!src || !dst || !bytes))) return set_error(BMX_ERR_ARG, "bmx_slot_stage_async: bad arguments");
+    for (int i = 0; i < n; ++i)
+    {
+        const hipError_t e = hipMemcpyAsync(dst[i], src[i], bytes[i], hipMemcpyDefault, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return set_error(BMX_ERR_HIP, "bmx_slot_stage_async: copy %d: %s", i, hipGetErrorString(e));
+    }
+    return BMX_OK;
+}
+
+int bmx_host_device_ptr(void* host, uint64_t* device_addr)
+{
+    if (!host || !device_addr) return set_error(BMX_ERR_ARG, "bmx_host_device_ptr: null pointer");
+    void* d = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&d, host, 0);
+    if (e != hipSuccess) return set_error(BMX_ERR_HIP, "bmx_host_device_ptr: %s", hipGetErrorString(e));
+    *device_addr = reinterpret_cast<uint64_t>(d);
+    return BMX_OK;
+}
+
+}  // extern "C"

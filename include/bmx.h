@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define BMX_ABI_VERSION 1
+#define BMX_ABI_VERSION 2
 
 typedef void* bmx_stream_t; /* hipStream_t */
 
@@ -70,6 +70,8 @@ typedef struct bmx_moe_desc {
     float act_limit;             /* 0 = off */
     const bmx_expert* experts;   /* device [E] */
     const bmx_expert* shared;    /* device [1] or NULL: shared expert, weight 1, added after the routed slots */
+    const int32_t* fresh;        /* device [E] or NULL: 1 = expert admitted to a slot by the last slot-table step (its
+                                    copy may still be in flight); read by BMX_STAGE_GATE_UP_RESIDENT / _STAGED */
 } bmx_moe_desc;
 
 /* Dispatch output: rows grouped per expert, stable by (expert, token, slot). R = T * topk (+ T with a shared expert,
@@ -163,11 +165,58 @@ int bmx_moe_experts(const bmx_moe_desc* desc, const void* x_fp16, int T, const b
  *   BMX_STAGE_DOWN_OUT down epilogue into y_rows for every row (instead of COMBINE) */
 enum bmx_stage {
     BMX_STAGE_GATE_UP = 0, BMX_STAGE_ACT = 1, BMX_STAGE_DOWN = 2, BMX_STAGE_COMBINE = 3, BMX_STAGE_DOWN_OUT = 4,
-    BMX_STAGE_PREP = 5
+    BMX_STAGE_PREP = 5,
+    /* BMX_STAGE_GATE_UP split by desc->fresh: the groups of experts that were resident before the slot-table step, and
+     * the groups of experts it admitted (run after their copies). Together they equal BMX_STAGE_GATE_UP. */
+    BMX_STAGE_GATE_UP_RESIDENT = 6, BMX_STAGE_GATE_UP_STAGED = 7
 };
 int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T, const bmx_routes* routes,
                   void* act_rows_fp16, float* y_rows, const void* w_fp16, float* out, void* workspace,
                   size_t workspace_bytes, int path, bmx_stream_t stream);
+
+/* ---- expert-slot table ----
+ * (layer, expert) -> VRAM slot (the reference's Pool, engine/tiers.py:275-373, and its step kernel ec_step_k,
+ * engine/ec.py:16-76). Every expert has a home holding its three trellis matrices (pinned host memory the GPU reads
+ * directly, or device memory); S uniform slots of rec bytes (gate at 0, up at off_u, down at off_d) hold copies of
+ * recently used experts. The layer tables' bmx_expert.tr point at the slot of a resident expert and at the home of any
+ * other, so the expert kernels read either. All state is device memory the caller allocates and initialises (slotof and
+ * owner -1, refb 0, pin 0 or < 0 for a disabled slot, ctl and stats 0, every table entry pointing at its home). Calls on
+ * one table are stream-ordered by the caller. H and I give the matrix sizes: H * I / 256 tiles of the expert's format. */
+typedef struct bmx_slot_table {
+    int32_t L, E, S, maxj;      /* layers, experts per layer (<= 512), slots, admissions per step (<= 64) */
+    int32_t H, I;
+    int64_t rec, off_u, off_d;  /* slot bytes and the up / down offsets inside a slot (16-byte multiples) */
+    int32_t* slotof;            /* [L * E] slot of (layer, expert), -1 = not resident */
+    int32_t* owner;             /* [S] li * E + e of the slot's expert, -1 = free */
+    int32_t* refb;              /* [S] CLOCK reference bits */
+    int32_t* pin;               /* [S] step counter value of the slot's last use; < 0 = slot disabled */
+    int32_t* ctl;               /* [4] CLOCK hand, step counter, admissions of the last step, reserved */
+    int32_t* jobs;              /* [2 * maxj] (expert, slot) of each admission of the last step */
+    int32_t* fresh;             /* [E] 1 = admitted by the last step (for bmx_moe_desc.fresh of that layer) */
+    int64_t* stats;             /* [5] running hits, misses, admissions, steps without a victim, evictions */
+    const uint64_t* home;       /* [L * E * 3] device-visible address of each expert's gate, up, down trellis */
+    const uint64_t* slot_base;  /* [S] address of each slot */
+    const uint64_t* tables;     /* [L] address of each layer's bmx_expert table (E entries) */
+} bmx_slot_table;
+
+/* One step of layer li over the picks sel[n] (global ids, local = id - first): the layer's picked experts that are
+ * resident are hits (reference bit set, pinned for this step); the others are misses, admitted when admit != 0 in
+ * ascending expert order, at most maxj, each into the first slot from the CLOCK hand that is enabled, not pinned this
+ * step and whose reference bit is clear (bits of slots passed over are cleared; at most 2 S probes per miss, a miss that
+ * finds none ends the step's admissions). An admission evicts the slot's previous expert (its table entry back to its
+ * home), points the admitted expert's entry at the slot, and writes a job; fresh marks the admitted experts. One
+ * workgroup; no host synchronisation. Misses that are not admitted run from their home. */
+int bmx_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit,
+                  bmx_stream_t stream);
+/* The copies of the last step's jobs of layer li, home -> slot (a kernel reading the home directly: pinned host memory
+ * over PCIe). Run it on a side stream ordered after bmx_slot_step; the admitted experts' gate / up
+ * (BMX_STAGE_GATE_UP_STAGED) must be ordered after it. */
+int bmx_slot_copy(const bmx_slot_table* t, int li, bmx_stream_t stream);
+/* Host-planned staging: n copies src[i] -> dst[i] of bytes[i] (hipMemcpyAsync, e.g. pinned host -> slot), in order on
+ * stream (the reference's stage_layer, engine/kernels/nv2/nv2_host.cpp:1558-1593). */
+int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream);
+/* Device-visible address of pinned host memory (hipHostGetDevicePointer), for bmx_slot_table.home. */
+int bmx_host_device_ptr(void* host, uint64_t* device_addr);
 
 /* Combine: out[t] = sum over k ascending of w[t, k] * y_rows[inv[t, k]] (picks with inv < 0 or w = 0 skipped), then
  * + y_rows[offsets[E] + t] when has_shared (x16_red_k order, engine/kernels/x16/x16_dev.cu:354-384). */

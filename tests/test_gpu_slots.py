@@ -1,0 +1,156 @@
+"""GPU expert-slot table against the oracle's CLOCK step (bit-exact state after every step), the staging copies (slot
+bytes equal the home bytes), and the layer with experts staged from pinned host memory (bit-identical outputs to the
+same layer with every expert resident)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def small_layers(n_layers, E, H, I, seed, home, fmts=None):
+    import bmx
+    fm = fmts or (bmx.TF_K3,) * 3
+    return [bmx.ExpertTable.random(H, I, E, fm, seed=seed + li, device="cuda", home=home) for li in range(n_layers)]
+
+
+def tables_of(slots):
+    """Host copies of every layer's bmx_expert tr pointers: [L, E, 3] uint64."""
+    import bmx
+    es = ctypes.sizeof(bmx._lib.Expert)
+    out = []
+    for t in slots.layers:
+        raw = t.table().cpu().numpy().tobytes()
+        arr = (bmx._lib.Expert * (t.E + (1 if t.has_shared else 0))).from_buffer_copy(raw)
+        out.append([[arr[e].tr[m] for m in range(3)] for e in range(t.E)])
+        assert len(raw) == es * (t.E + (1 if t.has_shared else 0))
+    return np.array(out, dtype=np.uint64)
+
+
+def check_state(slots, ref, fresh_want, step):
+    torch.cuda.synchronize()
+    S = slots.S
+    assert np.array_equal(slots.slotof.cpu().numpy(), ref.slotof), step
+    assert np.array_equal(slots.owner.cpu().numpy()[:S], ref.owner[:S]), step
+    assert np.array_equal(slots.refb.cpu().numpy()[:S], ref.refb[:S]), step
+    assert np.array_equal(slots.pin.cpu().numpy()[:S], ref.pin[:S]), step
+    ctl = slots.ctl.cpu().numpy()
+    assert ctl[0] == ref.hand and ctl[1] == ref.epoch, (step, ctl, ref.hand, ref.epoch)
+    assert np.array_equal(slots.stats_t.cpu().numpy(), ref.stats), (step, slots.stats_t.cpu().numpy(), ref.stats)
+    assert np.array_equal(slots.fresh.cpu().numpy(), fresh_want), step
+    # every table entry points at its slot when resident, at its home otherwise
+    tr = tables_of(slots)
+    base = slots.arena.data_ptr()
+    t0 = slots.layers[0]
+    for li, t in enumerate(slots.layers):
+        for e in range(t.E):
+            s = int(ref.slotof[li * t.E + e])
+            want = (t.addr[e] if s < 0 else (base + s * t0.rec, base + s * t0.rec + t0.off_u, base + s * t0.rec + t0.off_d))
+            assert tuple(int(v) for v in tr[li, e]) == tuple(want), (step, li, e)
+
+
+@pytest.mark.parametrize("S,maxj,disabled", [(10, 4, (3,)), (5, 8, ()), (0, 4, ())])
+def test_slot_step_matches_oracle(cuda, oracle, S, maxj, disabled):
+    import bmx
+    Lyr, E = 3, 16
+    layers = small_layers(Lyr, E, 256, 128, 10, "device")
+    slots = bmx.ExpertSlots(layers, S, maxj=maxj, disabled=disabled)
+    ref = oracle.SlotTable(Lyr, E, S)
+    for s in disabled:
+        ref.pin[s] = -1
+    rng = np.random.default_rng(S * 100 + maxj)
+    first = 7
+    for step in range(40):
+        li = int(rng.integers(0, Lyr))
+        n = int(rng.integers(0, 12))
+        sel = rng.integers(0, E + 3, n) + first - 1            # a few ids outside [first, first + E): dropped
+        admit = bool(rng.random() < 0.85)
+        say("slot step", step, "layer", li, "picks", n, "admit", admit)
+        slots.step(li, torch.from_numpy(sel.astype(np.int64)).cuda(), first, admit)
+        jobs, ev = ref.step(li, sel.astype(np.int64), first, admit, maxj)
+        fresh_want = np.zeros(E, np.int32)
+        fresh_want[jobs[:, 0]] = 1
+        check_state(slots, ref, fresh_want, step)
+        nj = int(slots.ctl[2].item())
+        assert nj == len(jobs)
+        assert np.array_equal(slots.jobs.cpu().numpy()[:2 * nj].reshape(nj, 2), jobs)
+
+
+def test_slot_copies_deliver_home_bytes(cuda):
+    import bmx
+    layers = small_layers(2, 12, 256, 128, 30, "host", fmts=(bmx.TF_K2, bmx.TF_K25, bmx.TF_K4))
+    slots = bmx.ExpertSlots(layers, 7, maxj=6)
+    rng = np.random.default_rng(5)
+    for step in range(12):
+        li = step % 2
+        sel = torch.from_numpy(rng.integers(0, 12, 5).astype(np.int64)).cuda()
+        slots.step(li, sel)
+    slots.wait_copies(0)
+    slots.wait_copies(1)
+    torch.cuda.synchronize()
+    slotof = slots.slotof.cpu().numpy().reshape(2, 12)
+    arena = slots.arena.cpu().numpy()
+    t0 = layers[0]
+    checked = 0
+    for li in range(2):
+        for e in range(12):
+            s = slotof[li, e]
+            if s < 0:
+                continue
+            home = layers[li].arena[e].numpy()
+            for m, off in enumerate((0, t0.off_u, t0.off_d)):
+                nb = layers[li].mat_bytes(e, m)
+                assert np.array_equal(arena[s, off:off + nb], home[off:off + nb]), (li, e, m)
+            checked += 1
+    say("resident experts checked", checked)
+    assert checked == 7
+
+
+def test_layer_with_staged_experts_matches_resident(cuda):
+    """The same layers computed with every expert resident in device memory and with homes in pinned host memory staged
+    through a small slot table (hits, admissions copied on the side stream, and misses left at home when maxj runs
+    out): identical outputs, bit for bit, decode and prefill paths."""
+    import bmx
+    from bmx import synth
+    Lyr, E, H, I, topk = 3, 24, 512, 256, 4
+    dev_layers = small_layers(Lyr, E, H, I, 50, "device")
+    host_layers = small_layers(Lyr, E, H, I, 50, "host")
+    slots = bmx.ExpertSlots(host_layers, 9, maxj=3)
+    kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
+    ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
+    st_layers = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(Lyr)]
+    rng = np.random.default_rng(9)
+    for step in range(9):
+        li = step % Lyr
+        T = (1, 3, 40)[step % 3]
+        x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16)).cuda()
+        lg = torch.from_numpy(synth.zipf_logits(T, E, 1.1, seed=step)).cuda()
+        for path in (bmx.PATH_DECODE, bmx.PATH_PREFILL):
+            sel, w = ref_layers[li].routing_fn(T, None, x, {"logits": lg})
+            want = ref_layers[li].run_bszN(x, sel, w, path)
+            sel2, w2 = st_layers[li].routing_fn(T, None, x, {"logits": lg})
+            st_layers[li].layer(li, sel2, w2, x, T)
+            got = st_layers[li].run_bszN(x, sel2, w2, path)
+            torch.cuda.synchronize()
+            say("staged layer step", step, "layer", li, "T", T, "path", path, "stats", slots.stats())
+            assert torch.equal(sel, sel2) and torch.equal(got, want)
+    h, m, adm, novic, ev = slots.stats()
+    assert m > 0 and adm > 0 and ev > 0 and m > adm      # misses, admissions, evictions and unadmitted misses all ran
+
+
+def test_stage_async_copies(cuda):
+    import bmx
+    layers = small_layers(1, 4, 256, 128, 70, "host")
+    slots = bmx.ExpertSlots(layers, 4, maxj=2)
+    t = layers[0]
+    src = [t.addr[e][0] for e in range(4)]
+    dst = [slots.arena.data_ptr() + s * t.rec for s in range(4)]
+    slots.stage_async(src, dst, [t.rec] * 4)
+    torch.cuda.synchronize()
+    assert torch.equal(slots.arena.cpu(), t.arena.clone())
