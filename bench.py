@@ -116,6 +116,137 @@ def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
             "us_per_layer": med * 1e6}
 
 
+def bench_c4(args):
+    """43 layers of the GLM-shaped layer in decode (batch 1) with the expert-slot table: routed experts at home in pinned
+    host memory, a VRAM cache of 30 % of them warmed with each layer's most popular experts, Zipf(1.1) routing with a
+    per-layer permutation over a cycle of synthetic tokens. A step is one token through the 43 layers: router, slot step
+    (copies of admissions on a side stream), dispatch, gate / up of resident experts, gate / up of staged experts after
+    their copies, epilogue, down, combine."""
+    import numpy as np
+    import torch
+    import bmx
+    from bmx import synth
+    dev = torch.device("cuda:0")
+    c = synth.CONFIGS["c4"]
+    NL, E, H, I, topk = c["layers"], c["E"], c["H"], c["I"], c["topk"]
+    NTOK = 64
+    S = int(round(c["cache_frac"] * NL * E))
+    log(f"bench c4: {NL} layers x {E} experts, homes in pinned host memory, {S} VRAM slots")
+    layers, biases, lgs = [], [], []
+    rng = np.random.default_rng(0)
+    NH = 16      # distinct pinned home arenas (2 GB each); layer li reads the trellis bytes of layer li % NH
+    for li in range(NL):
+        if li < NH:
+            t = bmx.ExpertTable.random(H, I, E, synth.formats("c4", E, True), shared=True, seed=1000 + li, device=dev,
+                                       home="host")
+        else:
+            h = layers[li % NH]
+            t = bmx.ExpertTable(H, I, h.arena, h.fmt, h.suh, h.svh, h.off_u, h.off_d, E, True)
+        t.shared_to_device()
+        layers.append(t)
+        biases.append(torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).to(dev))
+        lgs.append(synth.zipf_logits(NTOK, E, 1.1, seed=li, perm_seed=7919 * (li + 1)))
+        if li % 8 == 0:
+            log(f"bench c4: layer {li} built")
+    lg_all = torch.from_numpy(np.stack(lgs)).to(dev)            # [NL, NTOK, E] fp16
+    slots = bmx.ExpertSlots(layers, S, maxj=16)
+    # warm: each layer's most popular experts (Zipf rank order of its permutation), S // NL per layer
+    per = S // NL
+    for li in range(NL):
+        perm = np.random.default_rng(7919 * (li + 1)).permutation(E)
+        slots.warm(li, [int(e) for e in perm[:per]])
+    torch.cuda.synchronize()
+    h0 = slots.stats()
+    log(f"bench c4: warmed, stats {h0}")
+
+    L = bmx.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float16)).to(dev)
+    descs = [slots.desc(li, topk) for li in range(NL)]
+    sel = torch.empty((1, topk), dtype=torch.int64, device=dev)
+    w = torch.empty((1, topk), dtype=torch.float16, device=dev)
+    out = torch.empty((NL, H), dtype=torch.float32, device=dev)
+    rpg = L.bmx_rows_per_group(1, topk, 1)
+    routes = bmx.ops.RoutesBuf(1, topk, E, True, rpg, dev)
+    dws_n = L.bmx_dispatch_workspace(1, topk, E)
+    dws = torch.empty(max(dws_n, 1), dtype=torch.uint8, device=dev)
+    ws_n = L.bmx_experts_workspace(ctypes.byref(descs[0]), 1, 1)
+    ws = torch.zeros(ws_n, dtype=torch.uint8, device=dev)
+    stepped = [torch.cuda.Event() for _ in range(NL)]
+    copied = [torch.cuda.Event() for _ in range(NL)]
+    side = slots.side
+    tstruct = ctypes.byref(slots.struct)
+
+    def token(tok):
+        s = torch.cuda.current_stream()
+        sp = ctypes.c_void_p(s.cuda_stream)
+        for li in range(NL):
+            lgp = ctypes.c_void_p(lg_all.data_ptr() + (li * NTOK + tok) * E * 2)
+            bmx._lib.check(L.bmx_router_topk(lgp, P(biases[li]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0, P(sel),
+                                             P(w), sp), "router")
+            bmx._lib.check(L.bmx_slot_step(tstruct, li, P(sel), topk, 0, 1, sp), "slot step")
+            stepped[li].record(s)
+            side.wait_event(stepped[li])
+            bmx._lib.check(L.bmx_slot_copy(tstruct, li, ctypes.c_void_p(side.cuda_stream)), "slot copy")
+            copied[li].record(side)
+            bmx._lib.check(L.bmx_dispatch(P(sel), 1, topk, E, 0, 1, rpg, ctypes.byref(routes.struct), P(dws), dws_n, sp),
+                           "dispatch")
+            d = ctypes.byref(descs[li])
+            o = ctypes.c_void_p(out.data_ptr() + li * H * 4)
+            for st in (bmx._lib.STAGE_GATE_UP_RESIDENT, None, bmx._lib.STAGE_GATE_UP_STAGED, bmx._lib.STAGE_ACT,
+                       bmx._lib.STAGE_DOWN, bmx._lib.STAGE_COMBINE):
+                if st is None:
+                    s.wait_event(copied[li])
+                    continue
+                bmx._lib.check(L.bmx_moe_stage(d, st, P(x), 1, ctypes.byref(routes.struct), None, None, P(w), o, P(ws),
+                                               ws_n, 1, sp), "stage")
+
+    for i in range(args.warmup):
+        token(i % NTOK)
+    torch.cuda.synchronize()
+    st0 = slots.stats()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        token((args.warmup + i) % NTOK)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    st1 = slots.stats()
+    d = [b - a for a, b in zip(st0, st1)]
+    exp_bytes = layers[0].expert_bytes(0)
+    staged = d[2] * exp_bytes
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(layers[0], sel.repeat(4, 1), w.repeat(4, 1))
+        if cpu:
+            per_layer = cpu["us_per_layer"] / 4
+            cpu = {"value": round(1e6 / (per_layer * NL), 3), "unit": "tokens/s", "cores": cpu["cores"], "kind": "reference",
+                   "sample": f"one c4 layer's call on 4 tokens (routes of the last timed token), {cpu['sample']}; "
+                             f"per token x {NL} layers"}
+    res = {
+        "metric": METRIC, "value": round(1e3 / ms, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16",
+        "data": f"synthetic: random EXL3 3 bpw trellis codes, homes of routed experts in pinned host memory ({NH} distinct "
+                f"2 GB arenas, layer li reading those of layer li % {NH}: the box pins about 55 GB), suh ~ U(0.5,1.5), "
+                "svh ~ U(0.5,1.5)/sqrt(k), x ~ N(0,1) fp16, router logits = Zipf(1.1) log-popularity of a per-layer "
+                f"permutation + Gumbel noise over a cycle of {NTOK} tokens, bias ~ N(0,0.1); seed 0",
+        "config": {"workload": f"c4 decode stack: {NL} layers of {E} routed experts top-{topk} sigmoid+bias + 1 shared (in "
+                               f"VRAM), H {H}, I {I}, EXL3 3 bpw; expert-slot table of {S} VRAM slots (30 %) warmed with each "
+                               f"layer's top {per} experts by popularity", "tokens": 1, "layers": NL, "path": "decode",
+                   "step": "per layer: router + slot step (copies on a side stream) + dispatch + gate/up (resident, then "
+                           "staged) + down + combine"},
+        "us_per_token": round(ms * 1e3, 3), "us_per_layer": round(ms * 1e3 / NL, 3),
+        "slot_stats_per_token": {"hits": d[0] / args.steps, "misses": d[1] / args.steps, "admitted": d[2] / args.steps,
+                                 "no_victim": d[3] / args.steps, "evictions": d[4] / args.steps},
+        "hit_rate": round(d[0] / max(1, d[0] + d[1]), 4),
+        "staged_bytes_per_token": staged / args.steps,
+        "staged_gbps": round(staged / (ms * 1e-3 * args.steps) / 1e9, 2),
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,6 +263,8 @@ def main():
               f"across GPUs only in design, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    if args.config == "c4":
+        return bench_c4(args)
     import torch
     import bmx
     from bmx import synth

@@ -89,6 +89,15 @@ class ExpertTable:
         fmt = torch.tensor(fmts, dtype=torch.int32)
         return cls(H, I, arena, fmt, suh, svh, off_u, off_d, E, shared)
 
+    def shared_to_device(self):
+        """Keep the shared expert's trellis in device memory (a copy; the routed experts stay at their home). Call before
+        the table is built."""
+        if not self.has_shared or self._table is not None:
+            raise ValueError("shared_to_device: no shared expert, or the table is already built")
+        self._shared_dev = self.arena[self.E].to(self.device)
+        b = self._shared_dev.data_ptr()
+        self.addr[self.E] = (b, b + self.off_u, b + self.off_d)
+
     def mat_bytes(self, e, m):
         k, n = ((self.H, self.I), (self.H, self.I), (self.I, self.H))[m]
         return matrix_bytes(k, n, int(self.fmt[e, m]))

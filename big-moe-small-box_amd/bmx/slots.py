@@ -75,10 +75,12 @@ class ExpertSlots:
         return self.layers[li].desc(topk, first, act, gated, act_limit, fresh=self.fresh)
 
     def warm(self, li, experts, first=0):
-        """Admit the given local experts of layer li (a step over them) and wait for their copies."""
-        sel = torch.as_tensor(list(experts), dtype=torch.int64, device=self.arena.device) + first
-        self.step(li, sel, first)
-        self.wait_copies(li)
+        """Admit the given local experts of layer li (steps over maxj of them at a time) and wait for their copies."""
+        experts = list(experts)
+        for i in range(0, len(experts), max(1, self.maxj)):
+            sel = torch.as_tensor(experts[i:i + self.maxj], dtype=torch.int64, device=self.arena.device) + first
+            self.step(li, sel, first)
+            self.wait_copies(li)
 
     def stage_async(self, src, dst, nbytes, stream=None):
         """Host-planned staging: copies src[i] -> dst[i] of nbytes[i] bytes (addresses) with hipMemcpyAsync."""
