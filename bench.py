@@ -64,7 +64,8 @@ def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
     # sel / w: the routes of the bounded sample (the first tokens of the timed batch)
     """The reference's CPU lane (ft_n135.h moe_forward4, built from the reference sources into oracle/_ref) on the same
     routes, driven as the reference's cpu_forward drives it (nv2_host.cpp:1974-2003): experts in RAM, routes given (no
-    router), mode auto, the shared expert as a weight-1 job. Median of warm calls, whole-call wall time."""
+    router), mode auto (I16 when an expert of the sample has a format other than K 3), the shared expert as a weight-1
+    job. Median of warm calls, whole-call wall time."""
     import numpy as np
     from oracle import oracle as O
     R = O.ref_lane()
@@ -84,11 +85,16 @@ def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
         return None
     keep = []
     tf = {0: 0, 1: 1, 2: 2}
+    mode = -1
     try:
         for e in sorted(set(sel.ravel().tolist())):
             ex = tab.host_expert(e)
             if any(f not in tf for f in ex["fmt"]):
                 return None
+            if any(f != 2 for f in ex["fmt"]):
+                # formats other than K 3 decode only in the I16 (p16 VBMI) kernel; the reference switches to it when the
+                # first job's expert has one (ft_n135.h:933-936), a layer of mixed formats needs it for every call
+                mode = 2
             sc = [ex["suh"][0], ex["svh"][0], ex["suh"][1], ex["svh"][1], ex["suh"][2], ex["svh"][2]]
             sc = [np.ascontiguousarray(a.view(np.uint16)) for a in sc]
             keep += ex["tr"] + sc
@@ -101,7 +107,7 @@ def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
         t_end = time.perf_counter() + budget_s
         for i in range(10000):
             t0 = time.perf_counter()
-            R.ref_lane_forward(x.ctypes.data, T, si.ctypes.data, wf.ctypes.data, k, out.ctypes.data, -1)
+            R.ref_lane_forward(x.ctypes.data, T, si.ctypes.data, wf.ctypes.data, k, out.ctypes.data, mode)
             times.append(time.perf_counter() - t0)
             if (i >= 60 and time.perf_counter() > t_end) or time.perf_counter() > t_end + budget_s:
                 break
@@ -111,7 +117,7 @@ def cpu_baseline(tab, sel, w, budget_s=12.0, max_threads=16):
     return {"value": T / med, "unit": "tokens/s", "cores": len(cpus), "kind": "reference",
             "sample": f"{len(times)} calls of one {T}-token layer call (the routes of the first {T} tokens of the timed "
                       f"batch, {k} jobs per token{' incl. the shared expert' if tab.has_shared else ''}), median wall "
-                      f"time {med * 1e6:.0f} us; moe_forward4 mode auto, {len(cpus)} threads "
+                      f"time {med * 1e6:.0f} us; moe_forward4 mode {'I16' if mode == 2 else 'auto'}, {len(cpus)} threads "
                       f"pinned one per physical core ({ncores} physical cores available), {cpu_model()}",
             "us_per_layer": med * 1e6}
 
@@ -382,7 +388,7 @@ def main():
                    f"(profiles/{kind}_{args.config}_t{T}.md)") if traffic else None
     if prefill:
         ach = gu_flops / (gu_ms * 1e-3) / 1e12
-        roofline = {"kernel": "k_pf_gemm<2> (BMX_STAGE_GATE_UP: trellis decode to LDS + gate/up MFMA grouped GEMM)",
+        roofline = {"kernel": "k_pf_gemm<false> (BMX_STAGE_GATE_UP: trellis decode to LDS + gate/up MFMA grouped GEMM)",
                     "bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(ach / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": traffic, "algorithmic_flops": gu_flops,
                     "traffic_source": traffic_src}

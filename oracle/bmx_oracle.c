@@ -219,6 +219,8 @@ static float act_gate(int act, int gated, float g, float u, float limit)
     return (float)(x * uu);
 }
 
+float bmxo_act(int act, int gated, float g, float u, float limit) { return act_gate(act, gated, g, u, limit); }
+
 typedef struct { float* w[3]; } dense3;   /* dequantized gate [H][I], up [H][I], down [I][H] as fp32 */
 
 static void dense_expert(const bmxo_expert* e, int H, int I, dense3* d)

@@ -44,6 +44,9 @@ void bmxo_prep(const uint16_t* x, const uint16_t* suh, int k, uint16_t* xt);
 /* activations (exllamav3 MOE_COOP_ACT_* numbering) */
 enum { BMXO_ACT_SILU = 0, BMXO_ACT_GELU = 1, BMXO_ACT_RELU2 = 2, BMXO_ACT_SILU_OAI = 3 };
 
+/* a = act_gate(g, u): the epilogue's activation of one gate / up pair (limit 0 = no clamp) */
+float bmxo_act(int act, int gated, float g, float u, float limit);
+
 typedef struct {
     const uint8_t* tr[3];     /* gate, up, down trellis */
     const uint16_t* suh[3];   /* fp16 input scales: [H], [H], [I] */

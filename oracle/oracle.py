@@ -62,6 +62,7 @@ def lib():
                                        _P, _I, _P]
         L.bmxo_exp.argtypes = [ctypes.c_float]; L.bmxo_exp.restype = ctypes.c_float
         L.bmxo_sigmoid.argtypes = [ctypes.c_float]; L.bmxo_sigmoid.restype = ctypes.c_float
+        L.bmxo_act.argtypes = [_I, _I, ctypes.c_float, ctypes.c_float, ctypes.c_float]; L.bmxo_act.restype = ctypes.c_float
         L.bmxo_router.argtypes = [_P, _P, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, ctypes.c_int64, _P, _P]
         L.bmxo_dispatch.argtypes = [_P, _I, _I, _I, ctypes.c_int64, _I, _P, _P, _P, _P, _P, _P]
         L.bmxo_dispatch.restype = _I
@@ -237,6 +238,11 @@ class SlotTable:
 
 def exp32(x):
     return np.float32(lib().bmxo_exp(float(x)))
+
+
+def act(a, gated, g, u, limit=0.0):
+    """act_gate of one (gate, up) pair (x16_dev.cu:68-112)"""
+    return np.float32(lib().bmxo_act(int(a), int(gated), float(g), float(u), float(limit)))
 
 
 # ---- numpy twin of the decode (independent restatement) ---------------------------------------------------------

@@ -261,3 +261,34 @@ def test_full_size_properties_c2_t8(cuda):
     full = bmx.ops.moe_forward(tab.desc(8), x, sel, w)
     only_shared = bmx.ops.moe_forward(tab.desc(8), x, sel, torch.zeros_like(w))
     assert torch.allclose(full, out + only_shared, rtol=1e-5, atol=1e-5)
+
+
+ACTS = [("gelu", 1, True, 0.0), ("relu2", 2, True, 0.0), ("silu_oai", 3, True, 0.0), ("silu_oai limit 7", 3, True, 7.0),
+        ("silu limit 0.5", 0, True, 0.5), ("not gated", 0, False, 0.0)]
+
+
+@pytest.mark.parametrize("name,act,gated,limit", ACTS, ids=[a[0] for a in ACTS])
+@pytest.mark.parametrize("path", [1, 2], ids=["decode", "prefill"])
+def test_layer_activations(cuda, oracle, name, act, gated, limit, path):
+    """Each activation and clamp of the epilogue (x16_dev.cu:68-112) on both expert paths against the oracle."""
+    import bmx
+    from bmx import synth
+    say("act", name, "path", path)
+    E, T, H, I = 12, 6, 512, 384
+    tab = synth.table("c2", seed=7, device=cuda, E=E, H=H, I=I)
+    x, lg, bias = synth.inputs("c2", T=T, seed=8, device=cuda)
+    x = x[:, :H].contiguous()
+    layer = bmx.MoELayer(tab, 4, score=bmx.SCORE_SIGMOID, bias=bias[:E].contiguous(), renorm=True, scale=2.5, act=act,
+                         gated=gated, act_limit=limit)
+    sel, w = layer.routing_fn(T, None, x, {"logits": lg[:, :E].contiguous()})
+    out = layer.run_bszN(x, sel, w, path=path).cpu().numpy()
+    xs, ss, ws = x.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy()
+    exps = [tab.host_expert(e) for e in range(E)]
+    want = oracle.moe_forward(exps, 0, tab.host_expert(E), H, I, xs, ss, ws, act=act, gated=gated, limit=limit)
+    err_abs, err_rel = float(np.abs(out - want).max()), rel_rms(out, want)
+    say("act", name, "max_abs", err_abs, "rel_rms", err_rel)
+    assert err_abs < MAX_ABS and err_rel < REL_RMS
+    # the activation matters: SiLU without clamp gives a different layer
+    if (act, gated, limit) != (0, True, 0.0):
+        plain = oracle.moe_forward(exps, 0, tab.host_expert(E), H, I, xs, ss, ws)
+        assert rel_rms(plain, want) > 10 * REL_RMS

@@ -148,3 +148,67 @@ def test_dropped_picks_reference_known_answer(oracle):
     # first offset: ids 7.. with the sentinel first + E = 11
     out7 = oracle.moe_forward(exps, 7, None, H, I, x, sel + 7, w)
     assert np.array_equal(out7, out)
+
+
+def test_activations_closed_forms(oracle):
+    """act_gate (x16_dev.cu:68-112) against closed forms evaluated by scipy: SiLU = g * expit(g); the tanh GELU within its
+    published distance of the exact GELU g * Phi(g) (< 1e-3 here; dropping the cubic term costs ~2e-2); ReLU^2; the
+    gpt-oss SwiGLU (u + 1) * g * expit(1.702 g), whose glu is within 2.1e-2 of the exact GELU (1.0 instead of 1.702 is
+    off by > 0.1); the non-gated relu(u) * u; the clamps of limit (g from above only, u on both sides)."""
+    from scipy.special import expit, ndtr
+    rng = np.random.default_rng(17)
+    g = np.concatenate([rng.uniform(-6, 6, 400), [0.0, -0.0, 1e-3, -1e-3, 5.5]]).astype(np.float32)
+    u = rng.uniform(-3, 3, g.size).astype(np.float32)
+    A = lambda a, gd, lim=0.0: np.array([oracle.act(a, gd, gi, ui, lim) for gi, ui in zip(g, u)], np.float64)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    assert np.allclose(A(oracle.ACT_SILU, 1), g64 * expit(g64) * u64, rtol=1e-6, atol=1e-7)
+    gelu_exact = g64 * ndtr(g64)
+    assert np.abs(A(oracle.ACT_GELU, 1) / np.where(u64 == 0, 1, u64) - gelu_exact).max() < 1e-3
+    assert np.allclose(A(oracle.ACT_RELU2, 1), np.maximum(g64, 0) ** 2 * u64, rtol=1e-6, atol=1e-7)
+    oai = A(oracle.ACT_SILU_OAI, 1)
+    assert np.allclose(oai, (u64 + 1) * g64 * expit(1.702 * g64), rtol=1e-6, atol=1e-7)
+    assert np.abs(oai / (u64 + 1) - gelu_exact).max() < 2.1e-2
+    assert oracle.act(oracle.ACT_SILU_OAI, 1, 2.0, -1.0) == 0.0
+    assert np.allclose(A(oracle.ACT_SILU, 0), np.maximum(u64, 0) * u64, rtol=1e-6, atol=1e-7)
+    lim = 1.5
+    gc, uc = np.minimum(g64, lim), np.clip(u64, -lim, lim)
+    assert np.allclose(A(oracle.ACT_SILU_OAI, 1, lim), (uc + 1) * gc * expit(1.702 * gc), rtol=1e-6, atol=1e-7)
+    assert np.allclose(A(oracle.ACT_SILU, 1, lim), np.minimum(g64 * expit(g64), lim) * uc, rtol=1e-6, atol=1e-7)
+    assert np.allclose(A(oracle.ACT_RELU2, 1, lim), np.minimum(np.maximum(g64, 0) ** 2, lim) * uc, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("act,gated,limit", [(1, 1, 0.0), (2, 1, 0.0), (3, 1, 0.0), (3, 1, 7.0), (0, 1, 2.0), (0, 0, 0.0)])
+def test_expert_activation_vs_fp64_model(oracle, act, gated, limit):
+    """The whole expert with each activation against the fp64 model of the mathematics (activation from scipy)."""
+    from scipy.special import expit
+    rng = np.random.default_rng(31 + act)
+    H, I = 256, 128
+    ex = make_expert(oracle, rng, H, I)
+    x = rng.standard_normal(H).astype(np.float16)
+    y, g, u, a = oracle.expert_forward(ex, H, I, x, act=act, gated=bool(gated), limit=limit)
+    Hm = _hm()
+    blk = lambda v: (v.reshape(-1, 128) @ Hm).reshape(-1)
+
+    def lin(m, v):
+        k, n = ((H, I), (H, I), (I, H))[m]
+        W = oracle.np_dequant(ex["tr"][m], ex["fmt"][m], k, n).astype(np.float64)
+        return blk(blk(v * ex["suh"][m].astype(np.float64)) @ W) * ex["svh"][m].astype(np.float64)
+    g64, u64 = lin(0, x.astype(np.float64)), lin(1, x.astype(np.float64))
+    if act == 3:
+        if limit:
+            g64, u64 = np.minimum(g64, limit), np.clip(u64, -limit, limit)
+        av = (u64 + 1) * g64 * expit(1.702 * g64)
+    else:
+        if not gated:
+            xv = np.maximum(u64, 0)
+        elif act == 0:
+            xv = g64 * expit(g64)
+        elif act == 1:
+            xv = 0.5 * g64 * (1 + np.tanh(0.797884560803 * (g64 + 0.044715 * g64 ** 3)))
+        else:
+            xv = np.maximum(g64, 0) ** 2
+        if limit:
+            u64, xv = np.clip(u64, -limit, limit), np.minimum(xv, limit)
+        av = xv * u64
+    want = lin(2, av)
+    assert rel(y, want) < 3e-3 and np.abs(y - want).max() < 2e-2
