@@ -85,28 +85,52 @@ __device__ __forceinline__ uint16_t f2h_r(float v)
     return f2h(v);
 }
 
-// Codebook hash of one 16-bit state (only the low 16 bits of `st` are read; the bits above may hold anything):
+// Codebook weights of eight 16-bit states (only the low 16 bits of each state are read; the bits above may hold
+// anything), packed in pairs: w[q] = (weight of st[2q + 1]) << 16 | weight of st[2q]. Per state:
 //   x = st * MUL1 mod 2^32 = st * 0xD12D + ((st * 0x83DC mod 2^16) << 16)
-// in two full-rate VALU ops (v_pk_mul_lo_u16 writes the high product into the high half, v_mad_u32_u16 reads the low
-// halves).
-__device__ __forceinline__ uint32_t cb_hash(uint32_t st)
+//     v_pk_mul_lo_u16 (op_sel_hi [0, 1]: the high product of the low half lands in the high half, the low one is 0),
+//     then v_mad_u32_u16 (reads the low halves);
+//   1024 + bytesum(x) as fp16 bits: v_sad_u8 adds the bytes of x_a to 0x64006400, v_sad_hi_u8 adds those of x_b into
+//     the high half (a sum < 1024 never carries out of its half);
+//   w = RN16(fma(1024 + s, KINV, KBIAS)) for both halves with one v_pk_fma_f16.
+// One asm block: no instruction in it reads a register that a packed instruction with a high-half op_sel wrote, and the
+// one wait state the compiler adds after an inline-asm block is paid once per eight weights.
+__device__ __forceinline__ void cb_oct(const uint32_t (&st)[8], uint32_t (&w)[4])
 {
-    uint32_t t, x;
-    asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel_hi:[0,1]" : "=v"(t) : "v"(st), "s"(MUL1_HI_SHL16));
-    asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(st), "s"(MUL1_LO), "v"(t));
-    return x;
-}
-
-// Two hashes -> two fp16 codebook weights RN16(fma(1024 + bytesum, KINV, KBIAS)) packed (lo = a, hi = b):
-// v_sad_u8 adds the bytes of xa to 0x64006400, v_sad_hi_u8 adds the bytes of xb shifted into the high half, so the
-// register holds the fp16 bits of 1024 + s_a and 1024 + s_b (s < 1024 never carries out of its half); one v_pk_fma_f16
-// then applies the affine map with a single rounding per weight.
-__device__ __forceinline__ f16x2 cb_pair(uint32_t xa, uint32_t xb)
-{
-    const uint32_t r = __builtin_amdgcn_sad_hi_u8(xb, 0u, __builtin_amdgcn_sad_u8(xa, 0u, (F16_1024 << 16) | F16_1024));
-    const f16x2 kinv = __builtin_bit_cast(f16x2, (KINV_BITS << 16) | KINV_BITS);
-    const f16x2 kbias = __builtin_bit_cast(f16x2, (KBIAS_BITS << 16) | KBIAS_BITS);
-    return __builtin_elementwise_fma(__builtin_bit_cast(f16x2, r), kinv, kbias);
+    uint32_t t[8];
+    asm("v_pk_mul_lo_u16 %4, %12, %20 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %5, %13, %20 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %6, %14, %20 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %7, %15, %20 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %8, %16, %20 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %9, %17, %20 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %10, %18, %20 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %11, %19, %20 op_sel_hi:[0,1]\n\t"
+        "v_mad_u32_u16 %4, %12, %21, %4\n\t"
+        "v_mad_u32_u16 %5, %13, %21, %5\n\t"
+        "v_mad_u32_u16 %6, %14, %21, %6\n\t"
+        "v_mad_u32_u16 %7, %15, %21, %7\n\t"
+        "v_mad_u32_u16 %8, %16, %21, %8\n\t"
+        "v_mad_u32_u16 %9, %17, %21, %9\n\t"
+        "v_mad_u32_u16 %10, %18, %21, %10\n\t"
+        "v_mad_u32_u16 %11, %19, %21, %11\n\t"
+        "v_sad_u8 %0, %4, 0, %22\n\t"
+        "v_sad_u8 %1, %6, 0, %22\n\t"
+        "v_sad_u8 %2, %8, 0, %22\n\t"
+        "v_sad_u8 %3, %10, 0, %22\n\t"
+        "v_sad_hi_u8 %0, %5, 0, %0\n\t"
+        "v_sad_hi_u8 %1, %7, 0, %1\n\t"
+        "v_sad_hi_u8 %2, %9, 0, %2\n\t"
+        "v_sad_hi_u8 %3, %11, 0, %3\n\t"
+        "v_pk_fma_f16 %0, %0, %23, %24\n\t"
+        "v_pk_fma_f16 %1, %1, %23, %24\n\t"
+        "v_pk_fma_f16 %2, %2, %23, %24\n\t"
+        "v_pk_fma_f16 %3, %3, %23, %24"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]),
+          "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+        : "v"(st[0]), "v"(st[1]), "v"(st[2]), "v"(st[3]), "v"(st[4]), "v"(st[5]), "v"(st[6]), "v"(st[7]),
+          "s"(MUL1_HI_SHL16), "s"(MUL1_LO), "s"((F16_1024 << 16) | F16_1024), "s"((KINV_BITS << 16) | KINV_BITS),
+          "v"((KBIAS_BITS << 16) | KBIAS_BITS));
 }
 
 // ---- 128-point Hadamard over a wave: lane l holds elements 2l, 2l + 1 --------------------------------------------------

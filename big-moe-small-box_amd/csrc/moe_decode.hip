@@ -39,13 +39,21 @@ __device__ __forceinline__ void strip(const uint32_t (&own)[Fmt<F>::TB / 16], co
 #pragma unroll
         for (int d = 0; d < 8; ++d) X[m][d] = xr[m * xstride + d];
 #pragma unroll
-    for (int jj = 0; jj < 64; jj += 2)
+    for (int j8 = 0; j8 < 64; j8 += 8)
     {
-        const f16x2 w2 = cb_pair(cb_hash(win_state(prev, own, tab.q[jj])), cb_hash(win_state(prev, own, tab.q[jj + 1])));
-        const int cidx = strip_cidx(jj), dw = strip_dw(jj);
+        uint32_t st[8], w[4];
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
-            acc[cidx][m] = __builtin_amdgcn_fdot2(w2, __builtin_bit_cast(f16x2, X[m][dw]), acc[cidx][m], false);
+        for (int q = 0; q < 8; ++q) st[q] = win_state(prev, own, tab.q[j8 + q]);
+        cb_oct(st, w);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const int cidx = strip_cidx(j8 + 2 * q), dw = strip_dw(j8 + 2 * q);
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                acc[cidx][m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w[q]), __builtin_bit_cast(f16x2, X[m][dw]),
+                                                      acc[cidx][m], false);
+        }
     }
 }
 
@@ -194,6 +202,39 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
 // ---- epilogues: 16 lanes per (row or token, 128-column block), 8 consecutive columns per lane -----------------------------
 // UPW work units per wave: 4 (every lane busy) for large launches, 1 (lanes 16-63 idle; four times the waves, so a
 // decode-size launch spreads over more CUs) for small ones.
+// acc[4 v + i] = sum over splits s = 0, 1, ... ks - 1 in that order of p[s * stride + off(v) + i], off = 0, 4, 128, 132
+// (NV = 4: gate 8 | up 8) or 0, 4 (NV = 2). The loads of B splits are issued together before their adds, so a long
+// split list costs one memory latency per B splits instead of one per split.
+template <int NV, int B>
+__device__ __forceinline__ void sum_splits(const float* p, size_t stride, int ks, float (&acc)[NV * 4])
+{
+#pragma unroll
+    for (int i = 0; i < NV * 4; ++i) acc[i] = 0.0f;
+    int s = 0;
+    for (; s + B <= ks; s += B)
+    {
+        f32x4 q[B][NV];
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) q[b][v] = ldg4f(p + (size_t)(s + b) * stride + (v & 1) * 4 + (v >> 1) * 128);
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[b][v][i];
+    }
+    for (; s < ks; ++s)
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+        {
+            const f32x4 q = ldg4f(p + (size_t)s * stride + (v & 1) * 4 + (v >> 1) * 128);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[i];
+        }
+}
+
 template <int UPW>
 __device__ __forceinline__ int ep_unit()
 {
@@ -214,22 +255,11 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const int col = cb * 128 + 8 * j;
+    float gu[16];
+    sum_splits<4, 4>(a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j, (size_t)a.R_max * a.NB * 256, a.KS_gu, gu);
     float g[8], v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) { g[i] = 0.0f; v[i] = 0.0f; }
-    for (int s = 0; s < a.KS_gu; ++s)
-    {
-        const float* p = a.part_gu + (((size_t)s * a.R_max + r) * a.NB + cb) * 256 + 8 * j;
-        const f32x4 g0 = ldg4f(p), g1 = ldg4f(p + 4), u0 = ldg4f(p + 128), u1 = ldg4f(p + 132);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            g[i] = g[i] + g0[i];
-            g[i + 4] = g[i + 4] + g1[i];
-            v[i] = v[i] + u0[i];
-            v[i + 4] = v[i + 4] + u1[i];
-        }
-    }
+    for (int i = 0; i < 8; ++i) { g[i] = gu[i]; v[i] = gu[8 + i]; }
 #pragma unroll
     for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(g[i])); v[i] = h2f(f2h_r(v[i])); }
     had128_x8(g);
@@ -257,19 +287,7 @@ __device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float 
     const int j = threadIdx.x & 15;
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = 0.0f;
-    for (int s = 0; s < a.KS_dn; ++s)
-    {
-        const float* p = a.part_dn + (((size_t)s * a.R_max + r) * a.NBH + cb) * 128 + 8 * j;
-        const f32x4 d0 = ldg4f(p), d1 = ldg4f(p + 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            y[i] = y[i] + d0[i];
-            y[i + 4] = y[i + 4] + d1[i];
-        }
-    }
+    sum_splits<2, 8>(a.part_dn + ((size_t)r * a.NBH + cb) * 128 + 8 * j, (size_t)a.R_max * a.NBH * 128, a.KS_dn, y);
     had128_x8(y);
     float sv[8];
     unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 8 * j), sv);

@@ -100,10 +100,14 @@ __device__ __forceinline__ void decode_half(const uint32_t (&own)[Fmt<F>::TB / 1
     const uint32_t prev = __builtin_amdgcn_mov_dpp(own[NW - 1], 0x93, 0xf, 0xf, false);
     uint32_t fr[2][8];
 #pragma unroll
-    for (int jj = 32 * HALF; jj < 32 * HALF + 32; jj += 2)
+    for (int j8 = 32 * HALF; j8 < 32 * HALF + 32; j8 += 8)
     {
-        const f16x2 w2 = cb_pair(cb_hash(win_state(prev, own, tab.q[jj])), cb_hash(win_state(prev, own, tab.q[jj + 1])));
-        fr[strip_cidx(jj) >> 1][strip_dw(jj)] = __builtin_bit_cast(uint32_t, w2);
+        uint32_t st[8], w[4];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st[q] = win_state(prev, own, tab.q[j8 + q]);
+        cb_oct(st, w);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) fr[strip_cidx(j8 + 2 * q) >> 1][strip_dw(j8 + 2 * q)] = w[q];
     }
 #pragma unroll
     for (int ci = 0; ci < 2; ++ci)
