@@ -59,6 +59,8 @@ SIGNATURES = {
     "bmx_groups_max": (_I, [_I, _I, _I, _I, _I]),
     "bmx_dispatch_workspace": (_SZ, [_I, _I, _I]),
     "bmx_dispatch": (_I, [_P, _I, _I, _I, _I64, _I, _I, ctypes.POINTER(Routes), _P, _SZ, _P]),
+    "bmx_route_dispatch": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _I64, _I, _I, _P, _P,
+                                ctypes.POINTER(Routes), _P]),
     "bmx_moe_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_forward": (_I, [ctypes.POINTER(MoeDesc), _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
     "bmx_rows_per_group": (_I, [_I, _I, _I]),

@@ -88,6 +88,22 @@ def dispatch(sel, E, first=0, shared=False, rows_per_group=8):
     return r
 
 
+def route_dispatch(logits, topk, bias=None, n_group=1, topk_group=1, score=L.SCORE_SIGMOID, renorm=True, scale=1.0,
+                   first=0, shared=False, rows_per_group=1):
+    """Router + dispatch in one launch (T * topk <= 256) -> (sel, w, RoutesBuf)."""
+    _need(logits, torch.float16, "logits")
+    T, E = logits.shape
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+    sel = torch.empty((T, topk), dtype=torch.int64, device=logits.device)
+    w = torch.empty((T, topk), dtype=torch.float16, device=logits.device)
+    r = RoutesBuf(T, topk, E, shared, rows_per_group, logits.device)
+    check(lib().bmx_route_dispatch(_ptr(logits), _ptr(bias), T, E, topk, n_group, topk_group, score, int(renorm),
+                                   float(scale), int(first), int(shared), rows_per_group, _ptr(sel), _ptr(w),
+                                   ctypes.byref(r.struct), _stream()), "bmx_route_dispatch")
+    return sel, w, r
+
+
 def moe_forward(desc, x, sel, w, path=L.PATH_AUTO, workspace=None):
     """Layer output fp32 [T, H] for x fp16 [T, H] and routes (sel, w)."""
     _need(x, torch.float16, "x"); _need(sel, torch.int64, "sel"); _need(w, torch.float16, "w")

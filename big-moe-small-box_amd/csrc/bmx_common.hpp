@@ -133,6 +133,15 @@ __device__ __forceinline__ void cb_oct(const uint32_t (&st)[8], uint32_t (&w)[4]
           "v"((KBIAS_BITS << 16) | KBIAS_BITS));
 }
 
+// Workgroup barrier that orders LDS only: waits for the wave's LDS operations, not for its global loads and stores
+// (__syncthreads waits for those too). For barriers whose data is exchanged through LDS alone.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---- 128-point Hadamard over a wave: lane l holds elements 2l, 2l + 1 --------------------------------------------------
 // Sylvester order, stages of span 1, 2, 4, ..., 64; at each stage the lower element of a pair becomes a + b and the upper
 // one a - b (engine/kernels/nv2/ft_core.h:90-95; the cross-lane butterfly of x16_dev.cu:31-129 adds the same pairs in

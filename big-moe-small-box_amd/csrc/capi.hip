@@ -163,6 +163,18 @@ int bmx_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int 
                            static_cast<hipStream_t>(stream));
 }
 
+int bmx_route_dispatch(const void* logits_fp16, const float* bias, int T, int E, int topk, int n_group, int topk_group,
+                       int score_fn, int renorm, float scale, int64_t first, int shared, int rows_per_group, int64_t* sel,
+                       void* w_fp16, const bmx_routes* out, bmx_stream_t stream)
+{
+    if (!out || rows_per_group <= 0) return set_error(BMX_ERR_ARG, "bmx_route_dispatch: null routes or rows_per_group");
+    if (!route_dispatch_small_fits(T, E, topk))
+        return set_error(BMX_ERR_ARG, "bmx_route_dispatch: T * topk = %ld picks exceeds 256 (use bmx_router_topk + "
+                         "bmx_dispatch)", (long)T * topk);
+    return launch_route_dispatch_small(logits_fp16, bias, T, E, topk, n_group, topk_group, score_fn, renorm, scale, first,
+                                       sel, w_fp16, shared, rows_per_group, out, static_cast<hipStream_t>(stream));
+}
+
 int bmx_rows_per_group(int T, int topk, int path)
 {
     const int p = resolve_path(path, T, topk);

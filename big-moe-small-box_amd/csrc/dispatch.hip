@@ -138,7 +138,7 @@ __global__ __launch_bounds__(DP_THREADS) void k_dispatch_single(DpArgs a)
     {
         if (c >= nchunk) break;
         for (int i = tid; i < DP_WAVES * DP_MAXNE; i += DP_THREADS) whist[i] = 0;
-        __syncthreads();
+        lds_barrier();
         const int p = c * DP_THREADS + tid;
         int e = -1;
         if (p < n)
@@ -147,17 +147,17 @@ __global__ __launch_bounds__(DP_THREADS) void k_dispatch_single(DpArgs a)
             e = (g >= 0 && g < E) ? (int)g : -1;
         }
         const int rk = wave_rank(e, e >= 0, whist + wave * DP_MAXNE);
-        __syncthreads();
+        lds_barrier();
         prefix_waves(whist, E, base, true);
-        __syncthreads();
+        lds_barrier();
         myrank[c] = e >= 0 ? whist[wave * DP_MAXNE + e] + rk : -1;
         mye[c] = e;
-        __syncthreads();
+        lds_barrier();
     }
     if (a.shared && tid == 0) base[E] = a.T;
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) scan_wave(base, off, NE);
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < NE; e += DP_THREADS) { a.r.counts[e] = base[e]; a.r.offsets[e] = off[e]; }
     if (tid == 0) a.r.offsets[NE] = off[NE];
     for (int c = 0; c < nchunk; ++c)
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(DP_THREADS) void k_dispatch_blocks(DpArgs a)
     for (int e = tid; e < E; e += DP_THREADS) base[e] = 0;
     if (blockIdx.x == 0)
         for (int i = tid; i < a.zero_count; i += DP_THREADS) a.zero_ptr[i] = 0;
-    __syncthreads();
+    lds_barrier();
     const int p = blockIdx.x * DP_THREADS + tid;
     int e = -1;
     if (p < n)
@@ -206,9 +206,9 @@ __global__ __launch_bounds__(DP_THREADS) void k_dispatch_blocks(DpArgs a)
         e = (g >= 0 && g < E) ? (int)g : -1;
     }
     const int rk = wave_rank(e, e >= 0, whist + wave * DP_MAXNE);
-    __syncthreads();
+    lds_barrier();
     prefix_waves(whist, E, base, false);
-    __syncthreads();
+    lds_barrier();
     if (p < n) a.rank[p] = e >= 0 ? whist[wave * DP_MAXNE + e] + rk : -1;
     for (int x = tid; x < E; x += DP_THREADS) a.blk_hist[(size_t)blockIdx.x * E + x] = base[x];
 }
@@ -233,9 +233,9 @@ __global__ __launch_bounds__(DP_THREADS) void k_dispatch_scan(DpArgs a, int nblk
         cnt[e] = run;
     }
     if (a.shared && tid == 0) cnt[E] = a.T;
-    __syncthreads();
+    lds_barrier();
     if (tid < 64) scan_wave(cnt, off, NE);
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < NE; e += DP_THREADS) { a.r.counts[e] = cnt[e]; a.r.offsets[e] = off[e]; }
     if (tid == 0) a.r.offsets[NE] = off[NE];
     if (a.shared)

@@ -181,12 +181,12 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
         const int mat = i / ((mr - nr) * XW), rem = i % ((mr - nr) * XW);
         xs[(mat * MX + nr) * XW + rem] = 0u;
     }
-    __syncthreads();
+    lds_barrier();
     if (mr == 1) gemv_rows<1, MX, NM>(a, ex, cb, k0, KR, N, xs, red);
     else if (mr == 2) { if constexpr (MX >= 2) gemv_rows<2, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
     else if (mr == 4) { if constexpr (MX >= 4) gemv_rows<4, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
     else { if constexpr (MX >= 8) gemv_rows<8, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
-    __syncthreads();
+    lds_barrier();
     // the four waves in order, then one partial per (split, row, block)
     float* part = (NM == 2 ? a.part_gu : a.part_dn) + (((size_t)ks * a.R_max + r0) * NB + cb) * (NM * 128);
     for (int i = threadIdx.x; i < NM * nr * 128; i += GV_THREADS)
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
         for (int i = 0; i < 8; ++i) ys[k][8 * j + i] = y[i];
         if (j == 0) live[k] = 1;
     }
-    __syncthreads();
+    lds_barrier();
     if (k0) return;
     float o[8];
 #pragma unroll

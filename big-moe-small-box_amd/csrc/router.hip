@@ -27,37 +27,71 @@ __device__ __forceinline__ uint32_t okey(float v)
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// wave-wide max / min of a uint32, uniform result: xor 1 and xor 2 within quads, mirrors within half-rows and rows
-// (each lane then holds its row's result), then the four rows on the scalar unit
+// wave-wide max of a uint32 (softmax's max logit): DPP within rows, then row broadcasts; lane 63 holds the result
 __device__ __forceinline__ uint32_t wave_umax(uint32_t k)
 {
     k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0xB1, 0xf, 0xf, false));
     k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x4E, 0xf, 0xf, false));
     k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x141, 0xf, 0xf, false));
     k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x140, 0xf, 0xf, false));
-    const uint32_t a = __builtin_amdgcn_readlane(k, 0), b = __builtin_amdgcn_readlane(k, 16);
-    const uint32_t c = __builtin_amdgcn_readlane(k, 32), d = __builtin_amdgcn_readlane(k, 48);
-    return max(max(a, b), max(c, d));
+    k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x142, 0xa, 0xf, false));
+    k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x143, 0xc, 0xf, false));
+    return __builtin_amdgcn_readlane(k, 63);
 }
 
-__device__ __forceinline__ uint32_t wave_umin(uint32_t k)
+// Selection key of a candidate: the order-preserving key of its value above the complement of its index, so the
+// largest key is the larger value and, among equal values, the lower index. 0 = no candidate.
+__device__ __forceinline__ uint64_t sel_key(float v, int e)
 {
-    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0xB1, 0xf, 0xf, false));
-    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x4E, 0xf, 0xf, false));
-    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x141, 0xf, 0xf, false));
-    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x140, 0xf, 0xf, false));
-    const uint32_t a = __builtin_amdgcn_readlane(k, 0), b = __builtin_amdgcn_readlane(k, 16);
-    const uint32_t c = __builtin_amdgcn_readlane(k, 32), d = __builtin_amdgcn_readlane(k, 48);
-    return min(min(a, b), min(c, d));
+    return ((uint64_t)okey(v) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+}
+__device__ __forceinline__ int key_index(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void kmax_dpp(uint32_t& hi, uint32_t& lo)
+{
+    const uint32_t ph = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, ROW_MASK, 0xf, false);
+    const uint32_t pl = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, ROW_MASK, 0xf, false);
+    const bool take = ph > hi || (ph == hi && pl > lo);
+    hi = take ? ph : hi;
+    lo = take ? pl : lo;
 }
 
-// index of the best of (lane candidate v at index i; i < 0 = none) over the wave, -1 if none
-__device__ __forceinline__ int wave_argbest(float v, int i)
+// wave-wide max of a 64-bit key, uniform result: xor 1 and xor 2 within quads, mirrors within half-rows and rows, then
+// row 0 into row 1 and row 2 into row 3 (row_bcast:15), rows 0-1 into rows 2-3 (row_bcast:31): lane 63 holds the max
+__device__ __forceinline__ uint64_t wave_kmax(uint64_t k)
 {
-    const uint32_t k = i >= 0 ? okey(v) : 0u;
-    const uint32_t m = wave_umax(k);
-    if (m == 0u) return -1;
-    return (int)wave_umin((i >= 0 && k == m) ? (uint32_t)i : 0xffffffffu);
+    uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
+    kmax_dpp<0xB1, 0xf>(hi, lo);
+    kmax_dpp<0x4E, 0xf>(hi, lo);
+    kmax_dpp<0x141, 0xf>(hi, lo);
+    kmax_dpp<0x140, 0xf>(hi, lo);
+    kmax_dpp<0x142, 0xa>(hi, lo);
+    kmax_dpp<0x143, 0xc>(hi, lo);
+    return ((uint64_t)__builtin_amdgcn_readlane(hi, 63) << 32) | __builtin_amdgcn_readlane(lo, 63);
+}
+
+// four independent wave-wide maxima, interleaved step by step (their latencies overlap)
+__device__ __forceinline__ void wave_kmax4(uint64_t (&k)[4])
+{
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { hi[i] = (uint32_t)(k[i] >> 32); lo[i] = (uint32_t)k[i]; }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kmax_dpp<0xB1, 0xf>(hi[i], lo[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kmax_dpp<0x4E, 0xf>(hi[i], lo[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kmax_dpp<0x141, 0xf>(hi[i], lo[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kmax_dpp<0x140, 0xf>(hi[i], lo[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kmax_dpp<0x142, 0xa>(hi[i], lo[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kmax_dpp<0x143, 0xc>(hi[i], lo[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        k[i] = ((uint64_t)__builtin_amdgcn_readlane(hi[i], 63) << 32) | __builtin_amdgcn_readlane(lo[i], 63);
 }
 
 struct RouterArgs {
@@ -71,19 +105,20 @@ struct RouterArgs {
 };
 
 // Route token t with the calling wave. Writes sel / w of the token; returns the pick of slot `lane` (lanes < topk)
-// as a local expert id (-1 otherwise).
+// as a local expert id (-1 otherwise). Every selection is a wave-wide max of 64-bit keys (value, then lower index).
 template <int J>
 __device__ int route_token_wave(const RouterArgs& a, int t)
 {
     const int lane = threadIdx.x & 63, E = a.E;
     const uint16_t* lg = a.logits + (size_t)t * E;
-    float ch[J], sc[J];
+    float ch[J], sc[J], bias[J];
     float mx = -__builtin_huge_valf();
 #pragma unroll
     for (int j = 0; j < J; ++j)
     {
         const int e = lane + 64 * j;
         ch[j] = e < E ? canon(h2f(lg[e])) : -__builtin_huge_valf();
+        bias[j] = (a.bias && e < E) ? a.bias[e] : 0.0f;
         mx = fmaxf(mx, ch[j]);
     }
     if (a.score_fn == BMX_SCORE_SOFTMAX)
@@ -99,78 +134,116 @@ __device__ int route_token_wave(const RouterArgs& a, int t)
         else
         {
             sc[j] = e < E ? sigmoid_fixed(ch[j]) : 0.0f;
-            if (e < E) ch[j] = canon(a.bias ? __fadd_rn(sc[j], a.bias[e]) : sc[j]);
+            if (e < E) ch[j] = canon(a.bias ? __fadd_rn(sc[j], bias[j]) : sc[j]);
         }
     }
-    // group limit
-    uint64_t gok = ~0ull;
+    uint64_t key[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+    {
+        const int e = lane + 64 * j;
+        key[j] = e < E ? sel_key(ch[j], e) : 0ull;
+    }
+    // group limit: a group's score is the sum of its two best choices; the topk_group best groups stay eligible
     const int G = a.G, gs = E / G;
     if (G > 1)
     {
         float mygsc = 0.0f;                      // lane g holds group g's score
-        for (int g = 0; g < G; ++g)
+        for (int g0 = 0; g0 < G; g0 += 4)
         {
-            float v1 = 0.0f, v2 = 0.0f;
-            int i1 = -1, i2 = -1;
+            // best and second-best key of groups g0 .. g0 + 3 (groups past G are empty)
+            uint64_t k1[4], k2[4];
 #pragma unroll
-            for (int j = 0; j < J; ++j)
+            for (int i = 0; i < 4; ++i)
             {
-                const int e = lane + 64 * j;
-                if (e >= g * gs && e < (g + 1) * gs && (i1 < 0 || better(ch[j], e, v1, i1))) { v1 = ch[j]; i1 = e; }
-            }
-            const int b1 = wave_argbest(v1, i1);
+                const int g = g0 + i;
+                uint64_t b = 0;
 #pragma unroll
-            for (int j = 0; j < J; ++j)
-            {
-                const int e = lane + 64 * j;
-                if (e >= g * gs && e < (g + 1) * gs && e != b1 && (i2 < 0 || better(ch[j], e, v2, i2))) { v2 = ch[j]; i2 = e; }
+                for (int j = 0; j < J; ++j)
+                {
+                    const int e = lane + 64 * j;
+                    const uint64_t k = (g < G && e >= g * gs && e < (g + 1) * gs) ? key[j] : 0ull;
+                    b = k > b ? k : b;
+                }
+                k1[i] = b;
             }
-            const int b2 = wave_argbest(v2, i2);
-            float t1 = 0.0f, t2 = 0.0f;
+            wave_kmax4(k1);
 #pragma unroll
-            for (int j = 0; j < J; ++j)
+            for (int i = 0; i < 4; ++i)
             {
-                t1 = (lane + 64 * j == b1) ? ch[j] : t1;
-                t2 = (lane + 64 * j == b2) ? ch[j] : t2;
+                const int g = g0 + i, b1 = key_index(k1[i]);
+                uint64_t b = 0;
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                {
+                    const int e = lane + 64 * j;
+                    const uint64_t k = (g < G && e >= g * gs && e < (g + 1) * gs && e != b1) ? key[j] : 0ull;
+                    b = k > b ? k : b;
+                }
+                k2[i] = b;
             }
-            t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t1), b1 & 63));
-            t2 = b2 >= 0 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t2), b2 & 63)) : 0.0f;
-            if (lane == g) mygsc = canon(b2 >= 0 ? __fadd_rn(t1, t2) : t1);
+            wave_kmax4(k2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const int g = g0 + i;
+                if (g >= G) break;
+                const int b1 = key_index(k1[i]);
+                float t1 = 0.0f, t2 = 0.0f;
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                {
+                    t1 = (lane + 64 * j == b1) ? ch[j] : t1;
+                    t2 = (k2[i] && lane + 64 * j == key_index(k2[i])) ? ch[j] : t2;
+                }
+                t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t1), b1 & 63));
+                if (k2[i])
+                    t2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t2), key_index(k2[i]) & 63));
+                if (lane == g) mygsc = canon(k2[i] ? __fadd_rn(t1, t2) : t1);
+            }
         }
-        gok = 0;
+        uint64_t gk = lane < G ? sel_key(mygsc, lane) : 0ull, gok = 0;
         for (int r = 0; r < a.TG && r < G; ++r)
         {
-            const int bg = wave_argbest(mygsc, (lane < G && !((gok >> lane) & 1ull)) ? lane : -1);
+            const int bg = key_index(wave_kmax(gk));
             gok |= 1ull << bg;
+            if (lane == bg) gk = 0;
         }
-    }
-    // top-k: each lane keeps its best remaining candidate; the winner's lane drops it and rescans
-    uint32_t taken = 0;
-    auto local_best = [&](float& bv, int& bi, float& bs) {
-        bi = -1; bv = 0.0f; bs = 0.0f;
 #pragma unroll
         for (int j = 0; j < J; ++j)
         {
             const int e = lane + 64 * j;
-            const bool ok = e < E && !((taken >> j) & 1u) && (G <= 1 || ((gok >> (e / gs)) & 1ull));
-            if (ok && (bi < 0 || better(ch[j], e, bv, bi))) { bv = ch[j]; bi = e; bs = sc[j]; }
+            if (e < E && !((gok >> (e / gs)) & 1ull)) key[j] = 0;
+        }
+    }
+    // top-k: each lane offers its best remaining key; the winner's lane clears it and offers its next
+    auto lane_best = [&](uint64_t& bk, float& bs) {
+        bk = 0;
+        bs = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+        {
+            const bool tk = key[j] > bk;
+            bk = tk ? key[j] : bk;
+            bs = tk ? sc[j] : bs;
         }
     };
-    float bv, bs;
-    int bi;
-    local_best(bv, bi, bs);
+    uint64_t bk;
+    float bs;
+    lane_best(bk, bs);
     int mypick = -1;
     float vsum = 0.0f, myscore = 0.0f;
     for (int k = 0; k < a.topk; ++k)
     {
-        const int win = wave_argbest(bv, bi);
+        const int win = key_index(wave_kmax(bk));
         const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bs), win & 63));
         vsum = __fadd_rn(vsum, ws);
         if (lane == k) { mypick = win; myscore = ws; }
         if ((win & 63) == lane)
         {
-            taken |= 1u << (win >> 6);
-            local_best(bv, bi, bs);
+#pragma unroll
+            for (int j = 0; j < J; ++j) key[j] = (j == (win >> 6)) ? 0ull : key[j];
+            lane_best(bk, bs);
         }
     }
     float den = 1.0f;
@@ -208,6 +281,91 @@ struct SmallDispatch {
     bmx_routes r;
 };
 
+// Counting sort of at most 64 picks by one wave, without barriers: pick p in lane p; per-expert counts by LDS atomics,
+// offsets / group bases / unique ranks by one wave-wide scan over the experts, each pick's rank among its expert's
+// picks by readlane broadcasts. Same output as the workgroup version below.
+__device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, const SmallDispatch& d, int* scnt, int* soff,
+                              int* sgo, int* sui)
+{
+    const int lane = threadIdx.x & 63, NE = E + (d.shared ? 1 : 0), rpg = d.rpg;
+    const int e = lane < n ? pe[lane] : -1;
+    for (int x = lane; x < NE; x += 64) scnt[x] = 0;
+    if (lane < n && e >= 0) atomicAdd(&scnt[e], 1);
+    if (d.shared && lane == 0) scnt[E] = T;
+    // each lane scans a run of C consecutive experts; run totals are scanned across the wave
+    const int C = (NE + 63) / 64, x0 = lane * C;
+    int tc = 0, tg = 0, tu = 0;
+    for (int i = 0; i < C; ++i)
+    {
+        const int x = x0 + i;
+        const int c = x < NE ? scnt[x] : 0;
+        tc += c;
+        tg += (c + rpg - 1) / rpg;
+        tu += c > 0;
+    }
+    int ic = tc, ig = tg, iu = tu;                 // inclusive scans
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1)
+    {
+        const int pc = __shfl_up(ic, o), pg = __shfl_up(ig, o), pu = __shfl_up(iu, o);
+        if (lane >= o) { ic += pc; ig += pg; iu += pu; }
+    }
+    int bc = ic - tc, bg = ig - tg, bu = iu - tu;  // exclusive
+    for (int i = 0; i < C; ++i)
+    {
+        const int x = x0 + i;
+        if (x >= NE) break;
+        const int c = scnt[x];
+        soff[x] = bc;
+        sgo[x] = bg;
+        sui[x] = bu;
+        d.r.counts[x] = c;
+        d.r.offsets[x] = bc;
+        if (c > 0)
+        {
+            d.r.uexp[bu] = x;
+            for (int q = 0; q * rpg < c; ++q)
+            {
+                d.r.groups[3 * (bg + q) + 0] = x;
+                d.r.groups[3 * (bg + q) + 1] = bc + q * rpg;
+                d.r.groups[3 * (bg + q) + 2] = min(rpg, c - q * rpg);
+            }
+        }
+        bc += c;
+        bg += (c + rpg - 1) / rpg;
+        bu += c > 0;
+    }
+    if (lane == 63)
+    {
+        d.r.offsets[NE] = ic;
+        *d.r.nuniq = iu;
+        *d.r.ngroups = ig;
+    }
+    // rows of the routed picks: stable by (expert, pick)
+    int rank = 0;
+    for (int q = 0; q < n; ++q) rank += (__builtin_amdgcn_readlane(e, q) == e) && q < lane;
+    if (lane < n)
+    {
+        if (e < 0) d.r.inv[lane] = -1;
+        else
+        {
+            const int row = soff[e] + rank;
+            d.r.inv[lane] = row;
+            d.r.row_token[row] = lane / topk;
+            d.r.row_slot[row] = lane % topk;
+            d.r.row_expert[row] = e;
+        }
+    }
+    if (d.shared)
+        for (int t = lane; t < T; t += 64)
+        {
+            const int row = soff[E] + t;
+            d.r.row_token[row] = t;
+            d.r.row_slot[row] = -1;
+            d.r.row_expert[row] = E;
+        }
+}
+
 template <int J>
 __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs a, SmallDispatch d)
 {
@@ -219,7 +377,14 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
         const int pk = route_token_wave<J>(a, t);
         if (lane < a.topk) pe[t * a.topk + lane] = pk;
     }
-    __syncthreads();
+    if (n <= 64)
+    {
+        __shared__ int soff[RT_MAXE + 1], sgo[RT_MAXE + 1], sui[RT_MAXE + 1];
+        if (a.T > 1) lds_barrier();          // one token: wave 0 routed it and reads its own LDS writes in order
+        if (tid < 64) dispatch_wave(pe, n, E, a.T, a.topk, d, cnt, soff, sgo, sui);
+        return;
+    }
+    lds_barrier();
     const int NE = E + (d.shared ? 1 : 0);
     __shared__ int4 pe4[SM_MAXN / 4];        // the picks again, padded with -1 to a multiple of 4
     __shared__ int4 gc4[SM_MAXN / 4];        // per pick: groups of its expert if it is the expert's first pick, else 0
@@ -227,7 +392,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
     int* pev = reinterpret_cast<int*>(pe4);
     int* gcv = reinterpret_cast<int*>(gc4);
     for (int p = tid; p < 4 * n4; p += blockDim.x) pev[p] = p < n ? pe[p] : -1;
-    __syncthreads();
+    lds_barrier();
     // counts and offsets per expert (the shared segment last)
     int nvalid = 0;
     for (int q = 0; q < n4; ++q)
@@ -251,7 +416,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
         d.r.offsets[e] = below;
         if (e == NE - 1) d.r.offsets[NE] = below + c;
     }
-    __syncthreads();
+    lds_barrier();
     for (int p = tid; p < 4 * n4; p += blockDim.x)
     {
         const int e = pev[p];
@@ -259,7 +424,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
         for (int q = 0; q < p && first; ++q) first = pev[q] != e;
         gcv[p] = first ? (cnt[e] + d.rpg - 1) / d.rpg : 0;
     }
-    __syncthreads();
+    lds_barrier();
     int nu_r = 0, ng_r = 0;
     for (int q = 0; q < n4; ++q)
     {
@@ -356,11 +521,17 @@ int launch_router(const void* logits, const float* bias, int T, int E, int topk,
     const RouterArgs a = router_args(logits, bias, T, E, topk, n_group, topk_group, score_fn, renorm, scale, first, sel, w);
     const dim3 grid((unsigned)((T + RT_WAVES - 1) / RT_WAVES)), block(RT_THREADS);
     const int J = (E + 63) / 64;
-    if (J <= 1) hipLaunchKernelGGL(k_router<1>, grid, block, 0, s, a);
-    else if (J <= 2) hipLaunchKernelGGL(k_router<2>, grid, block, 0, s, a);
-    else if (J <= 4) hipLaunchKernelGGL(k_router<4>, grid, block, 0, s, a);
-    else if (J <= 8) hipLaunchKernelGGL(k_router<8>, grid, block, 0, s, a);
-    else hipLaunchKernelGGL(k_router<16>, grid, block, 0, s, a);
+    switch (J)
+    {
+        case 1: hipLaunchKernelGGL(k_router<1>, grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL(k_router<2>, grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL(k_router<3>, grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL(k_router<4>, grid, block, 0, s, a); break;
+        case 5: hipLaunchKernelGGL(k_router<5>, grid, block, 0, s, a); break;
+        case 6: hipLaunchKernelGGL(k_router<6>, grid, block, 0, s, a); break;
+        case 7: case 8: hipLaunchKernelGGL(k_router<8>, grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL(k_router<16>, grid, block, 0, s, a); break;
+    }
     return check_launch("bmx_router_topk");
 }
 
@@ -380,11 +551,17 @@ int launch_route_dispatch_small(const void* logits, const float* bias, int T, in
     d.r = *routes;
     const int J = (E + 63) / 64;
     const dim3 grid(1), block(RT_THREADS);
-    if (J <= 1) hipLaunchKernelGGL(k_route_dispatch_small<1>, grid, block, 0, s, a, d);
-    else if (J <= 2) hipLaunchKernelGGL(k_route_dispatch_small<2>, grid, block, 0, s, a, d);
-    else if (J <= 4) hipLaunchKernelGGL(k_route_dispatch_small<4>, grid, block, 0, s, a, d);
-    else if (J <= 8) hipLaunchKernelGGL(k_route_dispatch_small<8>, grid, block, 0, s, a, d);
-    else hipLaunchKernelGGL(k_route_dispatch_small<16>, grid, block, 0, s, a, d);
+    switch (J)
+    {
+        case 1: hipLaunchKernelGGL(k_route_dispatch_small<1>, grid, block, 0, s, a, d); break;
+        case 2: hipLaunchKernelGGL(k_route_dispatch_small<2>, grid, block, 0, s, a, d); break;
+        case 3: hipLaunchKernelGGL(k_route_dispatch_small<3>, grid, block, 0, s, a, d); break;
+        case 4: hipLaunchKernelGGL(k_route_dispatch_small<4>, grid, block, 0, s, a, d); break;
+        case 5: hipLaunchKernelGGL(k_route_dispatch_small<5>, grid, block, 0, s, a, d); break;
+        case 6: hipLaunchKernelGGL(k_route_dispatch_small<6>, grid, block, 0, s, a, d); break;
+        case 7: case 8: hipLaunchKernelGGL(k_route_dispatch_small<8>, grid, block, 0, s, a, d); break;
+        default: hipLaunchKernelGGL(k_route_dispatch_small<16>, grid, block, 0, s, a, d); break;
+    }
     return check_launch("route + dispatch");
 }
 

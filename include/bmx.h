@@ -118,6 +118,13 @@ size_t bmx_dispatch_workspace(int T, int topk, int E);
 int bmx_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int shared, int rows_per_group,
                  const bmx_routes* out, void* workspace, size_t workspace_bytes, bmx_stream_t stream);
 
+/* Router and dispatch in one launch, for decode-size calls (T * topk <= 256): the same outputs as bmx_router_topk
+ * followed by bmx_dispatch (the reference's nv_pub_k publishes a token's routes in one kernel,
+ * engine/kernels/nv2/nv2_dev.cu:23-95). */
+int bmx_route_dispatch(const void* logits_fp16, const float* bias, int T, int E, int topk, int n_group, int topk_group,
+                       int score_fn, int renorm, float scale, int64_t first, int shared, int rows_per_group, int64_t* sel,
+                       void* w_fp16, const bmx_routes* out, bmx_stream_t stream);
+
 /* ---- layer ----
  * The routed experts of one layer call plus the combine: exllamav3's BC_BlockSparseMLP run_bszN(z, sel, rw) writing
  * experts_cfg.out_bszn (engine/nv2.py:634-635) followed by cpu_split_combine (engine/tiers.py:730-739) and the

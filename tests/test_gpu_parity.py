@@ -138,6 +138,40 @@ def test_dispatch_bitexact(cuda, oracle, T, topk, E, shared, rpg):
     _check_dispatch(r, oracle.dispatch(sel, E, 0, shared), T, topk, E, shared, rpg)
 
 
+RD_CASES = [("c2 T1 shared", "c2 sigmoid+bias", 1, True, 1), ("c2 T8 shared", "c2 sigmoid+bias", 8, True, 8),
+            ("c1 T1", "c1 softmax", 1, False, 1), ("c3 groups T2", "c3 groups", 2, False, 2),
+            ("c3 groups T16", "c3 groups", 16, False, 8), ("c2 T32 shared", "c2 sigmoid+bias", 32, True, 8),
+            ("softmax raw T7", "softmax no renorm", 7, True, 4)]
+
+
+@pytest.mark.parametrize("name,router,T,shared,rpg", RD_CASES, ids=[c[0] for c in RD_CASES])
+def test_route_dispatch_bitexact(cuda, oracle, name, router, T, shared, rpg):
+    """The one-launch router + dispatch (one wave up to 64 picks, a workgroup up to 256) against the oracle's router
+    and counting sort, bit for bit."""
+    import bmx
+    cfg = dict(ROUTERS)[router]
+    rng = np.random.default_rng(100 + T)
+    E, topk = cfg["E"], cfg["topk"]
+    lg = (rng.standard_normal((T, E)) * 2).astype(np.float16)
+    lg[0, :4] = lg[0, 4]                                  # ties
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if cfg["bias"] else None
+    say("route+dispatch", name)
+    sel, w, r = bmx.ops.route_dispatch(torch.from_numpy(lg).to(cuda), topk,
+                                       torch.from_numpy(bias).to(cuda) if bias is not None else None, cfg["n_group"],
+                                       cfg["topk_group"], cfg["score"], cfg["renorm"], cfg["scale"], first=5,
+                                       shared=shared, rows_per_group=rpg)
+    torch.cuda.synchronize()
+    osel, ow = oracle.router(lg, topk, bias, cfg["n_group"], cfg["topk_group"], cfg["score"], cfg["renorm"],
+                             cfg["scale"], first=5)
+    assert np.array_equal(sel.cpu().numpy(), osel)
+    gw = w.cpu().numpy()
+    if cfg["score"] == 0 and not cfg["renorm"]:
+        assert np.allclose(gw.astype(np.float32), ow.astype(np.float32), rtol=2e-3)
+    else:
+        assert np.array_equal(gw.view(np.uint16), ow.view(np.uint16))
+    _check_dispatch(r, oracle.dispatch(osel, E, 5, shared), T, topk, E, shared, rpg)
+
+
 # ---- layer ------------------------------------------------------------------------------------------------------------
 
 def oracle_layer(oracle, tab, x, sel, w, rows):
