@@ -281,6 +281,48 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     *reinterpret_cast<u32x4*>(a.act_rows + (size_t)r * a.I + col) = pack8_r(act);
 }
 
+// Small launches: one wave per (row, 128-column block). Lane group q = lane >> 4 loads splits q, q + 4, ... at once and
+// the four groups' sums are added pairwise ((q0 + q1) + (q2 + q3)), so the k-splits cost one memory latency instead of
+// one per batch; the rest runs as in k_gu_epi (every group computes it, group 0 stores).
+__global__ __launch_bounds__(GV_THREADS) void k_gu_epi_w(GvArgs a)
+{
+    const int u = blockIdx.x * GV_WAVES + (threadIdx.x >> 6), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
+    const int r = u / a.NB, cb = u % a.NB;
+    if (r >= a.R_max) return;
+    const int nrows = a.offsets[a.NE], e = a.row_expert[r];
+    const size_t stride = (size_t)a.R_max * a.NB * 256;
+    const float* p = a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j + (size_t)q * stride;
+    float gu[16];
+    sum_splits<4, 4>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + __shfl_xor(gu[i], 16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + __shfl_xor(gu[i], 32);
+    if (r >= nrows) return;
+    const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
+    const int col = cb * 128 + 8 * j;
+    float g[8], v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(gu[i])); v[i] = h2f(f2h_r(gu[8 + i])); }
+    had128_x8(g);
+    had128_x8(v);
+    float svg[8], svu[8], sud[8];
+    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col), svg);
+    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col), svu);
+    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.suh[2]) + col), sud);
+    float act[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+    {
+        const float gi = (g[i] * R_SCALE) * svg[i], ui = (v[i] * R_SCALE) * svu[i];
+        act[i] = act_gate(a.act, a.gated, gi, ui, a.limit) * sud[i];
+    }
+    had128_x8(act);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) act[i] = act[i] * R_SCALE;
+    if (q == 0) *reinterpret_cast<u32x4*>(a.act_rows + (size_t)r * a.I + col) = pack8_r(act);
+}
+
 // down output of row r, block cb, lane's 8 columns: sum of the splits -> H128 * R * svh
 __device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float (&y)[8])
 {
@@ -455,7 +497,7 @@ int launch_epilogue(const GvArgs& a, int stage, hipStream_t s)
     {
         case BMX_STAGE_ACT:
             if (gu >= EP_SMALL) hipLaunchKernelGGL(k_gu_epi<4>, wgs(gu, 4), dim3(GV_THREADS), 0, s, a);
-            else hipLaunchKernelGGL(k_gu_epi<1>, wgs(gu, 1), dim3(GV_THREADS), 0, s, a);
+            else hipLaunchKernelGGL(k_gu_epi_w, wgs(gu, 1), dim3(GV_THREADS), 0, s, a);
             break;
         case BMX_STAGE_COMBINE:
             if (cmb >= EP_SMALL) hipLaunchKernelGGL(k_dn_combine, wgs(cmb, 4), dim3(GV_THREADS), 0, s, a);

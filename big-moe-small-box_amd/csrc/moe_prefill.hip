@@ -136,20 +136,22 @@ struct PfJob {
     const bmx_expert* ex;
 };
 
-// Every MFMA wave runs all its rows and columns: rows past the group's end hold copies of its last row and a missing
-// second 128-column half holds stale LDS, and neither is stored. (On a small group the MFMAs cost nothing: the step's
-// decode takes longer.)
+// An MFMA wave multiplies the 32-row blocks that hold rows of the group (rows past the group's end inside such a block
+// hold copies of its last row) and all its columns (a missing second 128-column half holds stale LDS); neither padding
+// is stored.
 struct PfFrag {
     f16x8 a[2];      // [row block]
     f16x8 b[4];      // [column block]
 };
 
+// NMB: row blocks of 32 this wave computes (2; 1 when the group's rows end in the wave's first block)
+template <int NMB>
 __device__ __forceinline__ void pf_frag_load(PfFrag& f, const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, int ks)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave & 1, wn = wave >> 1;
     const int slot = (2 * ks + (lane >> 5)) ^ ((lane >> 1) & 7);
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) f.a[mb] = __builtin_bit_cast(f16x8, sa[(64 * wm + 32 * mb + (lane & 31)) * 8 + slot]);
+    for (int mb = 0; mb < NMB; ++mb) f.a[mb] = __builtin_bit_cast(f16x8, sa[(64 * wm + 32 * mb + (lane & 31)) * 8 + slot]);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
     {
@@ -158,28 +160,30 @@ __device__ __forceinline__ void pf_frag_load(PfFrag& f, const u32x4* __restrict_
     }
 }
 
+template <int NMB>
 __device__ __forceinline__ void pf_frag_mfma(const PfFrag& f, f32x16 (&acc)[2][4])
 {
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < NMB; ++mb)
             acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[mb], f.b[nb], acc[mb][nb], 0, 0, 0);
 }
 
 // one k-step of an MFMA wave: 4 sub-steps of 16 k, the fragments of sub-step ks + 1 read while those of ks feed the MFMAs
+template <int NMB>
 __device__ __forceinline__ void pf_mfma_step(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb,
                                              f32x16 (&acc)[2][4])
 {
     PfFrag f0, f1;
-    pf_frag_load(f0, sa, sb, 0);
-    pf_frag_load(f1, sa, sb, 1);
-    pf_frag_mfma(f0, acc);
-    pf_frag_load(f0, sa, sb, 2);
-    pf_frag_mfma(f1, acc);
-    pf_frag_load(f1, sa, sb, 3);
-    pf_frag_mfma(f0, acc);
-    pf_frag_mfma(f1, acc);
+    pf_frag_load<NMB>(f0, sa, sb, 0);
+    pf_frag_load<NMB>(f1, sa, sb, 1);
+    pf_frag_mfma<NMB>(f0, acc);
+    pf_frag_load<NMB>(f0, sa, sb, 2);
+    pf_frag_mfma<NMB>(f1, acc);
+    pf_frag_load<NMB>(f1, sa, sb, 3);
+    pf_frag_mfma<NMB>(f0, acc);
+    pf_frag_mfma<NMB>(f1, acc);
 }
 
 // A rows of one k-step: lane's 32 bytes (chunks 2 (lane & 3), + 1) of row 16 d + (lane >> 2)
@@ -304,15 +308,26 @@ __global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    // row blocks past the group's end are neither read nor multiplied (a wave with none only keeps the barriers)
+    const int wm = wave & 1, wn = wave >> 1;
+    const int nmb = min(2, max(0, (jb.nr - 64 * wm + 31) / 32));
     step_barrier();
-    for (int i = 0; i < KT; ++i)
-    {
-        pf_mfma_step(a_stage(i & 1), b_stage(i & 1), acc);
-        step_barrier();
-    }
+    if (nmb == 2)
+        for (int i = 0; i < KT; ++i)
+        {
+            pf_mfma_step<2>(a_stage(i & 1), b_stage(i & 1), acc);
+            step_barrier();
+        }
+    else if (nmb == 1)
+        for (int i = 0; i < KT; ++i)
+        {
+            pf_mfma_step<1>(a_stage(i & 1), b_stage(i & 1), acc);
+            step_barrier();
+        }
+    else
+        for (int i = 0; i < KT; ++i) step_barrier();
 
     // accumulator element v of lane L: row 8 (v / 4) + 4 (L / 32) + v % 4, column L % 32 of its 32 x 32 block
-    const int wm = wave & 1, wn = wave >> 1;
     const int r0 = jb.r0, nr = jb.nr;
     const int cbo = 2 * jb.cb + wn;                 // this wave's 128-column output block
     if (cbo >= nb128) return;

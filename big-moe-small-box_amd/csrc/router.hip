@@ -288,6 +288,10 @@ __device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, cons
                               int* sgo, int* sui)
 {
     const int lane = threadIdx.x & 63, NE = E + (d.shared ? 1 : 0), rpg = d.rpg;
+    // groups of a count: ceil(c / rpg), a shift when rpg is a power of two (every path's group size is)
+    const bool pow2 = (rpg & (rpg - 1)) == 0;
+    const int sh = __builtin_ctz((unsigned)rpg);
+    auto ngr = [&](int c) { return pow2 ? (c + rpg - 1) >> sh : (c + rpg - 1) / rpg; };
     const int e = lane < n ? pe[lane] : -1;
     for (int x = lane; x < NE; x += 64) scnt[x] = 0;
     if (lane < n && e >= 0) atomicAdd(&scnt[e], 1);
@@ -300,7 +304,7 @@ __device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, cons
         const int x = x0 + i;
         const int c = x < NE ? scnt[x] : 0;
         tc += c;
-        tg += (c + rpg - 1) / rpg;
+        tg += ngr(c);
         tu += c > 0;
     }
     int ic = tc, ig = tg, iu = tu;                 // inclusive scans
@@ -332,7 +336,7 @@ __device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, cons
             }
         }
         bc += c;
-        bg += (c + rpg - 1) / rpg;
+        bg += ngr(c);
         bu += c > 0;
     }
     if (lane == 63)
