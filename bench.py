@@ -261,6 +261,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=None, help="tokens per step (default: the config's batch)")
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--path", choices=["auto", "decode", "mid", "prefill"], default="auto",
+                    help="expert-products path (auto: the library's choice for the batch)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -295,7 +297,8 @@ def main():
     L = bmx.lib()
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     desc, router = layer.desc, layer.router
-    need = L.bmx_moe_layer_workspace(ctypes.byref(desc), T, 0)
+    pa = {"auto": 0, "decode": 1, "prefill": 2, "mid": 3}[args.path]
+    need = L.bmx_moe_layer_workspace(ctypes.byref(desc), T, pa)
     lws = torch.zeros(need, dtype=torch.uint8, device=dev)
     sel_b = torch.empty((T, c["topk"]), dtype=torch.int64, device=dev)
     w_b = torch.empty((T, c["topk"]), dtype=torch.float16, device=dev)
@@ -304,7 +307,7 @@ def main():
     def step():
         s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         bmx._lib.check(L.bmx_moe_layer(ctypes.byref(desc), ctypes.byref(router), P(x), P(lg), T, P(sel_b), P(w_b),
-                                       P(out_b), P(lws), need, 0, s), "bmx_moe_layer")
+                                       P(out_b), P(lws), need, pa, s), "bmx_moe_layer")
 
     def timed(fn, steps):
         torch.cuda.synchronize()
@@ -341,16 +344,17 @@ def main():
     # per-stage timing with events on the launch stream (torch's current stream)
     L = bmx.lib()
     topk = layer.num_experts_per_tok
-    path = L.bmx_resolve_path(T, topk, 0)
+    path = L.bmx_resolve_path(T, topk, pa)
     prefill = path == bmx._lib.PATH_PREFILL
+    mid = path == bmx._lib.PATH_MID
     sel, w = sel_b.clone(), w_b.clone()
-    routes = bmx.ops.dispatch(sel, tab.E, 0, tab.has_shared, L.bmx_rows_per_group(T, topk, 0))
+    routes = bmx.ops.dispatch(sel, tab.E, 0, tab.has_shared, L.bmx_rows_per_group(T, topk, pa))
     desc = layer.desc
-    need = L.bmx_experts_workspace(ctypes.byref(desc), T, 0)
+    need = L.bmx_experts_workspace(ctypes.byref(desc), T, pa)
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
     out = torch.empty((T, tab.H), dtype=torch.float32, device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    stages = ([("prep", bmx._lib.STAGE_PREP)] if prefill else []) + [
+    stages = ([("prep", bmx._lib.STAGE_PREP)] if prefill or mid else []) + [
         ("gate_up", bmx._lib.STAGE_GATE_UP), ("act", bmx._lib.STAGE_ACT), ("down", bmx._lib.STAGE_DOWN),
         ("combine", bmx._lib.STAGE_COMBINE)]
     nst = min(args.steps, 50) if prefill else args.steps
@@ -360,7 +364,7 @@ def main():
         for j, (_, st) in enumerate(stages):
             if e: e[j].record()
             bmx._lib.check(L.bmx_moe_stage(ctypes.byref(desc), st, P(x), T, ctypes.byref(routes.struct), None, None, P(w),
-                                           P(out), P(ws), need, 0, s), "bmx_moe_stage")
+                                           P(out), P(ws), need, pa, s), "bmx_moe_stage")
         if e: e[-1].record()
     torch.cuda.synchronize()
     stage_ms = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j, (name, _) in enumerate(stages)}
@@ -379,7 +383,7 @@ def main():
     n_cpu = T if T <= 64 else 64
     cpu = None if args.no_cpu else cpu_baseline(tab, sel[:n_cpu], w[:n_cpu])
     traffic = None
-    kind = "prefill" if prefill else "decode"
+    kind = "prefill" if prefill else "mid" if mid else "decode"
     tpath = os.path.join(REPO, "profiles", f"{kind}_{args.config}_t{T}.json")
     if os.path.exists(tpath):
         tr = json.load(open(tpath))
@@ -394,7 +398,9 @@ def main():
                     "traffic_source": traffic_src}
     else:
         gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
-        roofline = {"kernel": "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)",
+        kern = ("k_mid_gemm<false> (BMX_STAGE_GATE_UP: trellis decode to LDS + gate/up MFMA in 32-row groups, k-split)"
+                if mid else "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)")
+        roofline = {"kernel": kern,
                     "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "algorithmic_bytes": gu_bytes,
                     "traffic_source": traffic_src}

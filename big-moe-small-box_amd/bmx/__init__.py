@@ -1,6 +1,6 @@
 """bmx: MI355X-native routed-expert MoE layer (HIP kernels for gfx950 behind a C ABI, PyTorch-ROCm host)."""
 from . import _lib
-from ._lib import (ACT_GELU, ACT_RELU2, ACT_SILU, ACT_SILU_OAI, PATH_AUTO, PATH_DECODE, PATH_PREFILL, SCORE_SIGMOID,
+from ._lib import (ACT_GELU, ACT_RELU2, ACT_SILU, ACT_SILU_OAI, PATH_AUTO, PATH_DECODE, PATH_MID, PATH_PREFILL, SCORE_SIGMOID,
                    SCORE_SOFTMAX, TF_K2, TF_K3, TF_K4, TF_K25, TILE_BYTES, BmxError, lib)
 from .experts import ExpertTable
 from .layer import MoELayer
@@ -9,4 +9,4 @@ from . import ops
 
 __all__ = ["ExpertTable", "ExpertSlots", "MoELayer", "ops", "lib", "BmxError", "TF_K2", "TF_K25", "TF_K3", "TF_K4", "TILE_BYTES",
            "SCORE_SIGMOID", "SCORE_SOFTMAX", "ACT_SILU", "ACT_GELU", "ACT_RELU2", "ACT_SILU_OAI", "PATH_AUTO",
-           "PATH_DECODE", "PATH_PREFILL", "_lib"]
+           "PATH_DECODE", "PATH_MID", "PATH_PREFILL", "_lib"]

@@ -65,6 +65,10 @@ int launch_slot_copy(const bmx_slot_table* t, int li, hipStream_t s);
 
 // moe_prefill.hip (same ws / stage conventions; ws layout [xt][part_gu][act rows][part_dn])
 int prefill_rows_per_group();
+int mid_rows_per_group();
+size_t mid_ws_bytes(const MoeShape& m);
+int launch_mid_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows, void* ws,
+                       size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages);
 size_t prefill_ws_bytes(const MoeShape& m);
 int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
                            void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s,

@@ -91,25 +91,33 @@ static bmx_routes routes_at(char* base, const RoutesLayout& L)
 
 constexpr int STAGES_LAYER = (1 << BMX_STAGE_PREP) | (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) | (1 << BMX_STAGE_COMBINE);
 
-// AUTO takes the MFMA path from this many routed rows (T * topk) up, the GEMV path below
-static long prefill_min_rows()
+// AUTO: the GEMV path below BMX_MID_MIN_ROWS routed rows (T * topk), the mid-size MFMA path below
+// BMX_PREFILL_MIN_ROWS, the prefill MFMA path from there up
+static long env_rows(const char* name, long dflt)
 {
-    const char* v = getenv("BMX_PREFILL_MIN_ROWS");
-    return (v && *v) ? atol(v) : 512;
+    const char* v = getenv(name);
+    return (v && *v) ? atol(v) : dflt;
 }
 
 static int resolve_path(int path, int T, int topk)
 {
-    if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL) return path;
-    if (path == BMX_PATH_AUTO) return (long)T * topk >= prefill_min_rows() ? BMX_PATH_PREFILL : BMX_PATH_DECODE;
-    return -1;
+    if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL || path == BMX_PATH_MID) return path;
+    if (path != BMX_PATH_AUTO) return -1;
+    const long rows = (long)T * topk;
+    if (rows >= env_rows("BMX_PREFILL_MIN_ROWS", 512)) return BMX_PATH_PREFILL;
+    if (rows >= env_rows("BMX_MID_MIN_ROWS", 1L << 30)) return BMX_PATH_MID;
+    return BMX_PATH_DECODE;
 }
 
-static int path_rows_per_group(int path, int T) { return path == BMX_PATH_PREFILL ? prefill_rows_per_group() : decode_rows_per_group(T); }
+static int path_rows_per_group(int path, int T)
+{
+    return path == BMX_PATH_PREFILL ? prefill_rows_per_group() : path == BMX_PATH_MID ? mid_rows_per_group()
+                                                                                       : decode_rows_per_group(T);
+}
 
 static size_t experts_ws_bytes(int path, const MoeShape& m)
 {
-    return path == BMX_PATH_PREFILL ? prefill_ws_bytes(m) : decode_ws_bytes(m);
+    return path == BMX_PATH_PREFILL ? prefill_ws_bytes(m) : path == BMX_PATH_MID ? mid_ws_bytes(m) : decode_ws_bytes(m);
 }
 
 static int launch_experts(int path, const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
@@ -117,6 +125,8 @@ static int launch_experts(int path, const MoeShape& m, const void* x, const bmx_
 {
     if (path == BMX_PATH_PREFILL)
         return launch_prefill_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
+    if (path == BMX_PATH_MID)
+        return launch_mid_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
     return launch_decode_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
 }
 

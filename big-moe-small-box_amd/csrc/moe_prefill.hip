@@ -19,37 +19,51 @@ namespace bmx {
 
 constexpr int PF_M = 128;                    // rows per group
 
-// Workgroups are handed to the 8 XCDs round-robin (block b runs on XCD b % 8). Renumber so that consecutive logical
-// blocks share an XCD: the column blocks of one row group then read the group's A rows through the same L2.
+// Workgroups are handed to the 8 XCDs round-robin (block b runs on XCD b % 8). Renumber so that chunks of 16
+// consecutive logical blocks (the column blocks of one row group) share an XCD, and the chunks go round-robin over the
+// XCDs: a group's units read its A rows through one L2, and the groups that exist (the grid is sized for the most a batch
+// can have) spread over all XCDs. Blocks past the last whole 128-block round keep their number.
 __device__ __forceinline__ int xcd_block(int bid, int nblk)
 {
-    const int q = nblk / 8, rem = nblk % 8, xcd = bid % 8, i = bid / 8;
-    return (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + i;
+    constexpr int C = 16;
+    if (bid >= nblk / (8 * C) * (8 * C)) return bid;
+    const int xcd = bid % 8, i = bid / 8;
+    return ((i / C) * 8 + xcd) * C + i % C;
 }
 
-// ---- rotated inputs: 16 lanes per (row, matrix), 8 consecutive inputs per lane -----------------------------------------
+// ---- rotated inputs: 16 lanes per (row, matrix, run of PREP_BPU 128-blocks), 8 consecutive inputs per lane -------------
+constexpr int PREP_BPU = 4;
 __global__ __launch_bounds__(256) void k_pf_prep(GvArgs a)
 {
-    const int u = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
-    const int r = u >> 1, mat = u & 1;
+    const int nblk = a.H / 128, nrun = (nblk + PREP_BPU - 1) / PREP_BPU;
+    const long u = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int j = threadIdx.x & 15, run = (int)(u % nrun), mat = (int)((u / nrun) & 1), r = (int)(u / nrun / 2);
     if (r >= a.offsets[a.NE]) return;
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const uint16_t* xr = a.x + (size_t)a.row_token[r] * a.H + 8 * j;
     const uint16_t* su = reinterpret_cast<const uint16_t*>(ex.suh[mat]) + 8 * j;
     uint16_t* dst = a.xt + ((size_t)mat * a.R_max + r) * a.H + 8 * j;
-    for (int b = 0; b < a.H / 128; ++b)
+#pragma unroll
+    for (int i = 0; i < PREP_BPU; ++i)
     {
+        const int b = run * PREP_BPU + i;
+        if (b >= nblk) break;
         float v[8], s[8];
         unpack8(ldg4(xr + 128 * b), v);
         unpack8(ldg4(su + 128 * b), s);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = v[i] * s[i];
+        for (int q = 0; q < 8; ++q) v[q] = v[q] * s[q];
         had128_x8(v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = v[i] * R_SCALE;
+        for (int q = 0; q < 8; ++q) v[q] = v[q] * R_SCALE;
         *reinterpret_cast<u32x4*>(dst + 128 * b) = pack8_r(v);
     }
+}
+
+static dim3 prep_grid(int R_max, int H)
+{
+    return dim3((unsigned)(((long)2 * R_max * ((H / 128 + PREP_BPU - 1) / PREP_BPU) + 15) / 16));
 }
 
 // ---- LDS stages ------------------------------------------------------------------------------------------------------
@@ -352,6 +366,166 @@ __global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
     }
 }
 
+// ---- mid-size grouped GEMM: groups of <= 32 rows, every wave decodes and multiplies ------------------------------------
+// For decode batches of several tokens (a few rows per expert): work unit = (group of <= 32 rows, matrix, 256-column block,
+// k-split). 8 waves; per k-step of 64 each wave decodes half a strip per tile-row exactly as a prefill decode wave does
+// (same B fragment layout, pf_b0 / pf_b1), copies 8 bytes of the A rows, and, from the previous step's stage, runs the 4
+// MFMAs (32 rows x 32 columns, k 16 each) of its 32-column block. One barrier per step; the fp32 products of each k-split
+// go to the partial layout the epilogues sum in split order.
+constexpr int MID_M = 32;
+constexpr int MID_WAVES = 8;
+constexpr int MID_A_U4 = MID_M * 8;
+__shared__ u32x4 mid_a0[MID_A_U4];
+__shared__ u32x4 mid_a1[MID_A_U4];
+__device__ __forceinline__ u32x4* mid_a_stage(int s) { return s == 0 ? mid_a0 : mid_a1; }
+
+struct MidArow {
+    uint32_t d[2];
+};
+
+// lane's 8 bytes of the A rows of a step: row 4 wave + lane / 16, bytes 8 (lane % 16) of the row's 128 (64 inputs)
+__device__ __forceinline__ void mid_a_fetch(MidArow& r, const uint16_t* rowp, int k0)
+{
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(rowp + k0);
+    r.d[0] = ldg(p, 0);
+    r.d[1] = ldg(p, 1);
+}
+
+__device__ __forceinline__ void mid_a_store(const MidArow& r, u32x4* __restrict__ stage)
+{
+    const int lane = threadIdx.x & 63, row = 4 * (threadIdx.x >> 6) + (lane >> 4), piece = lane & 15;
+    uint2* p = reinterpret_cast<uint2*>(stage + row * 8 + ((piece >> 1) ^ ((row >> 1) & 7))) + (piece & 1);
+    *p = make_uint2(r.d[0], r.d[1]);
+}
+
+// the wave's 32-column block of one step: 4 MFMAs, k 16 each, alternating between two accumulators
+__device__ __forceinline__ void mid_mfma_step(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, f32x16& acc0,
+                                              f32x16& acc1)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    f16x8 fa[4], fb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+    {
+        const int slot = (2 * ks + (lane >> 5)) ^ ((lane >> 1) & 7), fi = ks * 8 + wave;
+        fa[ks] = __builtin_bit_cast(f16x8, sa[(lane & 31) * 8 + slot]);
+        fb[ks] = __builtin_bit_cast(f16x8, sb[fi * 64 + bsw(fi, lane)]);
+    }
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[0], fb[0], acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1], fb[1], acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[2], fb[2], acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[3], fb[3], acc1, 0, 0, 0);
+}
+
+// steps s0 .. s0 + n - 1 of the unit; straight-line like pf_decoder (loads past the last step re-read it)
+template <int F, int HALF>
+__device__ __forceinline__ void mid_run(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int s0, int n,
+                                        f32x16& acc0, f32x16& acc1)
+{
+    constexpr int TB = Fmt<F>::TB, NW = TB / 16;
+    const int lane = threadIdx.x & 63, d = threadIdx.x >> 6;
+    const int h = lane >> 5, t = (lane >> 2) & 7, sl = lane & 3;
+    const int kt = 2 * (d >> 2) + h, th = (d >> 1) & 1;
+    const int tcol = min(2 * jb.cb + th, jb.nb128 - 1);
+    const size_t row_bytes = (size_t)(jb.N / 16) * TB, step_bytes = 4 * row_bytes;
+    const uint8_t* p = mat_base + (size_t)kt * row_bytes + (size_t)(tcol * 8 + t) * TB + sl * (TB / 4);
+    const int arow = 4 * d + (lane >> 4);
+    const uint16_t* rowp = asrc + (size_t)(jb.r0 + min(arow, jb.nr - 1)) * jb.K + 4 * (lane & 15);
+    auto wp = [&](int i) { return p + (size_t)(s0 + min(i, n - 1)) * step_bytes; };
+    auto ak = [&](int i) { return 64 * (s0 + min(i, n - 1)); };
+    uint32_t w0[NW], w1[NW], w2[NW];
+    MidArow a0, a1, a2;
+    mid_a_fetch(a0, rowp, ak(0));
+    mid_a_fetch(a1, rowp, ak(1));
+    mid_a_fetch(a2, rowp, ak(2));
+    load_words(w0, wp(0));
+    load_words(w1, wp(1));
+    load_words(w2, wp(2));
+    decode_half<F, HALF>(w0, pf_b0, kt, 128 * th);
+    mid_a_store(a0, mid_a0);
+    step_barrier();
+    // step i: the MFMAs of stage i % 2, the decode of step i + 1 into the other stage, the fetch of step i + 3
+    for (int i = 0; i < n; i += 3)
+    {
+        mid_a_fetch(a0, rowp, ak(i + 3));
+        load_words(w0, wp(i + 3));
+        mid_mfma_step(mid_a_stage(i & 1), b_stage(i & 1), acc0, acc1);
+        decode_half<F, HALF>(w1, b_stage((i + 1) & 1), kt, 128 * th);
+        mid_a_store(a1, mid_a_stage((i + 1) & 1));
+        step_barrier();
+        if (i + 1 >= n) break;
+        mid_a_fetch(a1, rowp, ak(i + 4));
+        load_words(w1, wp(i + 4));
+        mid_mfma_step(mid_a_stage((i + 1) & 1), b_stage((i + 1) & 1), acc0, acc1);
+        decode_half<F, HALF>(w2, b_stage(i & 1), kt, 128 * th);
+        mid_a_store(a2, mid_a_stage(i & 1));
+        step_barrier();
+        if (i + 2 >= n) break;
+        mid_a_fetch(a2, rowp, ak(i + 5));
+        load_words(w2, wp(i + 5));
+        mid_mfma_step(mid_a_stage(i & 1), b_stage(i & 1), acc0, acc1);
+        decode_half<F, HALF>(w0, b_stage((i + 1) & 1), kt, 128 * th);
+        mid_a_store(a0, mid_a_stage((i + 1) & 1));
+        step_barrier();
+    }
+}
+
+template <int F>
+__device__ __forceinline__ void mid_run_any(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int s0, int n,
+                                            f32x16& acc0, f32x16& acc1)
+{
+    if ((threadIdx.x >> 6) & 1) mid_run<F, 1>(jb, mat_base, asrc, s0, n, acc0, acc1);
+    else mid_run<F, 0>(jb, mat_base, asrc, s0, n, acc0, acc1);
+}
+
+template <bool DOWN>
+__global__ __launch_bounds__(MID_WAVES * 64) void k_mid_gemm(GvArgs a)
+{
+    const int nb128 = DOWN ? a.NBH : a.NB;
+    const int NB2 = (nb128 + 1) / 2, KS = DOWN ? a.KS_dn : a.KS_gu;
+    int lid = xcd_block(blockIdx.x, gridDim.x);
+    const int ksp = lid % KS;
+    lid /= KS;
+    PfJob jb;
+    jb.nb128 = nb128;
+    if (DOWN) { jb.g = lid / NB2; jb.mat = 2; jb.cb = lid % NB2; }
+    else { jb.g = lid / (2 * NB2); jb.mat = (lid / NB2) & 1; jb.cb = lid % NB2; }
+    if (jb.g >= *a.ngroups) return;
+    jb.e = a.groups[3 * jb.g];
+    if (!DOWN && group_skipped(a, jb.e)) return;
+    jb.r0 = a.groups[3 * jb.g + 1];
+    jb.nr = a.groups[3 * jb.g + 2];
+    jb.ex = jb.e == a.E ? a.shared : a.experts + jb.e;
+    jb.K = DOWN ? a.I : a.H;
+    jb.N = DOWN ? a.H : a.I;
+    const int n = jb.K / 64 / KS, s0 = ksp * n;
+    const uint16_t* asrc = DOWN ? a.act_rows : a.xt + (size_t)jb.mat * a.R_max * a.H;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(jb.ex->tr[jb.mat]);
+    f32x16 acc0 = f32x16{}, acc1 = f32x16{};
+    switch (jb.ex->fmt[jb.mat])
+    {
+        case BMX_TF_K2: mid_run_any<BMX_TF_K2>(jb, base, asrc, s0, n, acc0, acc1); break;
+        case BMX_TF_K25: mid_run_any<BMX_TF_K25>(jb, base, asrc, s0, n, acc0, acc1); break;
+        case BMX_TF_K3: mid_run_any<BMX_TF_K3>(jb, base, asrc, s0, n, acc0, acc1); break;
+        default: mid_run_any<BMX_TF_K4>(jb, base, asrc, s0, n, acc0, acc1); break;
+    }
+    // accumulator element v of lane L: row 8 (v / 4) + 4 (L / 32) + v % 4, column L % 32 of the wave's 32-column block
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int cbo = 2 * jb.cb + (wave >> 2);
+    if (cbo >= nb128) return;
+    const int col = 32 * (wave & 3) + (lane & 31);
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+    {
+        const int row = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row >= jb.nr) continue;
+        const size_t r = (size_t)ksp * a.R_max + jb.r0 + row;
+        const float y = acc0[v] + acc1[v];
+        if (DOWN) a.part_dn[(r * a.NBH + cbo) * 128 + col] = y;
+        else a.part_gu[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] = y;
+    }
+}
+
 // ---- plan and launch -------------------------------------------------------------------------------------------------
 struct PrefillPlan {
     int NB, NBH, G_max, R_max;
@@ -373,6 +547,99 @@ static PrefillPlan prefill_plan(const MoeShape& m)
 }
 
 int prefill_rows_per_group() { return PF_M; }
+
+// ---- mid-size path ------------------------------------------------------------------------------------------------------
+struct MidPlan {
+    int NB, NBH, G_max, R_max, KS_gu, KS_dn;
+    size_t xt_bytes, part_gu_bytes, act_bytes, part_dn_bytes;
+};
+
+// k-split: the most splits that keep at least MID_MIN_STEPS k-steps each (the routing, unknown here, may put all rows
+// on a few experts; splits keep the workgroup count up then, at the price of partial sums the epilogue adds)
+static int mid_split(int ksteps)
+{
+    const char* v = getenv("BMX_MID_MIN_STEPS");
+    const int min_steps = (v && *v) ? atoi(v) : 8;
+    for (int d = ksteps; d > 1; --d)
+        if (ksteps % d == 0 && ksteps / d >= min_steps) return d;
+    return 1;
+}
+
+static MidPlan mid_plan(const MoeShape& m)
+{
+    MidPlan p;
+    p.NB = m.I / 128;
+    p.NBH = m.H / 128;
+    p.G_max = groups_max(m.T, m.topk, m.E, m.shared, MID_M);
+    p.R_max = m.T * m.topk + (m.shared ? m.T : 0);
+    p.KS_gu = mid_split(m.H / 64);
+    p.KS_dn = mid_split(m.I / 64);
+    p.xt_bytes = (size_t)2 * p.R_max * m.H * 2;
+    p.part_gu_bytes = (size_t)p.KS_gu * p.R_max * p.NB * 256 * 4;
+    p.act_bytes = (size_t)p.R_max * m.I * 2;
+    p.part_dn_bytes = (size_t)p.KS_dn * p.R_max * p.NBH * 128 * 4;
+    return p;
+}
+
+int mid_rows_per_group() { return MID_M; }
+
+size_t mid_ws_bytes(const MoeShape& m)
+{
+    const MidPlan p = mid_plan(m);
+    return align_up(p.xt_bytes, 256) + align_up(p.part_gu_bytes, 256) + align_up(p.act_bytes, 256) +
+           align_up(p.part_dn_bytes, 256);
+}
+
+int launch_mid_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows, void* ws,
+                       size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages)
+{
+    if (m.H % 128 || m.I % 128 || m.H <= 0 || m.I <= 0)
+        return set_error(BMX_ERR_ARG, "moe experts: H (%d) and I (%d) must be multiples of 128", m.H, m.I);
+    if (ws_bytes < mid_ws_bytes(m))
+        return set_error(BMX_ERR_WORKSPACE, "moe experts: workspace %zu < %zu", ws_bytes, mid_ws_bytes(m));
+    if (!r->row_expert) return set_error(BMX_ERR_ARG, "moe experts: routes without row_expert");
+    const MidPlan p = mid_plan(m);
+    char* w = static_cast<char*>(ws);
+    GvArgs a;
+    a.experts = m.experts; a.shared = m.shared_ex; a.E = m.E; a.H = m.H; a.I = m.I; a.act = m.act; a.gated = m.gated;
+    a.limit = m.limit;
+    a.x = static_cast<const uint16_t*>(x);
+    a.row_token = r->row_token; a.groups = r->groups; a.ngroups = r->ngroups; a.row_expert = r->row_expert;
+    a.xt = reinterpret_cast<uint16_t*>(w);
+    w += align_up(p.xt_bytes, 256);
+    a.part_gu = reinterpret_cast<float*>(w);
+    w += align_up(p.part_gu_bytes, 256);
+    a.act_rows = act_rows ? static_cast<uint16_t*>(act_rows) : reinterpret_cast<uint16_t*>(w);
+    w += align_up(p.act_bytes, 256);
+    a.part_dn = reinterpret_cast<float*>(w);
+    a.y_rows = y_rows;
+    a.KS_gu = p.KS_gu; a.KS_dn = p.KS_dn; a.NB = p.NB; a.NBH = p.NBH; a.R_max = p.R_max;
+    a.NE = m.E + (m.shared ? 1 : 0);
+    a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
+    a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
+    a.fresh = m.fresh;
+    a.filter = 0;
+    int rc = BMX_OK;
+    if (stages & (1 << BMX_STAGE_PREP))
+        hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);
+    for (int f = 0; f < 3; ++f)
+    {
+        const int st = f == 0 ? BMX_STAGE_GATE_UP : f == 1 ? BMX_STAGE_GATE_UP_RESIDENT : BMX_STAGE_GATE_UP_STAGED;
+        if (!(stages & (1 << st))) continue;
+        GvArgs b = a;
+        b.filter = f;
+        hipLaunchKernelGGL(k_mid_gemm<false>, dim3((unsigned)(p.G_max * 2 * ((p.NB + 1) / 2) * p.KS_gu)),
+                           dim3(MID_WAVES * 64), 0, s, b);
+    }
+    if (stages & (1 << BMX_STAGE_ACT)) rc = launch_epilogue(a, BMX_STAGE_ACT, s);
+    if (!rc && (stages & (1 << BMX_STAGE_DOWN)))
+        hipLaunchKernelGGL(k_mid_gemm<true>, dim3((unsigned)(p.G_max * ((p.NBH + 1) / 2) * p.KS_dn)),
+                           dim3(MID_WAVES * 64), 0, s, a);
+    if (!rc && (stages & (1 << BMX_STAGE_COMBINE))) rc = launch_epilogue(a, BMX_STAGE_COMBINE, s);
+    if (!rc && (stages & (1 << BMX_STAGE_DOWN_OUT))) rc = launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
+    if (rc) return rc;
+    return check_launch("moe experts (mid-size path)");
+}
 
 size_t prefill_ws_bytes(const MoeShape& m)
 {
@@ -413,7 +680,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.filter = 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
-        hipLaunchKernelGGL(k_pf_prep, dim3((unsigned)((2 * p.R_max + 15) / 16)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);
     for (int f = 0; f < 3; ++f)
     {
         const int st = f == 0 ? BMX_STAGE_GATE_UP : f == 1 ? BMX_STAGE_GATE_UP_RESIDENT : BMX_STAGE_GATE_UP_STAGED;

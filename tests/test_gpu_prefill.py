@@ -10,7 +10,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 MAX_ABS, REL_RMS = 1e-2, 1e-3
-PREFILL, DECODE = 2, 1
+PREFILL, DECODE, MID = 2, 1, 3
 
 
 def say(*a):
@@ -137,3 +137,55 @@ def test_prefill_c3_full_size(cuda, oracle):
     w2 = w.clone()
     w2[::7, 2] = 0
     assert torch.equal(bmx.ops.moe_forward(d, x, s2, w), bmx.ops.moe_forward(d, x, sel, w2))
+
+
+MID_LAYERS = [
+    # name, config, E, T, H, I, oracle rows
+    ("c5 T16 K2/K2.5", "c5", 384, 16, None, None, [0, 7, 15]),
+    ("c2 T8 shared", "c2", 288, 8, None, None, [0, 5]),
+    ("c3 shape E24 T40", "c3", 24, 40, None, None, [0, 17, 39]),
+    ("c1 T4 K4", "c1", 64, 4, None, None, None),
+    ("odd blocks H384 I256", "c2", 8, 24, 384, 256, [0, 11, 23]),
+]
+
+
+@pytest.mark.parametrize("name,cfgname,E,T,H,I,rows", MID_LAYERS, ids=[l[0] for l in MID_LAYERS])
+def test_mid_layer_parity(cuda, oracle, name, cfgname, E, T, H, I, rows):
+    """The mid-size MFMA path (groups of 32 rows, k-splits) against the oracle and the GEMV path."""
+    import bmx
+    say("mid", name, "build")
+    tab, layer, x, lg = make_layer(cfgname, E, 13, cuda, T, H, I)
+    sel, w = layer.routing_fn(T, None, x, {"logits": lg})
+    say("mid", name, "run")
+    out = layer.run_bszN(x, sel, w, path=MID).cpu().numpy()
+    dec = layer.run_bszN(x, sel, w, path=DECODE).cpu().numpy()
+    fused = layer.forward(x, lg, path=MID).cpu().numpy()
+    assert np.array_equal(fused, out)
+    assert bmx.lib().bmx_rows_per_group(T, layer.num_experts_per_tok, MID) == 32
+    rows = list(range(T)) if rows is None else rows
+    want = oracle_layer(oracle, tab, x.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy(), rows)
+    got = out[rows]
+    err_abs, err_rel = float(np.abs(got - want).max()), rel_rms(got, want)
+    say("mid", name, "max_abs", err_abs, "rel_rms", err_rel)
+    assert err_abs < MAX_ABS and err_rel < REL_RMS
+    assert float(np.abs(out - dec).max()) < MAX_ABS and rel_rms(out, dec.astype(np.float64)) < REL_RMS
+    assert np.array_equal(out, layer.run_bszN(x, sel, w, path=MID).cpu().numpy())
+
+
+def test_mid_experts_rows_and_properties(cuda):
+    """Every dispatch row's expert output on the mid path against the GEMV path; weights x 2 -> output x 2 bit for bit."""
+    import bmx
+    tab, layer, x, lg = make_layer("c5", 384, 23, cuda, 16)
+    sel, w = layer.routing_fn(16, None, x, {"logits": lg})
+    d = tab.desc(6)
+    rm = bmx.ops.dispatch(sel, tab.E, 0, False, bmx.lib().bmx_rows_per_group(16, 6, MID))
+    rd = bmx.ops.dispatch(sel, tab.E, 0, False, bmx.lib().bmx_rows_per_group(16, 6, DECODE))
+    ym, am = bmx.ops.moe_experts(d, x, rm, path=MID, with_act=True)
+    yd, ad = bmx.ops.moe_experts(d, x, rd, path=DECODE, with_act=True)
+    torch.cuda.synchronize()
+    n = rm.rows()
+    assert n == 96 and torch.equal(rm.row_token, rd.row_token)
+    assert rel_rms(ym[:n].cpu().numpy(), yd[:n].cpu().numpy().astype(np.float64)) < REL_RMS
+    a = bmx.ops.moe_forward(d, x, sel, w, path=MID)
+    b = bmx.ops.moe_forward(d, x, sel, (w * 2).contiguous(), path=MID)
+    assert torch.equal(b, a * 2)
