@@ -179,7 +179,8 @@ def bench_c4(args):
     ws_n = L.bmx_experts_workspace(ctypes.byref(descs[0]), 1, 1)
     ws = torch.zeros(ws_n, dtype=torch.uint8, device=dev)
     stepped = [torch.cuda.Event() for _ in range(NL)]
-    copied = [torch.cuda.Event() for _ in range(NL)]
+    copied_gu = [torch.cuda.Event() for _ in range(NL)]
+    copied_dn = [torch.cuda.Event() for _ in range(NL)]
     side = slots.side
     tstruct = ctypes.byref(slots.struct)
 
@@ -193,16 +194,18 @@ def bench_c4(args):
             bmx._lib.check(L.bmx_slot_step(tstruct, li, P(sel), topk, 0, 1, sp), "slot step")
             stepped[li].record(s)
             side.wait_event(stepped[li])
-            bmx._lib.check(L.bmx_slot_copy(tstruct, li, ctypes.c_void_p(side.cuda_stream)), "slot copy")
-            copied[li].record(side)
+            bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 3, ctypes.c_void_p(side.cuda_stream)), "slot copy")
+            copied_gu[li].record(side)
+            bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 4, ctypes.c_void_p(side.cuda_stream)), "slot copy")
+            copied_dn[li].record(side)
             bmx._lib.check(L.bmx_dispatch(P(sel), 1, topk, E, 0, 1, rpg, ctypes.byref(routes.struct), P(dws), dws_n, sp),
                            "dispatch")
             d = ctypes.byref(descs[li])
             o = ctypes.c_void_p(out.data_ptr() + li * H * 4)
-            for st in (bmx._lib.STAGE_GATE_UP_RESIDENT, None, bmx._lib.STAGE_GATE_UP_STAGED, bmx._lib.STAGE_ACT,
+            for st in (bmx._lib.STAGE_GATE_UP_RESIDENT, "gu", bmx._lib.STAGE_GATE_UP_STAGED, bmx._lib.STAGE_ACT, "dn",
                        bmx._lib.STAGE_DOWN, bmx._lib.STAGE_COMBINE):
-                if st is None:
-                    s.wait_event(copied[li])
+                if isinstance(st, str):
+                    s.wait_event(copied_gu[li] if st == "gu" else copied_dn[li])
                     continue
                 bmx._lib.check(L.bmx_moe_stage(d, st, P(x), 1, ctypes.byref(routes.struct), None, None, P(w), o, P(ws),
                                                ws_n, 1, sp), "stage")

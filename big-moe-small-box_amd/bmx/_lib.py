@@ -73,6 +73,7 @@ SIGNATURES = {
     "bmx_moe_layer": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
     "bmx_slot_step": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, _I64, _I, _P]),
     "bmx_slot_copy": (_I, [ctypes.POINTER(SlotTable), _I, _P]),
+    "bmx_slot_copy_mats": (_I, [ctypes.POINTER(SlotTable), _I, _I, _P]),
     "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
     "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }

@@ -97,9 +97,12 @@ class MoELayer:
 
         stage(L.STAGE_PREP)
         stage(L.STAGE_GATE_UP_RESIDENT)
-        self.slots.wait_copies(self.li)
-        for st in (L.STAGE_GATE_UP_STAGED, L.STAGE_ACT, L.STAGE_DOWN, L.STAGE_COMBINE):
-            stage(st)
+        self.slots.wait_copies(self.li, part="gate_up")
+        stage(L.STAGE_GATE_UP_STAGED)
+        stage(L.STAGE_ACT)
+        self.slots.wait_copies(self.li, part="down")
+        stage(L.STAGE_DOWN)
+        stage(L.STAGE_COMBINE)
         self._routes = routes
         return out
 

@@ -59,17 +59,22 @@ class ExpertSlots:
         stepped = torch.cuda.Event()
         stepped.record(cur)
         self.side.wait_event(stepped)
-        L.check(L.lib().bmx_slot_copy(ctypes.byref(self.struct), li, ctypes.c_void_p(self.side.cuda_stream)),
-                "bmx_slot_copy")
-        ev = torch.cuda.Event()
-        ev.record(self.side)
-        self.copied[li] = ev
-        return ev
+        evs = []
+        for mats in (3, 4):          # gate and up first, down behind them
+            L.check(L.lib().bmx_slot_copy_mats(ctypes.byref(self.struct), li, mats,
+                                               ctypes.c_void_p(self.side.cuda_stream)), "bmx_slot_copy_mats")
+            ev = torch.cuda.Event()
+            ev.record(self.side)
+            evs.append(ev)
+        self.copied[li] = tuple(evs)
+        return evs[1]
 
-    def wait_copies(self, li, stream=None):
-        """Order `stream` (default: current) after the copies of layer li's last step."""
+    def wait_copies(self, li, stream=None, part="all"):
+        """Order `stream` (default: current) after the copies of layer li's last step: part "gate_up" (the admitted
+        experts' gate and up matrices), "down" or "all"."""
         if self.copied[li] is not None:
-            (stream or torch.cuda.current_stream()).wait_event(self.copied[li])
+            ev = self.copied[li][0 if part == "gate_up" else 1]
+            (stream or torch.cuda.current_stream()).wait_event(ev)
 
     def desc(self, li, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0):
         return self.layers[li].desc(topk, first, act, gated, act_limit, fresh=self.fresh)

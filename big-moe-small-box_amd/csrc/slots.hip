@@ -170,8 +170,9 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     }
 }
 
-// copies of the last step's admissions: blockIdx.y = job; 16-byte chunks, grid-stride
-__global__ __launch_bounds__(256) void k_slot_copy(bmx_slot_table t, int li)
+// copies of the last step's admissions: blockIdx.y = job; the matrices in `mats` (bit 0 gate, 1 up, 2 down); 16-byte
+// chunks, grid-stride
+__global__ __launch_bounds__(256) void k_slot_copy(bmx_slot_table t, int li, int mats)
 {
     const int j = blockIdx.y;
     if (j >= t.ctl[2]) return;
@@ -183,6 +184,7 @@ __global__ __launch_bounds__(256) void k_slot_copy(bmx_slot_table t, int li)
 #pragma unroll 1
     for (int m = 0; m < 3; ++m)
     {
+        if (!((mats >> m) & 1)) continue;
         const size_t n16 = tiles * tile_bytes_dev(ex.fmt[m]) / 16;
         const u32x4* src = reinterpret_cast<const u32x4*>(t.home[((size_t)li * t.E + e) * 3 + m]);
         u32x4* dst = reinterpret_cast<u32x4*>(b + (m == 0 ? 0 : m == 1 ? (uint64_t)t.off_u : (uint64_t)t.off_d));
@@ -231,13 +233,14 @@ int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n,
     return check_launch("bmx_slot_step");
 }
 
-int launch_slot_copy(const bmx_slot_table* t, int li, hipStream_t s)
+int launch_slot_copy(const bmx_slot_table* t, int li, int mats, hipStream_t s)
 {
     int rc = check_table(t, "bmx_slot_copy");
     if (rc) return rc;
     if (li < 0 || li >= t->L) return set_error(BMX_ERR_ARG, "bmx_slot_copy: bad layer");
-    if (t->maxj == 0) return BMX_OK;
-    hipLaunchKernelGGL(k_slot_copy, dim3(64, (unsigned)t->maxj), dim3(256), 0, s, *t, li);
+    if (mats < 0 || mats > 7) return set_error(BMX_ERR_ARG, "bmx_slot_copy: bad matrix mask %d", mats);
+    if (t->maxj == 0 || mats == 0) return BMX_OK;
+    hipLaunchKernelGGL(k_slot_copy, dim3(64, (unsigned)t->maxj), dim3(256), 0, s, *t, li, mats);
     return check_launch("bmx_slot_copy");
 }
 
@@ -255,7 +258,12 @@ int bmx_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, in
 
 int bmx_slot_copy(const bmx_slot_table* t, int li, bmx_stream_t stream)
 {
-    return launch_slot_copy(t, li, static_cast<hipStream_t>(stream));
+    return launch_slot_copy(t, li, 7, static_cast<hipStream_t>(stream));
+}
+
+int bmx_slot_copy_mats(const bmx_slot_table* t, int li, int mats, bmx_stream_t stream)
+{
+    return launch_slot_copy(t, li, mats, static_cast<hipStream_t>(stream));
 }
 
 int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream)

@@ -220,6 +220,10 @@ int bmx_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, in
  * over PCIe). Run it on a side stream ordered after bmx_slot_step; the admitted experts' gate / up
  * (BMX_STAGE_GATE_UP_STAGED) must be ordered after it. */
 int bmx_slot_copy(const bmx_slot_table* t, int li, bmx_stream_t stream);
+/* The same copies restricted to the matrices in mats (bit 0 gate, 1 up, 2 down), so that the staged gate / up can start
+ * when those two have landed while the down matrices are still in flight (the reference copies whole slots,
+ * engine/ec.py:78-105). */
+int bmx_slot_copy_mats(const bmx_slot_table* t, int li, int mats, bmx_stream_t stream);
 /* Host-planned staging: n copies src[i] -> dst[i] of bytes[i] (hipMemcpyAsync, e.g. pinned host -> slot), in order on
  * stream (the reference's stage_layer, engine/kernels/nv2/nv2_host.cpp:1558-1593). */
 int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream);
