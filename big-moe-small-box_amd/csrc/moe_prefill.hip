@@ -223,7 +223,7 @@ __device__ __forceinline__ void a_store(const PfArow& r, u32x4* __restrict__ sta
 // The loop is straight-line code (every step issues the same loads, past-the-end steps re-read the last one, a missing
 // second 128-column half decodes the first one's tiles again), so the compiler's wait counts for the prefetched
 // registers stay exact and the waits land only where the data is two steps old.
-template <int F, int HALF>
+template <int F, int HALF, bool ACOPY>
 __device__ __forceinline__ void pf_decoder(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int d)
 {
     constexpr int TB = Fmt<F>::TB, NW = TB / 16;
@@ -241,44 +241,57 @@ __device__ __forceinline__ void pf_decoder(const PfJob& jb, const uint8_t* mat_b
     auto ak = [&](int step) { return 64 * min(step, KT - 1); };
     uint32_t w0[NW], w1[NW], w2[NW];
     PfArow a0, a1, a2;
-    a_fetch(a0, rowp, ak(0));
-    a_fetch(a1, rowp, ak(1));
-    a_fetch(a2, rowp, ak(2));
+    if (ACOPY)
+    {
+        a_fetch(a0, rowp, ak(0));
+        a_fetch(a1, rowp, ak(1));
+        a_fetch(a2, rowp, ak(2));
+    }
     load_words(w0, wp(0));
     load_words(w1, wp(1));
     load_words(w2, wp(2));
     decode_half<F, HALF>(w0, pf_b0, kt, 128 * th);
-    a_store(a0, pf_a0, arow);
+    if (ACOPY) a_store(a0, pf_a0, arow);
     step_barrier();
     // step i: stage step i + 1 (A rows, B fragments) into stage (i + 1) % 2, fetch step i + 3 into the sets step i used
     for (int i = 0; i < KT; i += 3)
     {
-        a_fetch(a0, rowp, ak(i + 3));
+        if (ACOPY) a_fetch(a0, rowp, ak(i + 3));
         load_words(w0, wp(i + 3));
         decode_half<F, HALF>(w1, b_stage((i + 1) & 1), kt, 128 * th);
-        a_store(a1, a_stage((i + 1) & 1), arow);
+        if (ACOPY) a_store(a1, a_stage((i + 1) & 1), arow);
         step_barrier();
         if (i + 1 >= KT) break;
-        a_fetch(a1, rowp, ak(i + 4));
+        if (ACOPY) a_fetch(a1, rowp, ak(i + 4));
         load_words(w1, wp(i + 4));
         decode_half<F, HALF>(w2, b_stage(i & 1), kt, 128 * th);
-        a_store(a2, a_stage(i & 1), arow);
+        if (ACOPY) a_store(a2, a_stage(i & 1), arow);
         step_barrier();
         if (i + 2 >= KT) break;
-        a_fetch(a2, rowp, ak(i + 5));
+        if (ACOPY) a_fetch(a2, rowp, ak(i + 5));
         load_words(w2, wp(i + 5));
         decode_half<F, HALF>(w0, b_stage((i + 1) & 1), kt, 128 * th);
-        a_store(a0, a_stage((i + 1) & 1), arow);
+        if (ACOPY) a_store(a0, a_stage((i + 1) & 1), arow);
         step_barrier();
     }
 }
 
+// A rows are copied only where an MFMA wave reads them: the 32-row blocks that hold rows of the group
 template <int F>
 __device__ __forceinline__ void pf_decoder_any(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc)
 {
     const int d = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) - 4);
-    if (d & 1) pf_decoder<F, 1>(jb, mat_base, asrc, d);
-    else pf_decoder<F, 0>(jb, mat_base, asrc, d);
+    const bool acopy = 16 * d < (jb.nr + 31) / 32 * 32;
+    if (acopy)
+    {
+        if (d & 1) pf_decoder<F, 1, true>(jb, mat_base, asrc, d);
+        else pf_decoder<F, 0, true>(jb, mat_base, asrc, d);
+    }
+    else
+    {
+        if (d & 1) pf_decoder<F, 1, false>(jb, mat_base, asrc, d);
+        else pf_decoder<F, 0, false>(jb, mat_base, asrc, d);
+    }
 }
 
 template <bool DOWN>
@@ -554,12 +567,12 @@ struct MidPlan {
     size_t xt_bytes, part_gu_bytes, act_bytes, part_dn_bytes;
 };
 
-// k-split: the most splits that keep at least MID_MIN_STEPS k-steps each (the routing, unknown here, may put all rows
+// k-split: the most splits that keep at least 16 k-steps each (BMX_MID_MIN_STEPS) (the routing, unknown here, may put all rows
 // on a few experts; splits keep the workgroup count up then, at the price of partial sums the epilogue adds)
 static int mid_split(int ksteps)
 {
     const char* v = getenv("BMX_MID_MIN_STEPS");
-    const int min_steps = (v && *v) ? atoi(v) : 8;
+    const int min_steps = (v && *v) ? atoi(v) : 16;
     for (int d = ksteps; d > 1; --d)
         if (ksteps % d == 0 && ksteps / d >= min_steps) return d;
     return 1;
