@@ -115,7 +115,7 @@ def test_slot_copies_deliver_home_bytes(cuda):
 def test_layer_with_staged_experts_matches_resident(cuda):
     """The same layers computed with every expert resident in device memory and with homes in pinned host memory staged
     through a small slot table (hits, admissions copied on the side stream, and misses left at home when maxj runs
-    out): identical outputs, bit for bit, decode and prefill paths."""
+    out): identical outputs, bit for bit, on the GEMV, mid-size and prefill paths."""
     import bmx
     from bmx import synth
     Lyr, E, H, I, topk = 3, 24, 512, 256, 4
@@ -131,7 +131,7 @@ def test_layer_with_staged_experts_matches_resident(cuda):
         T = (1, 3, 40)[step % 3]
         x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16)).cuda()
         lg = torch.from_numpy(synth.zipf_logits(T, E, 1.1, seed=step)).cuda()
-        for path in (bmx.PATH_DECODE, bmx.PATH_PREFILL):
+        for path in (bmx.PATH_DECODE, bmx.PATH_MID, bmx.PATH_PREFILL):
             sel, w = ref_layers[li].routing_fn(T, None, x, {"logits": lg})
             want = ref_layers[li].run_bszN(x, sel, w, path)
             sel2, w2 = st_layers[li].routing_fn(T, None, x, {"logits": lg})
