@@ -1,9 +1,10 @@
 // Router and decode-size route + dispatch.
 //
-// One wavefront per token. Lane l holds experts l, l + 64, ...; each pick is a wave-wide argmax under the strict total
-// order (larger choice, then lower index): a DPP max of the order-preserving key of the value, then a DPP min of the
-// index among the lanes holding that value. The group limit picks each group's top-2 the same way, then the groups by
-// their top-2 sums. The order is the one the oracle's sequential selection produces, independent of scheduling.
+// One wavefront per token. Lane l holds experts l, l + 64, ...; the strict total order is larger choice, then lower
+// index (a 64-bit key: order-preserving value bits over the complement of the index). The group limit takes each
+// group's top-2 by wave-wide DPP maxima of the keys, then the groups by their top-2 sums; the top-k itself is a
+// bitwise search for the k-th largest value by wave ballots followed by a rank of the k picks. The order is the one
+// the oracle's sequential selection produces, independent of scheduling.
 #include "bmx_common.hpp"
 #include "bmx_internal.hpp"
 
@@ -37,6 +38,35 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t k)
     k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x142, 0xa, 0xf, false));
     k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x143, 0xc, 0xf, false));
     return __builtin_amdgcn_readlane(k, 63);
+}
+
+// wave-wide min of a uint32, the same steps as wave_umax; uniform result
+__device__ __forceinline__ uint32_t wave_umin(uint32_t k)
+{
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0xB1, 0xf, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x4E, 0xf, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x141, 0xf, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x140, 0xf, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x142, 0xa, 0xf, false));
+    k = min(k, (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)k, 0x143, 0xc, 0xf, false));
+    return __builtin_amdgcn_readlane(k, 63);
+}
+
+// float of an order-preserving key (the inverse of okey)
+__device__ __forceinline__ float unkey(uint32_t u)
+{
+    return __builtin_bit_cast(float, (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
+// the two largest of (a1 >= a2) and the pair of the lane CTRL selects
+template <int CTRL>
+__device__ __forceinline__ void top2_dpp(uint32_t& a1, uint32_t& a2)
+{
+    const uint32_t b1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a1, CTRL, 0xf, 0xf, false);
+    const uint32_t b2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a2, CTRL, 0xf, 0xf, false);
+    const uint32_t n2 = max(min(a1, b1), max(a2, b2));
+    a1 = max(a1, b1);
+    a2 = n2;
 }
 
 // Selection key of a candidate: the order-preserving key of its value above the complement of its index, so the
@@ -94,6 +124,159 @@ __device__ __forceinline__ void wave_kmax4(uint64_t (&k)[4])
         k[i] = ((uint64_t)__builtin_amdgcn_readlane(hi[i], 63) << 32) | __builtin_amdgcn_readlane(lo[i], 63);
 }
 
+// inclusive prefix sum over the wave (lane order): row shifts 1, 2, 4, 8 within rows of 16, then lane 15 into row 1 and
+// lane 47 into row 3 (row_bcast:15), lane 31 into rows 2 and 3 (row_bcast:31)
+__device__ __forceinline__ uint32_t wave_scan_add(uint32_t v)
+{
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
+    return v;
+}
+
+__device__ __forceinline__ uint64_t lanes_below() { return (1ull << (threadIdx.x & 63)) - 1ull; }
+
+// Per-wave LDS of the router.
+constexpr int TK_CAP = 128;        // candidates ranked directly; more (many equal values) take the bitwise search
+struct TopkLds {
+    union {
+        struct {
+            uint32_t lmax[64];
+            alignas(16) uint64_t ck[TK_CAP + 16];   // + room for the zero padding
+            float cs[TK_CAP];
+        };
+        uint32_t vb[RT_MAXE];                       // group limit: the value key of every expert
+    };
+    alignas(16) uint64_t gk[RT_MAXG];
+    int pick[RT_MAXK];
+    float psc[RT_MAXK];
+};
+
+// The wave's LDS writes are seen by its later LDS reads (one wave, in order); the fences keep the compiler from moving
+// accesses across the exchange.
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Top k of the candidates key[j] (sel_key; 0 = not a candidate; at least k candidates) in the order of the sequential
+// selection (larger value, then lower index). Lane r < k receives pick r and its score; the return value is the scores
+// summed in pick order.
+//
+// Let M be the k-th largest of the 64 lane maxima: k values are >= M, so every pick is >= M. The values >= M (about k
+// of them) are packed into LDS and each is ranked against the others; a step issues all its LDS reads before it waits
+// (one round trip each). When ties leave more than TK_CAP such values, the k-th largest value V is found by a bitwise
+// search over the value half of the keys (wave ballots, 32 steps), every key above V is taken and the lowest indices
+// among those equal to V fill the rest; those k are ranked the same way.
+template <int J>
+__device__ __forceinline__ float select_topk(const uint64_t (&key)[J], const float (&sc)[J], int k, TopkLds& L,
+                                             int& mypick, float& myscore)
+{
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = lanes_below();
+    uint32_t hv[J], hm = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+    {
+        hv[j] = (uint32_t)(key[j] >> 32);
+        hm = max(hm, hv[j]);
+    }
+    L.lmax[lane] = hm;
+    wave_lds_sync();
+    int above = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+    {
+        uint4 lm[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) lm[q] = reinterpret_cast<const uint4*>(L.lmax)[8 * h + q];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) above += (lm[q].x > hm) + (lm[q].y > hm) + (lm[q].z > hm) + (lm[q].w > hm);
+    }
+    const uint32_t M = wave_umin(above < k ? hm : 0xffffffffu);
+    bool sel[J];
+    int nc = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+    {
+        sel[j] = key[j] != 0ull && hv[j] >= M;
+        nc += __builtin_popcountll(__ballot(sel[j]));
+    }
+    if (nc > TK_CAP)
+    {
+        uint32_t v = 0;
+        for (int b = 31; b >= 0; --b)
+        {
+            const uint32_t cand = v | (1u << b);
+            int cnt = 0;
+#pragma unroll
+            for (int j = 0; j < J; ++j) cnt += __builtin_popcountll(__ballot(hv[j] >= cand));
+            if (cnt >= k) v = cand;
+        }
+        int need = k;
+#pragma unroll
+        for (int j = 0; j < J; ++j) need -= __builtin_popcountll(__ballot(hv[j] > v));
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+        {
+            const uint64_t meq = __ballot(hv[j] == v);
+            const int take = min(need, __builtin_popcountll(meq));
+            sel[j] = hv[j] > v || (hv[j] == v && __builtin_popcountll(meq & below) < take);
+            need -= take;
+        }
+        nc = k;
+    }
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+    {
+        const uint64_t ms = __ballot(sel[j]);
+        if (sel[j])
+        {
+            const int slot = base + __builtin_popcountll(ms & below);
+            L.ck[slot] = key[j];
+            L.cs[slot] = sc[j];
+        }
+        base += __builtin_popcountll(ms);
+    }
+    // zero keys up to a multiple of 16 (a zero key is below every candidate)
+    const int nc16 = (nc + 15) & ~15;
+    if (nc + lane < nc16) L.ck[nc + lane] = 0ull;
+    wave_lds_sync();
+    for (int c0 = 0; c0 < nc; c0 += 64)
+    {
+        const int c = c0 + lane;
+        const uint64_t my = c < nc ? L.ck[c] : ~0ull;
+        int r = 0;
+        for (int q = 0; q < nc16; q += 16)
+        {
+            ulonglong2 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const ulonglong2*>(&L.ck[q + 2 * i]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r += (v[i].x > my) + (v[i].y > my);
+        }
+        if (c < nc && r < k)
+        {
+            L.pick[r] = key_index(my);
+            L.psc[r] = L.cs[c];
+        }
+    }
+    wave_lds_sync();
+    mypick = lane < k ? L.pick[lane] : -1;
+    myscore = lane < k ? L.psc[lane] : 0.0f;
+    float vsum = 0.0f;
+    for (int q = 0; q < k; ++q)
+        vsum = __fadd_rn(vsum, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myscore), q)));
+    return vsum;
+}
+
 struct RouterArgs {
     const uint16_t* logits;
     const float* bias;
@@ -107,7 +290,7 @@ struct RouterArgs {
 // Route token t with the calling wave. Writes sel / w of the token; returns the pick of slot `lane` (lanes < topk)
 // as a local expert id (-1 otherwise). Every selection is a wave-wide max of 64-bit keys (value, then lower index).
 template <int J>
-__device__ int route_token_wave(const RouterArgs& a, int t)
+__device__ int route_token_wave(const RouterArgs& a, int t, TopkLds& L)
 {
     const int lane = threadIdx.x & 63, E = a.E;
     const uint16_t* lg = a.logits + (size_t)t * E;
@@ -146,7 +329,42 @@ __device__ int route_token_wave(const RouterArgs& a, int t)
     }
     // group limit: a group's score is the sum of its two best choices; the topk_group best groups stay eligible
     const int G = a.G, gs = E / G;
-    if (G > 1)
+    if (G >= 4 && (64 % G) == 0 && E == 64 * J)
+    {
+        // 64 / G lanes per group (lane l: group l / lpg), each reading J of the group's values from LDS; their top-2
+        // merged across the group's lanes by DPP (quad xor 1, xor 2, half-row mirror, row mirror); the groups ranked
+        // by (score, lower index) against the G scores in LDS
+        const int lpg = 64 / G, g = lane / lpg, sub = lane % lpg;
+#pragma unroll
+        for (int j = 0; j < J; ++j) L.vb[lane + 64 * j] = (uint32_t)(key[j] >> 32);
+        wave_lds_sync();
+        uint32_t v[J];
+#pragma unroll
+        for (int m = 0; m < J; ++m) v[m] = L.vb[g * gs + sub + lpg * m];
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t a1 = 0, a2 = 0;
+#pragma unroll
+        for (int m = 0; m < J; ++m)
+        {
+            a2 = max(a2, min(a1, v[m]));
+            a1 = max(a1, v[m]);
+        }
+        if (lpg >= 2) top2_dpp<0xB1>(a1, a2);
+        if (lpg >= 4) top2_dpp<0x4E>(a1, a2);
+        if (lpg >= 8) top2_dpp<0x141>(a1, a2);
+        if (lpg >= 16) top2_dpp<0x140>(a1, a2);
+        const float gsc = canon(gs >= 2 ? __fadd_rn(unkey(a1), unkey(a2)) : unkey(a1));
+        const uint64_t mine = sel_key(gsc, g);
+        if (sub == 0) L.gk[g] = mine;
+        wave_lds_sync();
+        int gr = 0;
+        for (int q = 0; q < G; ++q) gr += L.gk[q] > mine;
+        const uint64_t ok = __ballot(gr < a.TG);         // lane l: its group is eligible
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            if (!((ok >> ((lane + 64 * j) / gs * lpg)) & 1ull)) key[j] = 0;
+    }
+    else if (G > 1)
     {
         float mygsc = 0.0f;                      // lane g holds group g's score
         for (int g0 = 0; g0 < G; g0 += 4)
@@ -216,36 +434,9 @@ __device__ int route_token_wave(const RouterArgs& a, int t)
             if (e < E && !((gok >> (e / gs)) & 1ull)) key[j] = 0;
         }
     }
-    // top-k: each lane offers its best remaining key; the winner's lane clears it and offers its next
-    auto lane_best = [&](uint64_t& bk, float& bs) {
-        bk = 0;
-        bs = 0.0f;
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-        {
-            const bool tk = key[j] > bk;
-            bk = tk ? key[j] : bk;
-            bs = tk ? sc[j] : bs;
-        }
-    };
-    uint64_t bk;
-    float bs;
-    lane_best(bk, bs);
-    int mypick = -1;
-    float vsum = 0.0f, myscore = 0.0f;
-    for (int k = 0; k < a.topk; ++k)
-    {
-        const int win = key_index(wave_kmax(bk));
-        const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bs), win & 63));
-        vsum = __fadd_rn(vsum, ws);
-        if (lane == k) { mypick = win; myscore = ws; }
-        if ((win & 63) == lane)
-        {
-#pragma unroll
-            for (int j = 0; j < J; ++j) key[j] = (j == (win >> 6)) ? 0ull : key[j];
-            lane_best(bk, bs);
-        }
-    }
+    int mypick;
+    float myscore;
+    const float vsum = select_topk<J>(key, sc, a.topk, L, mypick, myscore);
     float den = 1.0f;
     if (a.score_fn == BMX_SCORE_SOFTMAX && !a.renorm)
     {
@@ -271,8 +462,9 @@ __device__ int route_token_wave(const RouterArgs& a, int t)
 template <int J>
 __global__ __launch_bounds__(RT_THREADS) void k_router(RouterArgs a)
 {
+    __shared__ TopkLds tl[RT_WAVES];
     const int t = blockIdx.x * RT_WAVES + (threadIdx.x >> 6);
-    if (t < a.T) route_token_wave<J>(a, t);
+    if (t < a.T) route_token_wave<J>(a, t, tl[threadIdx.x >> 6]);
 }
 
 // ---- fused decode kernel: route every token, then the counting sort of its picks, in one workgroup ------------------
@@ -281,11 +473,12 @@ struct SmallDispatch {
     bmx_routes r;
 };
 
-// Counting sort of at most 64 picks by one wave, without barriers: pick p in lane p; per-expert counts by LDS atomics,
-// offsets / group bases / unique ranks by one wave-wide scan over the experts, each pick's rank among its expert's
-// picks by readlane broadcasts. Same output as the workgroup version below.
-__device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, const SmallDispatch& d, int* scnt, int* soff,
-                              int* sgo, int* sui)
+// Counting sort of at most 64 picks by one wave, without barriers: pick p in lane p; per-expert counts by LDS atomics;
+// lane l takes the run of C consecutive experts from l * C (C <= JC: E <= 64 * (JC - 1) plus the shared expert), its
+// counts kept in registers; offsets / group bases / unique ranks by one DPP scan of the three run totals; each pick's
+// rank among its expert's picks by readlane broadcasts. Same output as the workgroup version below.
+template <int JC>
+__device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, const SmallDispatch& d, int* scnt, int* soff)
 {
     const int lane = threadIdx.x & 63, NE = E + (d.shared ? 1 : 0), rpg = d.rpg;
     // groups of a count: ceil(c / rpg), a shift when rpg is a power of two (every path's group size is)
@@ -293,46 +486,45 @@ __device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, cons
     const int sh = __builtin_ctz((unsigned)rpg);
     auto ngr = [&](int c) { return pow2 ? (c + rpg - 1) >> sh : (c + rpg - 1) / rpg; };
     const int e = lane < n ? pe[lane] : -1;
-    for (int x = lane; x < NE; x += 64) scnt[x] = 0;
+#pragma unroll
+    for (int i = 0; i < JC; ++i)
+        if (lane + 64 * i < NE) scnt[lane + 64 * i] = 0;
     if (lane < n && e >= 0) atomicAdd(&scnt[e], 1);
     if (d.shared && lane == 0) scnt[E] = T;
-    // each lane scans a run of C consecutive experts; run totals are scanned across the wave
     const int C = (NE + 63) / 64, x0 = lane * C;
+    int cv[JC];
     int tc = 0, tg = 0, tu = 0;
-    for (int i = 0; i < C; ++i)
-    {
-        const int x = x0 + i;
-        const int c = x < NE ? scnt[x] : 0;
-        tc += c;
-        tg += ngr(c);
-        tu += c > 0;
-    }
-    int ic = tc, ig = tg, iu = tu;                 // inclusive scans
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1)
+    for (int i = 0; i < JC; ++i)
     {
-        const int pc = __shfl_up(ic, o), pg = __shfl_up(ig, o), pu = __shfl_up(iu, o);
-        if (lane >= o) { ic += pc; ig += pg; iu += pu; }
+        cv[i] = (i < C && x0 + i < NE) ? scnt[x0 + i] : 0;
+        tc += cv[i];
+        tg += ngr(cv[i]);
+        tu += cv[i] > 0;
     }
+    // one inclusive scan of the three totals packed in 10-bit fields (n <= 64 picks and T <= 64 shared rows: every
+    // running total stays below 1024)
+    const uint32_t inc = wave_scan_add((uint32_t)tc | ((uint32_t)tg << 10) | ((uint32_t)tu << 20));
+    const int ic = inc & 1023u, ig = (inc >> 10) & 1023u, iu = inc >> 20;
     int bc = ic - tc, bg = ig - tg, bu = iu - tu;  // exclusive
-    for (int i = 0; i < C; ++i)
+#pragma unroll
+    for (int i = 0; i < JC; ++i)
     {
-        const int x = x0 + i;
-        if (x >= NE) break;
-        const int c = scnt[x];
-        soff[x] = bc;
-        sgo[x] = bg;
-        sui[x] = bu;
-        d.r.counts[x] = c;
-        d.r.offsets[x] = bc;
-        if (c > 0)
+        const int x = x0 + i, c = cv[i];
+        if (i < C && x < NE)
         {
-            d.r.uexp[bu] = x;
-            for (int q = 0; q * rpg < c; ++q)
+            soff[x] = bc;
+            d.r.counts[x] = c;
+            d.r.offsets[x] = bc;
+            if (c > 0)
             {
-                d.r.groups[3 * (bg + q) + 0] = x;
-                d.r.groups[3 * (bg + q) + 1] = bc + q * rpg;
-                d.r.groups[3 * (bg + q) + 2] = min(rpg, c - q * rpg);
+                d.r.uexp[bu] = x;
+                for (int q = 0; q * rpg < c; ++q)
+                {
+                    d.r.groups[3 * (bg + q) + 0] = x;
+                    d.r.groups[3 * (bg + q) + 1] = bc + q * rpg;
+                    d.r.groups[3 * (bg + q) + 2] = min(rpg, c - q * rpg);
+                }
             }
         }
         bc += c;
@@ -375,17 +567,18 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
 {
     __shared__ int pe[SM_MAXN];          // local expert of each pick (-1: dropped)
     __shared__ int cnt[RT_MAXE + 1];
+    __shared__ TopkLds tl[RT_WAVES];
     const int E = a.E, n = a.T * a.topk, tid = threadIdx.x, lane = tid & 63;
     for (int t = tid >> 6; t < a.T; t += RT_WAVES)
     {
-        const int pk = route_token_wave<J>(a, t);
+        const int pk = route_token_wave<J>(a, t, tl[tid >> 6]);
         if (lane < a.topk) pe[t * a.topk + lane] = pk;
     }
     if (n <= 64)
     {
-        __shared__ int soff[RT_MAXE + 1], sgo[RT_MAXE + 1], sui[RT_MAXE + 1];
+        __shared__ int soff[RT_MAXE + 1];
         if (a.T > 1) lds_barrier();          // one token: wave 0 routed it and reads its own LDS writes in order
-        if (tid < 64) dispatch_wave(pe, n, E, a.T, a.topk, d, cnt, soff, sgo, sui);
+        if (tid < 64) dispatch_wave<J + 1>(pe, n, E, a.T, a.topk, d, cnt, soff);
         return;
     }
     lds_barrier();

@@ -63,6 +63,12 @@ ROUTERS = [
     ("c2 sigmoid+bias", dict(E=288, topk=8, score=1, renorm=True, scale=2.5, n_group=1, topk_group=1, bias=True)),
     ("c3 groups", dict(E=384, topk=6, score=1, renorm=True, scale=2.5, n_group=8, topk_group=4, bias=True)),
     ("sigmoid raw", dict(E=160, topk=6, score=1, renorm=False, scale=1.0, n_group=1, topk_group=1, bias=False)),
+    # group limit: lanes per group 8 / 16 / 1 (one expert per group), and the general path (G = 3 and G = 2)
+    ("groups E256 G8", dict(E=256, topk=8, score=1, renorm=True, scale=2.5, n_group=8, topk_group=4, bias=True)),
+    ("groups E256 G4", dict(E=256, topk=8, score=1, renorm=True, scale=1.0, n_group=4, topk_group=2, bias=True)),
+    ("groups E64 G64", dict(E=64, topk=4, score=1, renorm=True, scale=1.0, n_group=64, topk_group=8, bias=True)),
+    ("groups E96 G3", dict(E=96, topk=4, score=1, renorm=True, scale=1.0, n_group=3, topk_group=2, bias=True)),
+    ("groups E128 G2", dict(E=128, topk=6, score=0, renorm=True, scale=1.0, n_group=2, topk_group=1, bias=False)),
 ]
 
 
@@ -87,6 +93,26 @@ def test_router_bitexact(cuda, oracle, name, cfg, T):
         assert np.allclose(gw.astype(np.float32), ow.astype(np.float32), rtol=2e-3)   # sum over E in parallel order
     else:
         assert np.array_equal(gw.view(np.uint16), ow.view(np.uint16))
+
+
+@pytest.mark.parametrize("name,cfg", [r for r in ROUTERS if r[0] in ("c2 sigmoid+bias", "c3 groups", "c1 softmax")],
+                         ids=["c1", "c2", "c3"])
+def test_router_ties(cuda, oracle, name, cfg):
+    """Equal values decide by lower index: every logit equal (more candidates than are ranked directly: the bitwise
+    search), runs of equal logits at the boundary, and two values only."""
+    import bmx
+    E = cfg["E"]
+    rng = np.random.default_rng(5)
+    rows = [np.full(E, 0.5), np.repeat(rng.standard_normal(E // 8), 8)[:E], np.where(np.arange(E) % 3 == 0, 1.0, -1.0),
+            np.round(rng.standard_normal(E) * 4) / 4]
+    lg = np.stack(rows).astype(np.float16)
+    say("router ties", name)
+    sel, w = bmx.ops.router_topk(torch.from_numpy(lg).to(cuda), cfg["topk"], None, cfg["n_group"], cfg["topk_group"],
+                                 cfg["score"], cfg["renorm"], cfg["scale"])
+    osel, ow = oracle.router(lg, cfg["topk"], None, cfg["n_group"], cfg["topk_group"], cfg["score"], cfg["renorm"],
+                             cfg["scale"])
+    assert np.array_equal(sel.cpu().numpy(), osel)
+    assert np.array_equal(w.cpu().numpy().view(np.uint16), ow.view(np.uint16))
 
 
 def test_router_zipf_c3(cuda, oracle):
