@@ -473,24 +473,41 @@ struct SmallDispatch {
     bmx_routes r;
 };
 
-// Counting sort of at most 64 picks by one wave, without barriers: pick p in lane p; per-expert counts by LDS atomics;
-// lane l takes the run of C consecutive experts from l * C (C <= JC: E <= 64 * (JC - 1) plus the shared expert), its
-// counts kept in registers; offsets / group bases / unique ranks by one DPP scan of the three run totals; each pick's
-// rank among its expert's picks by readlane broadcasts. Same output as the workgroup version below.
+// Counting sort of at most 256 picks of at most 64 tokens by one wave, without barriers: picks p = lane + 64 i; per
+// expert an LDS count and a bit mask of the tokens that picked it (a token picks an expert once, so the picks of an
+// expert in pick order are its tokens in order, and a pick's rank among them is the popcount of the mask below its
+// token); lane l takes the run of C consecutive experts from l * C (C <= JC: E <= 64 * (JC - 1) plus the shared expert),
+// its counts kept in registers; offsets / group bases / unique ranks by one DPP scan of the three run totals. Same
+// output as the workgroup version below.
 template <int JC>
-__device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, const SmallDispatch& d, int* scnt, int* soff)
+__device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, const SmallDispatch& d, int* scnt, int* soff,
+                              uint64_t* smask)
 {
     const int lane = threadIdx.x & 63, NE = E + (d.shared ? 1 : 0), rpg = d.rpg;
     // groups of a count: ceil(c / rpg), a shift when rpg is a power of two (every path's group size is)
     const bool pow2 = (rpg & (rpg - 1)) == 0;
     const int sh = __builtin_ctz((unsigned)rpg);
     auto ngr = [&](int c) { return pow2 ? (c + rpg - 1) >> sh : (c + rpg - 1) / rpg; };
-    const int e = lane < n ? pe[lane] : -1;
+    int ev[SM_MAXN / 64];
+#pragma unroll
+    for (int i = 0; i < SM_MAXN / 64; ++i) ev[i] = lane + 64 * i < n ? pe[lane + 64 * i] : -1;
 #pragma unroll
     for (int i = 0; i < JC; ++i)
-        if (lane + 64 * i < NE) scnt[lane + 64 * i] = 0;
-    if (lane < n && e >= 0) atomicAdd(&scnt[e], 1);
+        if (lane + 64 * i < NE)
+        {
+            scnt[lane + 64 * i] = 0;
+            smask[lane + 64 * i] = 0ull;
+        }
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < SM_MAXN / 64; ++i)
+        if (ev[i] >= 0)
+        {
+            atomicAdd(&scnt[ev[i]], 1);
+            atomicOr(reinterpret_cast<unsigned long long*>(&smask[ev[i]]), 1ull << ((lane + 64 * i) / topk));
+        }
     if (d.shared && lane == 0) scnt[E] = T;
+    wave_lds_sync();
     const int C = (NE + 63) / 64, x0 = lane * C;
     int cv[JC];
     int tc = 0, tg = 0, tu = 0;
@@ -502,7 +519,7 @@ __device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, cons
         tg += ngr(cv[i]);
         tu += cv[i] > 0;
     }
-    // one inclusive scan of the three totals packed in 10-bit fields (n <= 64 picks and T <= 64 shared rows: every
+    // one inclusive scan of the three totals packed in 10-bit fields (at most 256 picks and 64 shared rows: every
     // running total stays below 1024)
     const uint32_t inc = wave_scan_add((uint32_t)tc | ((uint32_t)tg << 10) | ((uint32_t)tu << 20));
     const int ic = inc & 1023u, ig = (inc >> 10) & 1023u, iu = inc >> 20;
@@ -537,20 +554,24 @@ __device__ void dispatch_wave(const int* pe, int n, int E, int T, int topk, cons
         *d.r.nuniq = iu;
         *d.r.ngroups = ig;
     }
+    wave_lds_sync();
     // rows of the routed picks: stable by (expert, pick)
-    int rank = 0;
-    for (int q = 0; q < n; ++q) rank += (__builtin_amdgcn_readlane(e, q) == e) && q < lane;
-    if (lane < n)
+#pragma unroll
+    for (int i = 0; i < SM_MAXN / 64; ++i)
     {
-        if (e < 0) d.r.inv[lane] = -1;
-        else
+        const int p = lane + 64 * i, e = ev[i];
+        if (p >= n) continue;
+        if (e < 0)
         {
-            const int row = soff[e] + rank;
-            d.r.inv[lane] = row;
-            d.r.row_token[row] = lane / topk;
-            d.r.row_slot[row] = lane % topk;
-            d.r.row_expert[row] = e;
+            d.r.inv[p] = -1;
+            continue;
         }
+        const int t = p / topk;
+        const int row = soff[e] + __builtin_popcountll(smask[e] & ((1ull << t) - 1ull));
+        d.r.inv[p] = row;
+        d.r.row_token[row] = t;
+        d.r.row_slot[row] = p % topk;
+        d.r.row_expert[row] = e;
     }
     if (d.shared)
         for (int t = lane; t < T; t += 64)
@@ -574,11 +595,12 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
         const int pk = route_token_wave<J>(a, t, tl[tid >> 6]);
         if (lane < a.topk) pe[t * a.topk + lane] = pk;
     }
-    if (n <= 64)
+    if (a.T <= 64)
     {
         __shared__ int soff[RT_MAXE + 1];
+        __shared__ uint64_t smask[RT_MAXE + 1];
         if (a.T > 1) lds_barrier();          // one token: wave 0 routed it and reads its own LDS writes in order
-        if (tid < 64) dispatch_wave<J + 1>(pe, n, E, a.T, a.topk, d, cnt, soff);
+        if (tid < 64) dispatch_wave<J + 1>(pe, n, E, a.T, a.topk, d, cnt, soff, smask);
         return;
     }
     lds_barrier();

@@ -69,6 +69,7 @@ ROUTERS = [
     ("groups E64 G64", dict(E=64, topk=4, score=1, renorm=True, scale=1.0, n_group=64, topk_group=8, bias=True)),
     ("groups E96 G3", dict(E=96, topk=4, score=1, renorm=True, scale=1.0, n_group=3, topk_group=2, bias=True)),
     ("groups E128 G2", dict(E=128, topk=6, score=0, renorm=True, scale=1.0, n_group=2, topk_group=1, bias=False)),
+    ("top2 E64", dict(E=64, topk=2, score=1, renorm=True, scale=1.0, n_group=1, topk_group=1, bias=True)),
 ]
 
 
@@ -167,13 +168,14 @@ def test_dispatch_bitexact(cuda, oracle, T, topk, E, shared, rpg):
 RD_CASES = [("c2 T1 shared", "c2 sigmoid+bias", 1, True, 1), ("c2 T8 shared", "c2 sigmoid+bias", 8, True, 8),
             ("c1 T1", "c1 softmax", 1, False, 1), ("c3 groups T2", "c3 groups", 2, False, 2),
             ("c3 groups T16", "c3 groups", 16, False, 8), ("c2 T32 shared", "c2 sigmoid+bias", 32, True, 8),
-            ("softmax raw T7", "softmax no renorm", 7, True, 4)]
+            ("softmax raw T7", "softmax no renorm", 7, True, 4), ("groups T64", "groups E64 G64", 64, True, 8),
+            ("top2 T100 workgroup", "top2 E64", 100, True, 8), ("top2 T128 workgroup", "top2 E64", 128, False, 1)]
 
 
 @pytest.mark.parametrize("name,router,T,shared,rpg", RD_CASES, ids=[c[0] for c in RD_CASES])
 def test_route_dispatch_bitexact(cuda, oracle, name, router, T, shared, rpg):
-    """The one-launch router + dispatch (one wave up to 64 picks, a workgroup up to 256) against the oracle's router
-    and counting sort, bit for bit."""
+    """The one-launch router + dispatch (the counting sort by one wave up to 64 tokens, by the workgroup beyond, at
+    most 256 picks) against the oracle's router and counting sort, bit for bit."""
     import bmx
     cfg = dict(ROUTERS)[router]
     rng = np.random.default_rng(100 + T)
