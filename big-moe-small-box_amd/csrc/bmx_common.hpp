@@ -42,7 +42,7 @@ template <int F> __host__ __device__ constexpr int ring_end(int i)
     return s;
 }
 
-__host__ inline int tile_bytes_of(int fmt)
+__host__ __device__ inline int tile_bytes_of(int fmt)
 {
     switch (fmt)
     {

@@ -96,6 +96,9 @@ __device__ __forceinline__ void gemv_any(int fmt, const uint8_t* mat, int tn, in
     }
 }
 
+template <int B>
+__device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint16_t* dst);
+
 // ---- split-K grouped GEMV -> partial sums ------------------------------------------------------------------------------
 // NM = 2: gate and up of the same expert on rotated x rows (the rotation is computed here, per matrix suh);
 // NM = 1: down on the rotated fp16 down-input rows. part[ks][row][cb][mat][128] (mat stride 128, cb stride NM * 128).
@@ -165,6 +168,14 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
             had128_wave(v0, v1);
             xs[(mat * MX + m) * XW + b * 64 + lane] = (uint32_t)f2h_r(v0 * R_SCALE) | ((uint32_t)f2h_r(v1 * R_SCALE) << 16);
         }
+    }
+    else if (a.act_in_down)
+    {
+        // the gate / up epilogue of the k-range's blocks, straight into LDS (one wave per row and block)
+        const int nblk = KR / 128;
+        for (int u = wave; u < nr * nblk; u += GV_WAVES)
+            gu_epi_wave<2>(a, r0 + u / nblk, k0 / 128 + u % nblk,     // two splits in flight: the GEMV's registers
+                        reinterpret_cast<uint16_t*>(xs + (u / nblk) * XW + (u % nblk) * 64));
     }
     else
     {
@@ -281,19 +292,19 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     *reinterpret_cast<u32x4*>(a.act_rows + (size_t)r * a.I + col) = pack8_r(act);
 }
 
-// Small launches: one wave per (row, 128-column block). Lane group q = lane >> 4 loads splits q, q + 4, ... at once and
-// the four groups' sums are added pairwise ((q0 + q1) + (q2 + q3)), so the k-splits cost one memory latency instead of
-// one per batch; the rest runs as in k_gu_epi (every group computes it, group 0 stores).
-__global__ __launch_bounds__(GV_THREADS) void k_gu_epi_w(GvArgs a)
+// Gate / up epilogue of row r, 128-column block cb, by one wave: its 128 fp16 down-input values go to dst (16 bytes per
+// lane of group 0, lane j at dst + 8 j: global memory or LDS). Lane group q = lane >> 4 loads splits q, q + 4, ... B at
+// a time (the sums are the same for every B) and the four groups' sums are added pairwise ((q0 + q1) + (q2 + q3)), so the k-splits cost one memory latency
+// instead of one per batch; the rest runs as in k_gu_epi (every group computes it, group 0 stores).
+template <int B>
+__device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint16_t* dst)
 {
-    const int u = blockIdx.x * GV_WAVES + (threadIdx.x >> 6), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
-    const int r = u / a.NB, cb = u % a.NB;
-    if (r >= a.R_max) return;
+    const int lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
     const int nrows = a.offsets[a.NE], e = a.row_expert[r];
     const size_t stride = (size_t)a.R_max * a.NB * 256;
     const float* p = a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j + (size_t)q * stride;
     float gu[16];
-    sum_splits<4, 4>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
+    sum_splits<4, B>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
 #pragma unroll
     for (int i = 0; i < 16; ++i) gu[i] = gu[i] + __shfl_xor(gu[i], 16);
 #pragma unroll
@@ -320,7 +331,16 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi_w(GvArgs a)
     had128_x8(act);
 #pragma unroll
     for (int i = 0; i < 8; ++i) act[i] = act[i] * R_SCALE;
-    if (q == 0) *reinterpret_cast<u32x4*>(a.act_rows + (size_t)r * a.I + col) = pack8_r(act);
+    if (q == 0) *reinterpret_cast<u32x4*>(dst + 8 * j) = pack8_r(act);
+}
+
+// Small launches: one wave per (row, 128-column block).
+__global__ __launch_bounds__(GV_THREADS) void k_gu_epi_w(GvArgs a)
+{
+    const int u = blockIdx.x * GV_WAVES + (threadIdx.x >> 6);
+    const int r = u / a.NB, cb = u % a.NB;
+    if (r >= a.R_max) return;
+    gu_epi_wave<4>(a, r, cb, a.act_rows + (size_t)r * a.I + cb * 128);
 }
 
 // down output of row r, block cb, lane's 8 columns: sum of the splits -> H128 * R * svh
@@ -513,6 +533,13 @@ int launch_epilogue(const GvArgs& a, int stage, hipStream_t s)
 }
 
 // ---- plan ------------------------------------------------------------------------------------------------------------
+// BMX_ACT_IN_DOWN=0 keeps the separate gate / up epilogue kernel for one-token calls
+static bool act_in_down_allowed()
+{
+    const char* v = getenv("BMX_ACT_IN_DOWN");
+    return !(v && *v == '0');
+}
+
 static int rows_per_group_of(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
 
 // smallest divisor d of nblk128 (so the k-range stays a whole number of 128-blocks) reaching `target` workgroups
@@ -585,7 +612,7 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
         b.filter = f;
         hipLaunchKernelGGL((k_gemv_part<MR, 2>), dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds_gu, s, b);
     }
-    if (stages & (1 << BMX_STAGE_ACT)) launch_epilogue(a, BMX_STAGE_ACT, s);
+    if ((stages & (1 << BMX_STAGE_ACT)) && !a.act_in_down) launch_epilogue(a, BMX_STAGE_ACT, s);
     if (stages & (1 << BMX_STAGE_DOWN))
         hipLaunchKernelGGL((k_gemv_part<MR, 1>), dim3((unsigned)(p.G_max * p.NBH * p.KS_dn)), dim3(GV_THREADS), lds_dn, s, a);
     if (stages & (1 << BMX_STAGE_COMBINE)) launch_epilogue(a, BMX_STAGE_COMBINE, s);
@@ -620,6 +647,12 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
     a.xt = nullptr;
     a.fresh = m.fresh;
     a.filter = 0;
+    // One-row groups (one token) with the activation and the down product in the same call and no act rows asked
+    // for: the down GEMV computes the activation of its k-range itself, once per output block instead of once, for
+    // one launch and one round trip through memory fewer. Worth it up to 16 output blocks (H <= 2048: 31.0 -> 29.6 us
+    // for a 64-expert top-8 layer of H 2048, I 768); at 32 blocks the repeated epilogue costs what it saves.
+    a.act_in_down = rows_per_group_of(m.T) == 1 && (stages & (1 << BMX_STAGE_ACT)) && (stages & (1 << BMX_STAGE_DOWN)) &&
+                    !act_rows && m.H / 128 <= 16 && act_in_down_allowed();
     switch (rows_per_group_of(m.T))
     {
         case 1: launch_mr<1>(a, p, stages, s); break;

@@ -31,6 +31,7 @@ struct GvArgs {
     uint16_t* xt;              // prefill: rotated gate / up input rows [2][R_max][H]
     const int32_t* fresh;      // [E] admitted-this-step flags of the expert-slot table, or null
     int filter;                // gate / up groups: 0 all, 1 experts not fresh, 2 fresh experts only
+    int act_in_down;           // the down GEMV computes its input rows from the gate / up partials (one-row groups)
 };
 
 // group filter of the split gate / up stages (the shared expert, index E, is never fresh)

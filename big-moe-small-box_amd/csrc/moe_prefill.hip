@@ -632,6 +632,7 @@ int launch_mid_experts(const MoeShape& m, const void* x, const bmx_routes* r, fl
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
     a.fresh = m.fresh;
     a.filter = 0;
+    a.act_in_down = 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);
@@ -691,6 +692,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
     a.fresh = m.fresh;
     a.filter = 0;
+    a.act_in_down = 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);

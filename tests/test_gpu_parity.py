@@ -354,3 +354,25 @@ def test_layer_activations(cuda, oracle, name, act, gated, limit, path):
     if (act, gated, limit) != (0, True, 0.0):
         plain = oracle.moe_forward(exps, 0, tab.host_expert(E), H, I, xs, ss, ws)
         assert rel_rms(plain, want) > 10 * REL_RMS
+
+
+@pytest.mark.parametrize("fmts,shared", [((2, 1, 3), True), ((0, 0, 0), False), ((3, 2, 1), True)])
+def test_one_token_act_in_down(cuda, fmts, shared):
+    """One token: the down GEMV computes the activation of its k-range from the gate / up partials itself. The same
+    sums as the separate epilogue kernel (BMX_ACT_IN_DOWN=0), so the outputs are bit-identical."""
+    import bmx
+    E, H, I, topk = 40, 512, 768, 6
+    tab = bmx.ExpertTable.random(H, I, E, fmts, shared=shared, seed=11, device=cuda)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(12)
+    x = torch.randn((1, H), generator=g, device=cuda).half()
+    lg = torch.randn((1, E), generator=g, device=cuda).half()
+    layer = bmx.MoELayer(tab, topk, score=bmx.SCORE_SIGMOID, renorm=True, scale=2.0)
+    say("act in down", fmts, shared)
+    a = layer.forward(x, lg, path=bmx.PATH_DECODE).cpu().numpy()
+    os.environ["BMX_ACT_IN_DOWN"] = "0"
+    try:
+        b = layer.forward(x, lg, path=bmx.PATH_DECODE).cpu().numpy()
+    finally:
+        os.environ.pop("BMX_ACT_IN_DOWN", None)
+    assert np.array_equal(a, b) and np.abs(a).max() > 0
