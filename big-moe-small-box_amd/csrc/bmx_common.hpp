@@ -142,27 +142,6 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// ---- 128-point Hadamard over a wave: lane l holds elements 2l, 2l + 1 --------------------------------------------------
-// Sylvester order, stages of span 1, 2, 4, ..., 64; at each stage the lower element of a pair becomes a + b and the upper
-// one a - b (engine/kernels/nv2/ft_core.h:90-95; the cross-lane butterfly of x16_dev.cu:31-129 adds the same pairs in
-// the same order). Results are bit-identical to the sequential form.
-__device__ __forceinline__ void had128_wave(float& v0, float& v1)
-{
-    const int lane = threadIdx.x & 63;
-    {
-        const float a = v0, b = v1;
-        v0 = a + b;
-        v1 = a - b;
-    }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1)
-    {
-        const float p0 = __shfl_xor(v0, m), p1 = __shfl_xor(v1, m);
-        if (lane & m) { v0 = p0 - v0; v1 = p1 - v1; }
-        else { v0 = v0 + p0; v1 = v1 + p1; }
-    }
-}
-
 // ---- 128-point Hadamard over 16 lanes, 8 elements per lane -------------------------------------------------------------
 // Lane j of a 16-lane row holds elements 8 j .. 8 j + 7. Same transform and rounding as had128_wave: spans 1, 2, 4 inside
 // the lane, spans 8, 16, 32, 64 between lanes j ^ 1, ^ 2, ^ 4, ^ 8 of the row (DPP, no LDS traffic). A cross-lane stage is
@@ -181,6 +160,50 @@ __device__ __forceinline__ float dpp_xor4(float v)
     int p = __builtin_amdgcn_update_dpp(b, b, 0x104, 0xf, 0x5, false);
     p = __builtin_amdgcn_update_dpp(p, b, 0x114, 0xf, 0xa, false);
     return __builtin_bit_cast(float, p);
+}
+
+// the value of lane ^ 16 / lane ^ 32, register to register (gfx950 v_permlane16_swap / v_permlane32_swap: with both
+// operands the same value, the instruction's two results hold the partner values of the two halves)
+__device__ __forceinline__ float xor16_f(float v)
+{
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    return __builtin_bit_cast(float, (uint32_t)(((threadIdx.x >> 4) & 1) ? r[0] : r[1]));
+}
+__device__ __forceinline__ float xor32_f(float v)
+{
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    return __builtin_bit_cast(float, (uint32_t)(((threadIdx.x >> 5) & 1) ? r[0] : r[1]));
+}
+
+// ---- 128-point Hadamard over a wave: lane l holds elements 2l, 2l + 1 --------------------------------------------------
+// Sylvester order, stages of span 1, 2, 4, ..., 64; at each stage the lower element of a pair becomes a + b and the upper
+// one a - b (engine/kernels/nv2/ft_core.h:90-95; the cross-lane butterfly of x16_dev.cu:31-129 adds the same pairs in
+// the same order). Results are bit-identical to the sequential form. Cross-lane partners by DPP (lane xor 1, 2, 4, 8)
+// and the permlane swaps (xor 16, 32); fma(+-1, v, partner) rounds a + b and a - b exactly as the add and the subtract.
+__device__ __forceinline__ void had128_wave(float& v0, float& v1)
+{
+    const int lane = threadIdx.x & 63;
+    {
+        const float a = v0, b = v1;
+        v0 = a + b;
+        v1 = a - b;
+    }
+    const float s1 = (lane & 1) ? -1.0f : 1.0f, s2 = (lane & 2) ? -1.0f : 1.0f, s4 = (lane & 4) ? -1.0f : 1.0f;
+    const float s8 = (lane & 8) ? -1.0f : 1.0f, s16 = (lane & 16) ? -1.0f : 1.0f, s32 = (lane & 32) ? -1.0f : 1.0f;
+    v0 = __builtin_fmaf(s1, v0, dpp_f<0xB1>(v0));
+    v1 = __builtin_fmaf(s1, v1, dpp_f<0xB1>(v1));
+    v0 = __builtin_fmaf(s2, v0, dpp_f<0x4E>(v0));
+    v1 = __builtin_fmaf(s2, v1, dpp_f<0x4E>(v1));
+    v0 = __builtin_fmaf(s4, v0, dpp_xor4(v0));
+    v1 = __builtin_fmaf(s4, v1, dpp_xor4(v1));
+    v0 = __builtin_fmaf(s8, v0, dpp_f<0x128>(v0));
+    v1 = __builtin_fmaf(s8, v1, dpp_f<0x128>(v1));
+    v0 = __builtin_fmaf(s16, v0, xor16_f(v0));
+    v1 = __builtin_fmaf(s16, v1, xor16_f(v1));
+    v0 = __builtin_fmaf(s32, v0, xor32_f(v0));
+    v1 = __builtin_fmaf(s32, v1, xor32_f(v1));
 }
 
 __device__ __forceinline__ void had128_x8(float (&v)[8])

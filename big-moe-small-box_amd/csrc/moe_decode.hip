@@ -125,7 +125,7 @@ __device__ __forceinline__ void gemv_rows(const GvArgs& a, const bmx_expert& ex,
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int m = 0; m < MR; ++m) acc[c][m] = acc[c][m] + __shfl_xor(acc[c][m], 32);
+            for (int m = 0; m < MR; ++m) acc[c][m] = acc[c][m] + xor32_f(acc[c][m]);
         if (lane < 32)
 #pragma unroll
             for (int c = 0; c < 4; ++c)
@@ -306,9 +306,9 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
     float gu[16];
     sum_splits<4, B>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + __shfl_xor(gu[i], 16);
+    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor16_f(gu[i]);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + __shfl_xor(gu[i], 32);
+    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor32_f(gu[i]);
     if (r >= nrows) return;
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const int col = cb * 128 + 8 * j;
