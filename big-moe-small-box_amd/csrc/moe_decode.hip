@@ -100,38 +100,38 @@ template <int B>
 __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint16_t* dst);
 
 // ---- split-K grouped GEMV -> partial sums ------------------------------------------------------------------------------
-// NM = 2: gate and up of the same expert on rotated x rows (the rotation is computed here, per matrix suh);
-// NM = 1: down on the rotated fp16 down-input rows. part[ks][row][cb][mat][128] (mat stride 128, cb stride NM * 128).
-// MX: the most rows a group can hold (LDS layout); the GEMV itself runs with the group's own row count rounded up to
-// 1, 2, 4 or 8, so a one-token group costs one row of dot products whatever the batch.
+// NM = 2: gate and up of the same expert on rotated x rows (the rotation is computed here, per matrix suh); waves 0-1
+// take gate and waves 2-3 up, each half of the k-range, so a wave runs one format's code. NM = 1: down on the rotated
+// fp16 down-input rows, the four waves a quarter of the k-range each. part[ks][row][cb][mat][128] (mat stride 128, cb
+// stride NM * 128). MX: the most rows a group can hold (LDS layout); the GEMV itself runs with the group's own row count
+// rounded up to 1, 2, 4 or 8, so a one-token group costs one row of dot products whatever the batch.
+constexpr int GV_WPM = GV_WAVES / 2;      // waves per matrix of the gate / up GEMV
 template <int MR, int MX, int NM>
 __device__ __forceinline__ void gemv_rows(const GvArgs& a, const bmx_expert& ex, int cb, int k0, int KR, int N,
                                           const uint32_t* xs, float* red)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, XW = KR / 2;
-    const int TRW = KR / 16 / GV_WAVES;
-    const int tr0 = k0 / 16 + wave * TRW;
+    const int WPM = NM == 2 ? GV_WPM : GV_WAVES;           // waves sharing a matrix's k-range
+    const int mat = NM == 2 ? wave / GV_WPM : 0, sub = NM == 2 ? wave % GV_WPM : wave;
+    const int mi = NM == 2 ? mat : 2;
+    const int TRW = KR / 16 / WPM;
+    const int tr0 = k0 / 16 + sub * TRW;
+    float acc[4][MR];
 #pragma unroll
-    for (int mat = 0; mat < NM; ++mat)
-    {
-        const int mi = NM == 2 ? mat : 2;
-        float acc[4][MR];
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[c][m] = 0.0f;
+    gemv_any<MR>(ex.fmt[mi], reinterpret_cast<const uint8_t*>(ex.tr[mi]), N / 16, cb, tr0, TRW, xs + mat * MX * XW, XW,
+                 k0 / 16, acc);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[c][m] = acc[c][m] + xor32_f(acc[c][m]);
+    if (lane < 32)
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int m = 0; m < MR; ++m) acc[c][m] = 0.0f;
-        gemv_any<MR>(ex.fmt[mi], reinterpret_cast<const uint8_t*>(ex.tr[mi]), N / 16, cb, tr0, TRW, xs + mat * MX * XW,
-                     XW, k0 / 16, acc);
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) acc[c][m] = acc[c][m] + xor32_f(acc[c][m]);
-        if (lane < 32)
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-#pragma unroll
-                for (int m = 0; m < MR; ++m) red[((mat * GV_WAVES + wave) * MX + m) * 128 + lane_col(lane, c)] = acc[c][m];
-    }
+            for (int m = 0; m < MR; ++m) red[(wave * MX + m) * 128 + lane_col(lane, c)] = acc[c][m];
 }
 
 template <int MX, int NM>
@@ -150,24 +150,29 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
     const int K = NM == 2 ? a.H : a.I, N = NM == 2 ? a.I : a.H;
     const int KR = K / KS, k0 = ks * KR, XW = KR / 2;
     uint32_t* xs = smem;                                           // [NM][MX][KR / 2] fp16 pairs
-    float* red = reinterpret_cast<float*>(smem + NM * MX * XW);    // [NM][GV_WAVES][MX][128]
+    float* red = reinterpret_cast<float*>(smem + NM * MX * XW);    // [GV_WAVES][MX][128] (gate / up: waves 0-1 gate)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 
     if (NM == 2)
     {
         // input rotation of each token row for gate and up: xt = RN16(H128(x * suh) * R)
+        // units (matrix, row, 128-block) in turn over the waves (counted, not divided: the index math stays scalar)
         const int nblk = KR / 128;
-        for (int u = wave; u < 2 * nr * nblk; u += GV_WAVES)
-        {
-            const int mat = u / (nr * nblk), rem = u % (nr * nblk), m = rem / nblk, b = rem % nblk;
-            const int tok = a.row_token[r0 + m];
-            const int k = k0 + b * 128 + 2 * lane;
-            const uint32_t xv = ldg(a.x + (size_t)tok * a.H + k, 0);
-            const uint32_t sv = ldg(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k, 0);
-            float v0 = h2f(xv & 0xffffu) * h2f(sv & 0xffffu), v1 = h2f(xv >> 16) * h2f(sv >> 16);
-            had128_wave(v0, v1);
-            xs[(mat * MX + m) * XW + b * 64 + lane] = (uint32_t)f2h_r(v0 * R_SCALE) | ((uint32_t)f2h_r(v1 * R_SCALE) << 16);
-        }
+        int u = 0;
+        for (int mat = 0; mat < 2; ++mat)
+            for (int m = 0; m < nr; ++m)
+                for (int b = 0; b < nblk; ++b, ++u)
+                {
+                    if ((u & (GV_WAVES - 1)) != wave) continue;
+                    const int tok = a.row_token[r0 + m];
+                    const int k = k0 + b * 128 + 2 * lane;
+                    const uint32_t xv = ldg(a.x + (size_t)tok * a.H + k, 0);
+                    const uint32_t sv = ldg(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k, 0);
+                    float v0 = h2f(xv & 0xffffu) * h2f(sv & 0xffffu), v1 = h2f(xv >> 16) * h2f(sv >> 16);
+                    had128_wave(v0, v1);
+                    xs[(mat * MX + m) * XW + b * 64 + lane] =
+                        (uint32_t)f2h_r(v0 * R_SCALE) | ((uint32_t)f2h_r(v1 * R_SCALE) << 16);
+                }
     }
     else if (a.act_in_down)
     {
@@ -198,14 +203,15 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
     else if (mr == 4) { if constexpr (MX >= 4) gemv_rows<4, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
     else { if constexpr (MX >= 8) gemv_rows<8, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
     lds_barrier();
-    // the four waves in order, then one partial per (split, row, block)
+    // the waves of a matrix in order, then one partial per (split, row, block)
     float* part = (NM == 2 ? a.part_gu : a.part_dn) + (((size_t)ks * a.R_max + r0) * NB + cb) * (NM * 128);
+    constexpr int WPM = NM == 2 ? GV_WPM : GV_WAVES;
     for (int i = threadIdx.x; i < NM * nr * 128; i += GV_THREADS)
     {
-        const int mat = i / (nr * 128), m = (i / 128) % nr, c = i % 128;
+        const int c = i & 127, mat = (i >> 7) & (NM - 1), m = i >> (NM + 6);   // i = (m * NM + mat) * 128 + c
         float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < GV_WAVES; ++w) s = s + red[((mat * GV_WAVES + w) * MX + m) * 128 + c];
+        for (int w = 0; w < WPM; ++w) s = s + red[((mat * WPM + w) * MX + m) * 128 + c];
         part[(size_t)m * NB * NM * 128 + mat * 128 + c] = s;
     }
 }
@@ -602,7 +608,7 @@ size_t decode_ws_bytes(const MoeShape& m)
 template <int MR>
 static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStream_t s)
 {
-    const size_t lds_gu = (size_t)2 * MR * (a.H / p.KS_gu) / 2 * 4 + (size_t)2 * GV_WAVES * MR * 128 * 4;
+    const size_t lds_gu = (size_t)2 * MR * (a.H / p.KS_gu) / 2 * 4 + (size_t)GV_WAVES * MR * 128 * 4;
     const size_t lds_dn = (size_t)MR * (a.I / p.KS_dn) / 2 * 4 + (size_t)GV_WAVES * MR * 128 * 4;
     for (int f = 0; f < 3; ++f)
     {
