@@ -36,7 +36,7 @@ class SlotTable(ctypes.Structure):
                 ("H", ctypes.c_int32), ("I", ctypes.c_int32),
                 ("rec", ctypes.c_int64), ("off_u", ctypes.c_int64), ("off_d", ctypes.c_int64)] + \
                [(n, _P) for n in ("slotof", "owner", "refb", "pin", "ctl", "jobs", "fresh", "stats", "home", "slot_base",
-                                  "tables")]
+                                  "tables", "pjobs", "pfl")]
 
 
 class RouterDesc(ctypes.Structure):
@@ -74,6 +74,8 @@ SIGNATURES = {
     "bmx_slot_step": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, _I64, _I, _P]),
     "bmx_slot_copy": (_I, [ctypes.POINTER(SlotTable), _I, _P]),
     "bmx_slot_copy_mats": (_I, [ctypes.POINTER(SlotTable), _I, _I, _P]),
+    "bmx_slot_prefetch": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, _I64, _I, _I, _P]),
+    "bmx_slot_prefetch_copy": (_I, [ctypes.POINTER(SlotTable), _I, _I, _I, _P]),
     "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
     "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }

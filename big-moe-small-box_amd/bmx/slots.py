@@ -5,8 +5,9 @@ engine/ec.py:16-76, copies ec_copy_k engine/ec.py:78-105 and stage_layer engine/
 Every layer keeps its experts' trellis at home (an ExpertTable, typically with its arena in pinned host memory); S
 uniform slots of the layers' record size live in VRAM. step(li, sel) runs the CLOCK step of layer li on the current
 stream (hits pinned, misses admitted, table pointers rewritten) and the copies of its admissions on a side stream;
-the layer's expert products wait for those copies only in their staged part (MoELayer.run_bszN). No host
-synchronisation anywhere."""
+the layer's expert products wait for those copies only in their staged part (MoELayer.run_bszN). prefetch(lj, guess)
+admits a later layer's guessed experts ahead of its step (the reference's layer-ahead routing guess, engine/nv2.py:
+450-487) with copies on the same side stream. No host synchronisation anywhere."""
 import ctypes
 
 import torch
@@ -35,7 +36,9 @@ class ExpertSlots:
         self.ctl = torch.zeros(4, **i32)
         self.jobs = torch.zeros(2 * max(maxj, 1), **i32)
         self.fresh = torch.zeros(self.E, **i32)
-        self.stats_t = torch.zeros(5, dtype=torch.int64, device=dev)
+        self.pjobs = torch.zeros(2 * (1 + 2 * max(maxj, 1)), **i32)
+        self.pfl = torch.zeros(max(S, 1), **i32)
+        self.stats_t = torch.zeros(8, dtype=torch.int64, device=dev)
         home = [a for t in layers for e in range(t.E) for a in t.addr[e]]
         self.home = torch.tensor(home, dtype=torch.int64, device=dev)       # uint64 addresses, int64 storage
         base = self.arena.data_ptr()
@@ -44,9 +47,12 @@ class ExpertSlots:
         P = lambda x: x.data_ptr()
         self.struct = L.SlotTable(self.L, self.E, S, maxj, t0.H, t0.I, t0.rec, t0.off_u, t0.off_d,
                                   P(self.slotof), P(self.owner), P(self.refb), P(self.pin), P(self.ctl), P(self.jobs),
-                                  P(self.fresh), P(self.stats_t), P(self.home), P(self.slot_base), P(self.tables))
+                                  P(self.fresh), P(self.stats_t), P(self.home), P(self.slot_base), P(self.tables),
+                                  P(self.pjobs), P(self.pfl))
         self.side = torch.cuda.Stream(device=dev)
         self.copied = [None] * self.L        # event: copies of the layer's last step done
+        self.pf_copied = [None, None]        # event per prefetch job buffer: its last copies done
+        self.pf_calls = 0
 
     def step(self, li, sel, first=0, admit=True):
         """CLOCK step of layer li over the picks sel (int64 device tensor) on the current stream, then the copies of
@@ -68,6 +74,35 @@ class ExpertSlots:
             evs.append(ev)
         self.copied[li] = tuple(evs)
         return evs[1]
+
+    def prefetch(self, li, guess, first=0, limit=None):
+        """Layer-ahead prefetch into layer li's slots: the first `limit` (default maxj) distinct guesses (int64 device
+        tensor, best first) that are not resident are admitted on the current stream without advancing the step counter
+        (the slots the last step pinned stay pinned) and copied on the side stream, ahead of layer li's step. A hint
+        only: layer li's next step hands the prefetched experts it uses to the staged part, so results never change."""
+        if guess.dtype != torch.int64 or not guess.is_contiguous():
+            guess = guess.long().contiguous()
+        n = guess.numel()
+        if n > 512:
+            raise ValueError("ExpertSlots.prefetch: at most 512 guesses")
+        cur = torch.cuda.current_stream()
+        b = self.pf_calls & 1
+        self.pf_calls += 1
+        if self.pf_copied[b] is not None:      # the buffer's previous copies read its jobs while they run
+            cur.wait_event(self.pf_copied[b])
+        lim = self.maxj if limit is None else int(limit)
+        L.check(L.lib().bmx_slot_prefetch(ctypes.byref(self.struct), li, ctypes.c_void_p(guess.data_ptr()), n,
+                                          int(first), lim, b, ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_prefetch")
+        admitted = torch.cuda.Event()
+        admitted.record(cur)
+        self.side.wait_event(admitted)
+        guess.record_stream(self.side)
+        L.check(L.lib().bmx_slot_prefetch_copy(ctypes.byref(self.struct), li, b, 7,
+                                               ctypes.c_void_p(self.side.cuda_stream)), "bmx_slot_prefetch_copy")
+        ev = torch.cuda.Event()
+        ev.record(self.side)
+        self.pf_copied[b] = ev
+        return ev
 
     def wait_copies(self, li, stream=None, part="all"):
         """Order `stream` (default: current) after the copies of layer li's last step: part "gate_up" (the admitted
@@ -97,5 +132,6 @@ class ExpertSlots:
         L.check(L.lib().bmx_slot_stage_async(a, b, c, n, ctypes.c_void_p(s.cuda_stream)), "bmx_slot_stage_async")
 
     def stats(self):
-        """(hits, misses, admissions, steps without a victim, evictions) (synchronises)."""
+        """(hits, misses, admissions, steps without a victim, evictions, prefetch admissions, prefetched experts used,
+        prefetched experts evicted unused) (synchronises)."""
         return tuple(int(v) for v in self.stats_t.cpu())

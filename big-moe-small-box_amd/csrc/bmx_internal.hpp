@@ -61,7 +61,9 @@ int launch_zero_i32(int32_t* p, int n, hipStream_t s);
 
 // slots.hip
 int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s);
-int launch_slot_copy(const bmx_slot_table* t, int li, int mats, hipStream_t s);
+int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
+                         hipStream_t s);
+int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStream_t s);
 
 // moe_prefill.hip (same ws / stage conventions; ws layout [xt][part_gu][act rows][part_dn])
 int prefill_rows_per_group();

@@ -15,11 +15,35 @@ struct SlotArgs {
     const int64_t* sel;
     int64_t first;
     int li, n, admit;
+    int pf;       // 0: a step; 1: a prefetch into job buffer `buf` with at most `limit` candidates
+    int limit, buf;
 };
 
 __device__ __forceinline__ int tile_bytes_dev(int fmt)
 {
     return fmt == BMX_TF_K2 ? 64 : fmt == BMX_TF_K25 ? 80 : fmt == BMX_TF_K3 ? 96 : 128;
+}
+
+// job buffer of a step (pf = 0: the step's jobs, count in ctl[2]) or of prefetch buffer b (count, then the pairs)
+__device__ __forceinline__ int32_t* prefetch_jobs(const bmx_slot_table& t, int b) { return t.pjobs + b * (1 + 2 * t.maxj); }
+
+// Ballot compaction of the flagged experts of the workgroup (thread = candidate index) into `out`, in thread order;
+// returns the total. The order within a wave is the lane order, across waves the wave order.
+__device__ __forceinline__ int compact_flags(bool flag, int value, int32_t* out, int* wave_cnt)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t b = __ballot(flag);
+    if (lane == 0) wave_cnt[wave] = __popcll(b);
+    __syncthreads();
+    int base = 0, total = 0;
+    for (int w = 0; w < SL_THREADS / 64; ++w)
+    {
+        if (w < wave) base += wave_cnt[w];
+        total += wave_cnt[w];
+    }
+    if (flag) out[base + __popcll(b & ((1ull << lane) - 1ull))] = value;
+    __syncthreads();
+    return total;
 }
 
 __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
@@ -28,66 +52,81 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     __shared__ int32_t refb[SL_MAXS];
     __shared__ uint32_t mark[16];
     __shared__ int32_t miss[512];
-    __shared__ int wave_miss[SL_THREADS / 64], wave_hit[SL_THREADS / 64];
+    __shared__ int32_t first_at[512];
+    __shared__ int wave_cnt[SL_THREADS / 64];
+    __shared__ int n_hit, n_pfused;
     const bmx_slot_table& t = a.t;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int S = t.S, E = t.E;
-    const int epoch = t.ctl[1] + 1;
+    const int epoch = t.ctl[1] + (a.pf ? 0 : 1);
     for (int s = tid; s < S; s += SL_THREADS)
     {
         pin[s] = t.pin[s];
         refb[s] = t.refb[s];
     }
     if (tid < 16) mark[tid] = 0;
+    if (tid < E) first_at[tid] = INT32_MAX;
+    if (tid == 0) n_hit = n_pfused = 0;
     __syncthreads();
-    for (int i = tid; i < a.n; i += SL_THREADS)
-    {
-        const int64_t e = a.sel[i] - a.first;
-        if (e >= 0 && e < E) atomicOr(&mark[e >> 5], 1u << (e & 31));
-    }
-    __syncthreads();
-
-    // hits: reference bit, pinned for this step; misses: compacted in ascending expert order
     int32_t* slotof = t.slotof + (size_t)a.li * E;
-    const int e = tid;
-    bool is_miss = false, is_hit = false;
-    if (e < E)
+    int nmiss;
+    if (!a.pf)
     {
-        t.fresh[e] = 0;
-        if ((mark[e >> 5] >> (e & 31)) & 1u)
+        for (int i = tid; i < a.n; i += SL_THREADS)
         {
-            const int s = slotof[e];
-            if (s >= 0)
-            {
-                refb[s] = 1;
-                pin[s] = epoch;
-                is_hit = true;
-            }
-            else is_miss = true;
+            const int64_t e = a.sel[i] - a.first;
+            if (e >= 0 && e < E) atomicOr(&mark[e >> 5], 1u << (e & 31));
         }
+        __syncthreads();
+        // hits: reference bit, pinned for this step (the first use of a prefetched slot counts and marks the expert
+        // fresh: its copy may still be in flight); misses: compacted in ascending expert order
+        const int e = tid;
+        bool is_miss = false;
+        if (e < E)
+        {
+            int fr = 0;
+            if ((mark[e >> 5] >> (e & 31)) & 1u)
+            {
+                const int s = slotof[e];
+                if (s >= 0)
+                {
+                    refb[s] = 1;
+                    pin[s] = epoch;
+                    atomicAdd(&n_hit, 1);
+                    if (t.pfl[s])
+                    {
+                        t.pfl[s] = 0;
+                        fr = 1;
+                        atomicAdd(&n_pfused, 1);
+                    }
+                }
+                else is_miss = true;
+            }
+            t.fresh[e] = fr;
+        }
+        nmiss = compact_flags(is_miss, e, miss, wave_cnt);
     }
-    const uint64_t bm = __ballot(is_miss), bh = __ballot(is_hit);
-    if (lane == 0)
+    else
     {
-        wave_miss[wave] = __popcll(bm);
-        wave_hit[wave] = __popcll(bh);
+        // prefetch candidates: the first occurrence of each in-range expert, if not resident, in the order given
+        int64_t e = -1;
+        if (tid < a.n)
+        {
+            e = a.sel[tid] - a.first;
+            if (e >= 0 && e < E) atomicMin(&first_at[e], tid);
+            else e = -1;
+        }
+        __syncthreads();
+        const bool cand = e >= 0 && first_at[e] == tid && slotof[e] < 0;
+        nmiss = min(compact_flags(cand, (int)e, miss, wave_cnt), a.limit);
     }
-    __syncthreads();
-    int base = 0, nmiss = 0, nhit = 0;
-    for (int w = 0; w < SL_THREADS / 64; ++w)
-    {
-        if (w < wave) base += wave_miss[w];
-        nmiss += wave_miss[w];
-        nhit += wave_hit[w];
-    }
-    if (is_miss) miss[base + __popcll(bm & ((1ull << lane) - 1ull))] = e;
-    __syncthreads();
 
     // admissions: one wave sweeps the CLOCK hand 64 slots at a time. Within a chunk every slot is probed once, so taking
     // the first candidate and clearing the reference bits of the unpinned slots before it is the sequential sweep.
     if (wave == 0)
     {
-        int hand = t.ctl[0], nj = 0, novictim = 0, evicted = 0;
+        int32_t* jobs = a.pf ? prefetch_jobs(t, a.buf) + 1 : t.jobs;
+        int hand = t.ctl[0], nj = 0, novictim = 0, evicted = 0, wasted = 0;
         const int chunk = S < 64 ? S : 64;
         for (int k = 0; a.admit && S > 0 && k < nmiss && nj < t.maxj; ++k)
         {
@@ -118,7 +157,7 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
             }
             if (found < 0)
             {
-                novictim = 1;
+                novictim = a.pf ? 0 : 1;
                 break;
             }
             if (lane == 0)
@@ -134,32 +173,44 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                     tab[oe].tr[1] = h[1];
                     tab[oe].tr[2] = h[2];
                     ++evicted;
+                    wasted += t.pfl[s];
                 }
                 t.owner[s] = a.li * E + ex;
                 slotof[ex] = s;
                 refb[s] = 1;
                 pin[s] = epoch;
+                t.pfl[s] = a.pf;
                 bmx_expert* tab = reinterpret_cast<bmx_expert*>(t.tables[a.li]);
                 const uint64_t b = t.slot_base[s];
                 tab[ex].tr[0] = b;
                 tab[ex].tr[1] = b + (uint64_t)t.off_u;
                 tab[ex].tr[2] = b + (uint64_t)t.off_d;
-                t.jobs[2 * nj] = ex;
-                t.jobs[2 * nj + 1] = s;
-                t.fresh[ex] = 1;
+                jobs[2 * nj] = ex;
+                jobs[2 * nj + 1] = s;
+                if (!a.pf) t.fresh[ex] = 1;
             }
             ++nj;
         }
         if (lane == 0)
         {
             if (a.admit && S > 0) t.ctl[0] = hand;
-            t.ctl[1] = epoch;
-            t.ctl[2] = nj;
-            t.stats[0] += nhit;
-            t.stats[1] += nmiss;
-            t.stats[2] += nj;
-            t.stats[3] += novictim;
+            if (a.pf)
+            {
+                prefetch_jobs(t, a.buf)[0] = nj;
+                t.stats[5] += nj;
+            }
+            else
+            {
+                t.ctl[1] = epoch;
+                t.ctl[2] = nj;
+                t.stats[0] += n_hit;
+                t.stats[1] += nmiss;
+                t.stats[2] += nj;
+                t.stats[3] += novictim;
+                t.stats[6] += n_pfused;
+            }
             t.stats[4] += evicted;
+            t.stats[7] += wasted;
         }
     }
     __syncthreads();
@@ -170,13 +221,14 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     }
 }
 
-// copies of the last step's admissions: blockIdx.y = job; the matrices in `mats` (bit 0 gate, 1 up, 2 down); 16-byte
-// chunks, grid-stride
-__global__ __launch_bounds__(256) void k_slot_copy(bmx_slot_table t, int li, int mats)
+// copies of the last step's admissions (buf < 0) or of prefetch buffer buf: blockIdx.y = job; the matrices in `mats`
+// (bit 0 gate, 1 up, 2 down); 16-byte chunks, grid-stride
+__global__ __launch_bounds__(256) void k_slot_copy(bmx_slot_table t, int li, int mats, int buf)
 {
     const int j = blockIdx.y;
-    if (j >= t.ctl[2]) return;
-    const int e = t.jobs[2 * j], s = t.jobs[2 * j + 1];
+    const int32_t* jobs = buf < 0 ? t.jobs : prefetch_jobs(t, buf) + 1;
+    if (j >= (buf < 0 ? t.ctl[2] : jobs[-1])) return;
+    const int e = jobs[2 * j], s = jobs[2 * j + 1];
     const bmx_expert& ex = reinterpret_cast<const bmx_expert*>(t.tables[li])[e];
     const size_t tiles = (size_t)t.H * t.I / 256;
     const uint64_t b = t.slot_base[s];
@@ -212,7 +264,7 @@ static int check_table(const bmx_slot_table* t, const char* who)
     if (t->H <= 0 || t->I <= 0 || t->H % 16 || t->I % 16 || t->rec <= 0 || t->rec % 16 || t->off_u % 16 || t->off_d % 16)
         return set_error(BMX_ERR_ARG, "%s: bad geometry", who);
     if (!t->slotof || !t->owner || !t->refb || !t->pin || !t->ctl || !t->jobs || !t->fresh || !t->stats || !t->home ||
-        !t->slot_base || !t->tables)
+        !t->slot_base || !t->tables || !t->pjobs || !t->pfl)
         return set_error(BMX_ERR_ARG, "%s: null table array", who);
     return BMX_OK;
 }
@@ -229,19 +281,46 @@ int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n,
     a.li = li;
     a.n = n;
     a.admit = admit ? 1 : 0;
+    a.pf = 0;
+    a.limit = 0;
+    a.buf = 0;
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
     return check_launch("bmx_slot_step");
 }
 
-int launch_slot_copy(const bmx_slot_table* t, int li, int mats, hipStream_t s)
+int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
+                         hipStream_t s)
 {
-    int rc = check_table(t, "bmx_slot_copy");
+    int rc = check_table(t, "bmx_slot_prefetch");
     if (rc) return rc;
-    if (li < 0 || li >= t->L) return set_error(BMX_ERR_ARG, "bmx_slot_copy: bad layer");
-    if (mats < 0 || mats > 7) return set_error(BMX_ERR_ARG, "bmx_slot_copy: bad matrix mask %d", mats);
+    if (li < 0 || li >= t->L || n < 0 || n > SL_THREADS || (n && !sel))
+        return set_error(BMX_ERR_ARG, "bmx_slot_prefetch: bad layer or guesses (n <= %d)", SL_THREADS);
+    if (buf < 0 || buf > 1 || limit < 0) return set_error(BMX_ERR_ARG, "bmx_slot_prefetch: bad buffer %d or limit %d", buf, limit);
+    SlotArgs a;
+    a.t = *t;
+    a.sel = sel;
+    a.first = first;
+    a.li = li;
+    a.n = n;
+    a.admit = 1;
+    a.pf = 1;
+    a.limit = limit;
+    a.buf = buf;
+    hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
+    return check_launch("bmx_slot_prefetch");
+}
+
+int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStream_t s)
+{
+    const char* who = buf < 0 ? "bmx_slot_copy" : "bmx_slot_prefetch_copy";
+    int rc = check_table(t, who);
+    if (rc) return rc;
+    if (li < 0 || li >= t->L) return set_error(BMX_ERR_ARG, "%s: bad layer", who);
+    if (mats < 0 || mats > 7) return set_error(BMX_ERR_ARG, "%s: bad matrix mask %d", who, mats);
+    if (buf > 1) return set_error(BMX_ERR_ARG, "%s: bad buffer %d", who, buf);
     if (t->maxj == 0 || mats == 0) return BMX_OK;
-    hipLaunchKernelGGL(k_slot_copy, dim3(64, (unsigned)t->maxj), dim3(256), 0, s, *t, li, mats);
-    return check_launch("bmx_slot_copy");
+    hipLaunchKernelGGL(k_slot_copy, dim3(64, (unsigned)t->maxj), dim3(256), 0, s, *t, li, mats, buf);
+    return check_launch(who);
 }
 
 }  // namespace bmx
@@ -258,12 +337,24 @@ int bmx_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, in
 
 int bmx_slot_copy(const bmx_slot_table* t, int li, bmx_stream_t stream)
 {
-    return launch_slot_copy(t, li, 7, static_cast<hipStream_t>(stream));
+    return launch_slot_copy(t, li, 7, -1, static_cast<hipStream_t>(stream));
 }
 
 int bmx_slot_copy_mats(const bmx_slot_table* t, int li, int mats, bmx_stream_t stream)
 {
-    return launch_slot_copy(t, li, mats, static_cast<hipStream_t>(stream));
+    return launch_slot_copy(t, li, mats, -1, static_cast<hipStream_t>(stream));
+}
+
+int bmx_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
+                      bmx_stream_t stream)
+{
+    return launch_slot_prefetch(t, li, sel, n, first, limit, buf, static_cast<hipStream_t>(stream));
+}
+
+int bmx_slot_prefetch_copy(const bmx_slot_table* t, int li, int buf, int mats, bmx_stream_t stream)
+{
+    if (buf < 0) return set_error(BMX_ERR_ARG, "bmx_slot_prefetch_copy: bad buffer %d", buf);
+    return launch_slot_copy(t, li, mats, buf, static_cast<hipStream_t>(stream));
 }
 
 int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream)

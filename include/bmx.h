@@ -200,11 +200,15 @@ typedef struct bmx_slot_table {
     int32_t* pin;               /* [S] step counter value of the slot's last use; < 0 = slot disabled */
     int32_t* ctl;               /* [4] CLOCK hand, step counter, admissions of the last step, reserved */
     int32_t* jobs;              /* [2 * maxj] (expert, slot) of each admission of the last step */
-    int32_t* fresh;             /* [E] 1 = admitted by the last step (for bmx_moe_desc.fresh of that layer) */
-    int64_t* stats;             /* [5] running hits, misses, admissions, steps without a victim, evictions */
+    int32_t* fresh;             /* [E] 1 = admitted by the last step, or a prefetched expert the step used for the first
+                                   time (for bmx_moe_desc.fresh of that layer) */
+    int64_t* stats;             /* [8] running hits, misses, admissions, steps without a victim, evictions, prefetch
+                                   admissions, prefetched experts used by a step, prefetched experts evicted unused */
     const uint64_t* home;       /* [L * E * 3] device-visible address of each expert's gate, up, down trellis */
     const uint64_t* slot_base;  /* [S] address of each slot */
     const uint64_t* tables;     /* [L] address of each layer's bmx_expert table (E entries) */
+    int32_t* pjobs;             /* [2 * (1 + 2 * maxj)] two prefetch job buffers: count, then (expert, slot) pairs */
+    int32_t* pfl;               /* [S] 1 = admitted by a prefetch and not used by a step since (caller zeroes) */
 } bmx_slot_table;
 
 /* One step of layer li over the picks sel[n] (global ids, local = id - first): the layer's picked experts that are
@@ -212,8 +216,10 @@ typedef struct bmx_slot_table {
  * ascending expert order, at most maxj, each into the first slot from the CLOCK hand that is enabled, not pinned this
  * step and whose reference bit is clear (bits of slots passed over are cleared; at most 2 S probes per miss, a miss that
  * finds none ends the step's admissions). An admission evicts the slot's previous expert (its table entry back to its
- * home), points the admitted expert's entry at the slot, and writes a job; fresh marks the admitted experts. One
- * workgroup; no host synchronisation. Misses that are not admitted run from their home. */
+ * home), points the admitted expert's entry at the slot, and writes a job; fresh marks the admitted experts and the hits
+ * on slots a prefetch filled that no step has used yet (their copies may still be in flight, so the layer computes
+ * them with its admissions, after the copies). One workgroup; no host synchronisation. Misses that are not admitted run
+ * from their home. */
 int bmx_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit,
                   bmx_stream_t stream);
 /* The copies of the last step's jobs of layer li, home -> slot (a kernel reading the home directly: pinned host memory
@@ -224,6 +230,19 @@ int bmx_slot_copy(const bmx_slot_table* t, int li, bmx_stream_t stream);
  * when those two have landed while the down matrices are still in flight (the reference copies whole slots,
  * engine/ec.py:78-105). */
 int bmx_slot_copy_mats(const bmx_slot_table* t, int li, int mats, bmx_stream_t stream);
+/* Layer-ahead prefetch (the reference's next-layer routing guess, engine/nv2.py:450-487, whose picks it hands on as
+ * prefetch hints, engine/kernels/nv2/nv2_dev.cu:75-85 and nv2_host.cpp:1046-1056): the first `limit` distinct guesses
+ * sel[n] (n <= 512, best first, ids outside [first, first + E) ignored) that are not resident in layer li are admitted
+ * in that order, at most maxj, by the step's CLOCK sweep within the current step counter (slots the last step pinned
+ * stay pinned and the counter does not advance; hits and reference bits of resident guesses are left alone). Jobs go to
+ * prefetch buffer buf (0 or 1), never to the step's, so the copies of the last step may still be in flight. Stream
+ * order: after the step of the layer being computed; the copies (bmx_slot_prefetch_copy) on the same side stream as
+ * the step copies, before the next step's copies; the next prefetch into the same buffer after those copies. A
+ * prefetch never changes a result: the layer's next step hands its prefetched hits to the staged part (fresh). */
+int bmx_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
+                      bmx_stream_t stream);
+/* The copies of prefetch buffer buf's jobs of layer li (matrices in mats, as bmx_slot_copy_mats). */
+int bmx_slot_prefetch_copy(const bmx_slot_table* t, int li, int buf, int mats, bmx_stream_t stream);
 /* Host-planned staging: n copies src[i] -> dst[i] of bytes[i] (hipMemcpyAsync, e.g. pinned host -> slot), in order on
  * stream (the reference's stage_layer, engine/kernels/nv2/nv2_host.cpp:1558-1593). */
 int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream);

@@ -566,13 +566,59 @@ int bmxo_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int
  * them with a shared-memory atomicAdd, so its order is unspecified): hit -> refb = 1, pin = epoch; per miss the hand
  * skips slots pinned this epoch or disabled (pin < 0), clears set reference bits, and takes the first clear slot within
  * 2 S steps; the victim's owner goes back home (slotof = -1). */
+/* the CLOCK admission of the misses miss[nmiss] of layer li (ec_step_k, engine/ec.py:40-76, with misses taken in the
+ * order given): each takes the first slot from the hand that is enabled, not pinned in `epoch` and whose reference bit is
+ * clear, clearing the bits it passes; a miss that finds none in 2 S probes ends the admissions. */
+static int clock_admit(bmxo_slots* t, int li, const int* miss, int nmiss, int maxj, int epoch, int pf, int32_t* jobs,
+                       int32_t* evicted, int32_t* fresh, int64_t* stats)
+{
+    const int E = t->E, S = t->S;
+    int nj = 0, hand = t->hand;
+    for (int k = 0; k < nmiss && nj < maxj; ++k)
+    {
+        const int e = miss[k];
+        int found = -1;
+        for (int step = 0; step < 2 * S; ++step)
+        {
+            const int s = hand;
+            hand = (hand + 1 == S) ? 0 : hand + 1;
+            if (t->pin[s] == epoch || t->pin[s] < 0) continue;
+            if (t->refb[s]) { t->refb[s] = 0; continue; }
+            found = s;
+            break;
+        }
+        if (found < 0) { if (!pf) stats[3] += 1; break; }
+        const int s = found, old = t->owner[s];
+        if (old >= 0)
+        {
+            t->slotof[old] = -1;
+            stats[4] += 1;
+            if (t->pfl[s]) stats[7] += 1;
+        }
+        evicted[nj] = old;
+        t->owner[s] = li * E + e;
+        t->slotof[(size_t)li * E + e] = s;
+        t->refb[s] = 1;
+        t->pin[s] = epoch;
+        t->pfl[s] = pf;
+        if (fresh) fresh[e] = 1;
+        jobs[2 * nj] = e;
+        jobs[2 * nj + 1] = s;
+        ++nj;
+        stats[pf ? 5 : 2] += 1;
+    }
+    t->hand = hand;
+    return nj;
+}
+
 int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int admit, int maxj, int32_t* jobs,
-                   int32_t* evicted, int64_t* stats)
+                   int32_t* evicted, int32_t* fresh, int64_t* stats)
 {
     const int E = t->E, S = t->S;
     unsigned char* mark = (unsigned char*)calloc((size_t)E, 1);
     int* miss = (int*)malloc((size_t)E * sizeof(int));
     const int epoch = ++t->epoch;
+    if (fresh) memset(fresh, 0, (size_t)E * sizeof(int32_t));
     for (int i = 0; i < n; ++i)
     {
         const int64_t e = sel[i] - first;
@@ -584,43 +630,45 @@ int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t fir
     {
         if (!mark[e]) continue;
         const int s = slotof[e];
-        if (s >= 0) { t->refb[s] = 1; t->pin[s] = epoch; ++nhit; }
+        if (s >= 0)
+        {
+            t->refb[s] = 1;
+            t->pin[s] = epoch;
+            ++nhit;
+            if (t->pfl[s])             /* first use of a prefetched expert: its copy may still be in flight */
+            {
+                t->pfl[s] = 0;
+                stats[6] += 1;
+                if (fresh) fresh[e] = 1;
+            }
+        }
         else miss[nmiss++] = e;
     }
     stats[0] += nhit;
     stats[1] += nmiss;
-    if (admit && S > 0)
-    {
-        int hand = t->hand;
-        for (int k = 0; k < nmiss && nj < maxj; ++k)
-        {
-            const int e = miss[k];
-            int found = -1;
-            for (int step = 0; step < 2 * S; ++step)
-            {
-                const int s = hand;
-                hand = (hand + 1 == S) ? 0 : hand + 1;
-                if (t->pin[s] == epoch || t->pin[s] < 0) continue;
-                if (t->refb[s]) { t->refb[s] = 0; continue; }
-                found = s;
-                break;
-            }
-            if (found < 0) { stats[3] += 1; break; }
-            const int s = found, old = t->owner[s];
-            if (old >= 0) { t->slotof[old] = -1; stats[4] += 1; }
-            evicted[nj] = old;
-            t->owner[s] = li * E + e;
-            slotof[e] = s;
-            t->refb[s] = 1;
-            t->pin[s] = epoch;
-            jobs[2 * nj] = e;
-            jobs[2 * nj + 1] = s;
-            ++nj;
-            stats[2] += 1;
-        }
-        t->hand = hand;
-    }
+    if (admit && S > 0) nj = clock_admit(t, li, miss, nmiss, maxj, epoch, 0, jobs, evicted, fresh, stats);
     free(mark);
     free(miss);
+    return nj;
+}
+
+int bmxo_slot_prefetch(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int limit, int maxj,
+                       int32_t* jobs, int32_t* evicted, int64_t* stats)
+{
+    const int E = t->E;
+    unsigned char* seen = (unsigned char*)calloc((size_t)E, 1);
+    int* cand = (int*)malloc((size_t)E * sizeof(int));
+    int nc = 0;
+    for (int i = 0; i < n && nc < limit; ++i)
+    {
+        const int64_t e = sel[i] - first;
+        if (e < 0 || e >= E || seen[e]) continue;
+        seen[e] = 1;
+        if (t->slotof[(size_t)li * E + e] < 0) cand[nc++] = (int)e;
+    }
+    int nj = 0;
+    if (t->S > 0) nj = clock_admit(t, li, cand, nc, maxj, t->epoch, 1, jobs, evicted, NULL, stats);
+    free(seen);
+    free(cand);
     return nj;
 }

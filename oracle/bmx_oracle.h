@@ -88,12 +88,19 @@ typedef struct {
     int32_t* owner;    /* [S], li * E + e or -1 */
     int32_t* refb;     /* [S] */
     int32_t* pin;      /* [S], epoch of the last use; < 0 = slot disabled */
+    int32_t* pfl;      /* [S], 1 = admitted by a prefetch and not used by a step since */
     int32_t hand, epoch;
 } bmxo_slots;
 /* returns the number of admission jobs written to jobs[2 * j] = e, jobs[2 * j + 1] = slot, evicted[j] = old owner or -1.
- * stats[0..4] += hits, misses, admitted, no_victim, evictions */
+ * fresh [E] (or NULL) = 1 for the experts admitted by this step and for the hits on prefetched slots.
+ * stats[0..7] += hits, misses, admitted, no_victim, evictions, (prefetch:) admitted, used, evicted unused */
 int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int admit, int maxj, int32_t* jobs,
-                   int32_t* evicted, int64_t* stats);
+                   int32_t* evicted, int32_t* fresh, int64_t* stats);
+/* layer-ahead prefetch into layer li's slots: the first `limit` distinct in-range picks of sel[n] (rank order) that are
+ * not resident are admitted in that order, at most maxj, by the same CLOCK sweep as a step but within the current epoch
+ * (slots pinned by the last step stay pinned; the epoch does not advance); hits and hit bits are left alone. */
+int bmxo_slot_prefetch(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int limit, int maxj,
+                       int32_t* jobs, int32_t* evicted, int64_t* stats);
 
 #ifdef __cplusplus
 }

@@ -66,8 +66,10 @@ def lib():
         L.bmxo_router.argtypes = [_P, _P, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, ctypes.c_int64, _P, _P]
         L.bmxo_dispatch.argtypes = [_P, _I, _I, _I, ctypes.c_int64, _I, _P, _P, _P, _P, _P, _P]
         L.bmxo_dispatch.restype = _I
-        L.bmxo_slot_step.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _I, _I, _P, _P, _P]
+        L.bmxo_slot_step.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _I, _I, _P, _P, _P, _P]
         L.bmxo_slot_step.restype = _I
+        L.bmxo_slot_prefetch.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _I, _I, _P, _P, _P]
+        L.bmxo_slot_prefetch.restype = _I
         _lib = L
     return _lib
 
@@ -202,12 +204,14 @@ def dispatch(sel, E, first=0, shared=False):
 
 
 class _Slots(ctypes.Structure):
-    _fields_ = [("L", _I), ("E", _I), ("S", _I), ("slotof", _P), ("owner", _P), ("refb", _P), ("pin", _P),
+    _fields_ = [("L", _I), ("E", _I), ("S", _I), ("slotof", _P), ("owner", _P), ("refb", _P), ("pin", _P), ("pfl", _P),
                 ("hand", ctypes.c_int32), ("epoch", ctypes.c_int32)]
 
 
 class SlotTable:
-    """The oracle's CLOCK expert-slot table (numpy state, C step)."""
+    """The oracle's CLOCK expert-slot table (numpy state, C step and prefetch).
+    stats: hits, misses, admissions, steps without a victim, evictions, prefetch admissions, prefetched experts used by a
+    step, prefetched experts evicted unused."""
 
     def __init__(self, L, E, S):
         self.L, self.E, self.S = L, E, S
@@ -215,9 +219,11 @@ class SlotTable:
         self.owner = np.full(max(S, 1), -1, np.int32)
         self.refb = np.zeros(max(S, 1), np.int32)
         self.pin = np.zeros(max(S, 1), np.int32)
-        self.stats = np.zeros(5, np.int64)
+        self.pfl = np.zeros(max(S, 1), np.int32)
+        self.stats = np.zeros(8, np.int64)
+        self.fresh = np.zeros(E, np.int32)
         self._s = _Slots(L, E, S, self.slotof.ctypes.data, self.owner.ctypes.data, self.refb.ctypes.data,
-                         self.pin.ctypes.data, 0, 0)
+                         self.pin.ctypes.data, self.pfl.ctypes.data, 0, 0)
 
     @property
     def hand(self):
@@ -228,11 +234,20 @@ class SlotTable:
         return self._s.epoch
 
     def step(self, li, sel, first=0, admit=True, maxj=1024):
+        """Returns (jobs [nj, 2] = (expert, slot), evicted owners [nj]); self.fresh is the step's fresh flags."""
         sel = _c(sel, np.int64).ravel()
         jobs = np.zeros(2 * maxj, np.int32)
         ev = np.zeros(maxj, np.int32)
         nj = lib().bmxo_slot_step(ctypes.byref(self._s), li, _p(sel), sel.size, first, int(admit), maxj, _p(jobs),
-                                  _p(ev), _p(self.stats))
+                                  _p(ev), _p(self.fresh), _p(self.stats))
+        return jobs[:2 * nj].reshape(nj, 2), ev[:nj]
+
+    def prefetch(self, li, sel, first=0, limit=1 << 30, maxj=1024):
+        sel = _c(sel, np.int64).ravel()
+        jobs = np.zeros(2 * maxj, np.int32)
+        ev = np.zeros(maxj, np.int32)
+        nj = lib().bmxo_slot_prefetch(ctypes.byref(self._s), li, _p(sel), sel.size, first, min(limit, 1 << 30), maxj,
+                                      _p(jobs), _p(ev), _p(self.stats))
         return jobs[:2 * nj].reshape(nj, 2), ev[:nj]
 
 

@@ -44,6 +44,7 @@ def check_state(slots, ref, fresh_want, step):
     assert ctl[0] == ref.hand and ctl[1] == ref.epoch, (step, ctl, ref.hand, ref.epoch)
     assert np.array_equal(slots.stats_t.cpu().numpy(), ref.stats), (step, slots.stats_t.cpu().numpy(), ref.stats)
     assert np.array_equal(slots.fresh.cpu().numpy(), fresh_want), step
+    assert np.array_equal(slots.pfl.cpu().numpy()[:S], ref.pfl[:S]), step
     # every table entry points at its slot when resident, at its home otherwise
     tr = tables_of(slots)
     base = slots.arena.data_ptr()
@@ -76,10 +77,50 @@ def test_slot_step_matches_oracle(cuda, oracle, S, maxj, disabled):
         jobs, ev = ref.step(li, sel.astype(np.int64), first, admit, maxj)
         fresh_want = np.zeros(E, np.int32)
         fresh_want[jobs[:, 0]] = 1
+        assert np.array_equal(ref.fresh, fresh_want)          # no prefetches here: fresh = the admissions
         check_state(slots, ref, fresh_want, step)
         nj = int(slots.ctl[2].item())
         assert nj == len(jobs)
         assert np.array_equal(slots.jobs.cpu().numpy()[:2 * nj].reshape(nj, 2), jobs)
+
+
+@pytest.mark.parametrize("S,maxj", [(10, 4), (6, 8), (0, 2)])
+def test_slot_prefetch_matches_oracle(cuda, oracle, S, maxj):
+    """Steps and layer-ahead prefetches interleaved (guesses with duplicates, resident experts, ids out of range, limits):
+    slot state, prefetch job buffers, fresh flags and counters bit-exact against the oracle after every call."""
+    import bmx
+    Lyr, E = 3, 20
+    layers = small_layers(Lyr, E, 256, 128, 20, "device")
+    slots = bmx.ExpertSlots(layers, S, maxj=maxj, disabled=(2,) if S else ())
+    ref = oracle.SlotTable(Lyr, E, S)
+    if S:
+        ref.pin[2] = -1
+    rng = np.random.default_rng(S * 10 + maxj)
+    first = 3
+    fresh_want = np.zeros(E, np.int32)
+    for it in range(60):
+        li = int(rng.integers(0, Lyr))
+        if rng.random() < 0.5:
+            sel = rng.integers(0, E + 2, int(rng.integers(0, 10))) + first - 1
+            say("slot step", it, "layer", li, "picks", sel.size)
+            slots.step(li, torch.from_numpy(sel.astype(np.int64)).cuda(), first)
+            jobs, _ = ref.step(li, sel.astype(np.int64), first, True, maxj)
+            fresh_want = ref.fresh.copy()
+        else:
+            g = rng.integers(0, E + 2, int(rng.integers(0, 16))) + first - 1
+            limit = int(rng.integers(0, 6))
+            b = slots.pf_calls & 1
+            say("slot prefetch", it, "layer", li, "guesses", g.size, "limit", limit, "buffer", b)
+            slots.prefetch(li, torch.from_numpy(g.astype(np.int64)).cuda(), first, limit)
+            jobs, _ = ref.prefetch(li, g.astype(np.int64), first, limit, maxj)
+            torch.cuda.synchronize()
+            pj = slots.pjobs.cpu().numpy()[b * (1 + 2 * maxj):]
+            assert pj[0] == len(jobs) and np.array_equal(pj[1:1 + 2 * len(jobs)].reshape(-1, 2), jobs), it
+        check_state(slots, ref, fresh_want, it)
+    st = ref.stats
+    say("oracle stats", st.tolist())
+    if S:
+        assert st[5] > 0 and st[6] > 0
 
 
 def test_slot_copies_deliver_home_bytes(cuda):
@@ -140,8 +181,44 @@ def test_layer_with_staged_experts_matches_resident(cuda):
             torch.cuda.synchronize()
             say("staged layer step", step, "layer", li, "T", T, "path", path, "stats", slots.stats())
             assert torch.equal(sel, sel2) and torch.equal(got, want)
-    h, m, adm, novic, ev = slots.stats()
+    h, m, adm, novic, ev = slots.stats()[:5]
     assert m > 0 and adm > 0 and ev > 0 and m > adm      # misses, admissions, evictions and unadmitted misses all ran
+
+
+def test_prefetch_keeps_outputs(cuda):
+    """A decode loop over a stack of layers with homes in pinned host memory, each layer's step followed by a prefetch
+    of the next layer's guessed experts (its router on noisy logits: right and wrong guesses) before the layer's
+    products: outputs identical, bit for bit, to the same layers with every expert resident; prefetched experts are
+    used and some are evicted unused."""
+    import bmx
+    from bmx import synth
+    Lyr, E, H, I, topk = 4, 24, 512, 256, 4
+    dev_layers = small_layers(Lyr, E, H, I, 80, "device")
+    host_layers = small_layers(Lyr, E, H, I, 80, "host")
+    slots = bmx.ExpertSlots(host_layers, 10, maxj=3)
+    kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
+    ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
+    st_layers = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(Lyr)]
+    rng = np.random.default_rng(11)
+    for tok in range(12):
+        T = 1 if tok % 4 else 3
+        lgs = [torch.from_numpy(synth.zipf_logits(T, E, 1.1, seed=100 * tok + li)).cuda() for li in range(Lyr)]
+        x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16)).cuda()
+        for li in range(Lyr):
+            sel, w = ref_layers[li].routing_fn(T, None, x, {"logits": lgs[li]})
+            want = ref_layers[li].run_bszN(x, sel, w)
+            sel2, w2 = st_layers[li].routing_fn(T, None, x, {"logits": lgs[li]})
+            st_layers[li].layer(li, sel2, w2, x, T)
+            if li + 1 < Lyr:
+                noisy = lgs[li + 1].float() + torch.randn(lgs[li + 1].shape, device="cuda") * 0.7
+                guess, _ = st_layers[li + 1].routing_fn(T, None, x, {"logits": noisy.half()})
+                slots.prefetch(li + 1, guess.view(-1), limit=4)
+            got = st_layers[li].run_bszN(x, sel2, w2)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), (tok, li)
+        say("prefetch token", tok, "stats", slots.stats())
+    h, m, adm, novic, ev, pfa, pfu, pfw = slots.stats()
+    assert pfa > 0 and pfu > 0 and pfw > 0
 
 
 def test_stage_async_copies(cuda):
