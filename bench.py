@@ -163,7 +163,18 @@ def bench_c4(args):
         if li % 8 == 0:
             log(f"bench c4: layer {li} built")
     lg_all = torch.from_numpy(np.stack(lgs)).to(dev)            # [NL, NTOK, E] fp16
-    slots = bmx.ExpertSlots(layers, S, maxj=16)
+    PF = args.prefetch
+    if PF:
+        # layer-ahead guesses: layer li routes its logits plus noise (a stand-in for its router on the previous layer's
+        # MoE input); routed inside the timed region like the real picks
+        noise = np.random.default_rng(99).standard_normal((NL, NTOK, E)).astype(np.float32) * args.guess_noise
+        lg_guess = torch.from_numpy((np.stack(lgs).astype(np.float32) + noise).astype(np.float16)).to(dev)
+        gsel = torch.empty((1, topk), dtype=torch.int64, device=dev)
+        gw = torch.empty((1, topk), dtype=torch.float16, device=dev)
+        pf_copied = [None, None]
+        pf_admitted = [torch.cuda.Event() for _ in range(NL)]
+    slots = bmx.ExpertSlots(layers, S, maxj=16, copies=args.copies)
+    DMA = args.copies == "dma"
     # warm: each layer's most popular experts (Zipf rank order of its permutation), S // NL per layer
     per = S // NL
     for li in range(NL):
@@ -191,6 +202,7 @@ def bench_c4(args):
     copied_dn = [torch.cuda.Event() for _ in range(NL)]
     side = slots.side
     tstruct = ctypes.byref(slots.struct)
+    seq, pseq, seqs = ctypes.c_int64(), ctypes.c_int64(), [0] * NL
 
     def token(tok):
         s = torch.cuda.current_stream()
@@ -199,13 +211,39 @@ def bench_c4(args):
             lgp = ctypes.c_void_p(lg_all.data_ptr() + (li * NTOK + tok) * E * 2)
             bmx._lib.check(L.bmx_router_topk(lgp, P(biases[li]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0, P(sel),
                                              P(w), sp), "router")
-            bmx._lib.check(L.bmx_slot_step(tstruct, li, P(sel), topk, 0, 1, sp), "slot step")
-            stepped[li].record(s)
-            side.wait_event(stepped[li])
-            bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 3, ctypes.c_void_p(side.cuda_stream)), "slot copy")
-            copied_gu[li].record(side)
-            bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 4, ctypes.c_void_p(side.cuda_stream)), "slot copy")
-            copied_dn[li].record(side)
+            if DMA:
+                bmx._lib.check(L.bmx_slot_step_agent(tstruct, slots.agent, li, P(sel), topk, 0, 1, ctypes.byref(seq),
+                                                     sp), "slot step")
+                seqs[li] = seq.value
+            else:
+                bmx._lib.check(L.bmx_slot_step(tstruct, li, P(sel), topk, 0, 1, sp), "slot step")
+                stepped[li].record(s)
+                side.wait_event(stepped[li])
+                bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 3, ctypes.c_void_p(side.cuda_stream)), "slot copy")
+                copied_gu[li].record(side)
+                bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 4, ctypes.c_void_p(side.cuda_stream)), "slot copy")
+                copied_dn[li].record(side)
+            if PF and li + 1 < NL and DMA:
+                lgq = ctypes.c_void_p(lg_guess.data_ptr() + ((li + 1) * NTOK + tok) * E * 2)
+                bmx._lib.check(L.bmx_router_topk(lgq, P(biases[li + 1]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0,
+                                                 P(gsel), P(gw), sp), "guess router")
+                bmx._lib.check(L.bmx_slot_prefetch_agent(tstruct, slots.agent, li + 1, P(gsel), topk, 0, PF,
+                                                         ctypes.byref(pseq), sp), "slot prefetch")
+            elif PF and li + 1 < NL:
+                b = li & 1
+                lgq = ctypes.c_void_p(lg_guess.data_ptr() + ((li + 1) * NTOK + tok) * E * 2)
+                bmx._lib.check(L.bmx_router_topk(lgq, P(biases[li + 1]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0,
+                                                 P(gsel), P(gw), sp), "guess router")
+                if pf_copied[b] is not None:
+                    s.wait_event(pf_copied[b])
+                bmx._lib.check(L.bmx_slot_prefetch(tstruct, li + 1, P(gsel), topk, 0, PF, b, sp), "slot prefetch")
+                pf_admitted[li].record(s)
+                side.wait_event(pf_admitted[li])
+                bmx._lib.check(L.bmx_slot_prefetch_copy(tstruct, li + 1, b, 7, ctypes.c_void_p(side.cuda_stream)),
+                               "prefetch copy")
+                ev = torch.cuda.Event()
+                ev.record(side)
+                pf_copied[b] = ev
             bmx._lib.check(L.bmx_dispatch(P(sel), 1, topk, E, 0, 1, rpg, ctypes.byref(routes.struct), P(dws), dws_n, sp),
                            "dispatch")
             d = ctypes.byref(descs[li])
@@ -213,7 +251,10 @@ def bench_c4(args):
             for st in (bmx._lib.STAGE_GATE_UP_RESIDENT, "gu", bmx._lib.STAGE_GATE_UP_STAGED, bmx._lib.STAGE_ACT, "dn",
                        bmx._lib.STAGE_DOWN, bmx._lib.STAGE_COMBINE):
                 if isinstance(st, str):
-                    s.wait_event(copied_gu[li] if st == "gu" else copied_dn[li])
+                    if DMA:
+                        bmx._lib.check(L.bmx_copy_wait_layer(slots.agent, li, 0 if st == "gu" else 1, sp), "copy wait")
+                    else:
+                        s.wait_event(copied_gu[li] if st == "gu" else copied_dn[li])
                     continue
                 bmx._lib.check(L.bmx_moe_stage(d, st, P(x), 1, ctypes.byref(routes.struct), None, None, P(w), o, P(ws),
                                                ws_n, 1, sp), "stage")
@@ -230,7 +271,7 @@ def bench_c4(args):
     st1 = slots.stats()
     d = [b - a for a, b in zip(st0, st1)]
     exp_bytes = layers[0].expert_bytes(0)
-    staged = d[2] * exp_bytes
+    staged = (d[2] + d[5]) * exp_bytes
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(layers[0], sel.repeat(4, 1), w.repeat(4, 1))
@@ -250,11 +291,19 @@ def bench_c4(args):
         "config": {"workload": f"c4 decode stack: {NL} layers of {E} routed experts top-{topk} sigmoid+bias + 1 shared (in "
                                f"VRAM), H {H}, I {I}, EXL3 3 bpw; expert-slot table of {S} VRAM slots (30 %) warmed with each "
                                f"layer's top {per} experts by popularity", "tokens": 1, "layers": NL, "path": "decode",
-                   "step": "per layer: router + slot step (copies on a side stream) + dispatch + gate/up (resident, then "
-                           "staged) + down + combine"},
+                   "step": "per layer: router + slot step (copies " + ("by the copy agent on the DMA engines" if DMA else
+                                                               "on a side stream") + ") + "
+                           + (f"next layer's guess (router on noisy logits) + slot prefetch of up to {PF} (copies on the "
+                              "side stream) + " if PF else "")
+                           + "dispatch + gate/up (resident, then staged) + down + combine"},
         "us_per_token": round(ms * 1e3, 3), "us_per_layer": round(ms * 1e3 / NL, 3),
         "slot_stats_per_token": {"hits": d[0] / args.steps, "misses": d[1] / args.steps, "admitted": d[2] / args.steps,
-                                 "no_victim": d[3] / args.steps, "evictions": d[4] / args.steps},
+                                 "no_victim": d[3] / args.steps, "evictions": d[4] / args.steps,
+                                 "prefetched": d[5] / args.steps, "prefetch_used": d[6] / args.steps,
+                                 "prefetch_wasted": d[7] / args.steps},
+        "copies": args.copies,
+        "prefetch": {"limit": PF, "guess_noise": args.guess_noise,
+                     "precision": round(d[6] / max(1, d[5]), 4)} if PF else None,
         "hit_rate": round(d[0] / max(1, d[0] + d[1]), 4),
         "staged_bytes_per_token": staged / args.steps,
         "staged_gbps": round(staged / (ms * 1e-3 * args.steps) / 1e9, 2),
@@ -262,6 +311,9 @@ def bench_c4(args):
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+    if DMA:
+        log(f"bench c4: copy agent {slots.agent_status()}")
+        slots.close()
 
 
 def main():
@@ -274,6 +326,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--path", choices=["auto", "decode", "mid", "prefill"], default="auto",
                     help="expert-products path (auto: the library's choice for the batch)")
+    ap.add_argument("--prefetch", type=int, default=0, metavar="N",
+                    help="c4: layer-ahead prefetch of up to N guessed experts of the next layer per layer (0: off)")
+    ap.add_argument("--copies", choices=["kernel", "dma"], default="kernel",
+                    help="c4: slot copies by a kernel on a side stream or by the copy agent on the DMA engines")
+    ap.add_argument("--guess-noise", type=float, default=1.0, metavar="SIGMA",
+                    help="c4 prefetch: the next layer's guess routes its own logits plus N(0, SIGMA) noise")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (scale reference for HBM byte counters)")
     args = ap.parse_args()

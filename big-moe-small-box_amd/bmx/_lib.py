@@ -76,6 +76,13 @@ SIGNATURES = {
     "bmx_slot_copy_mats": (_I, [ctypes.POINTER(SlotTable), _I, _I, _P]),
     "bmx_slot_prefetch": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, _I64, _I, _I, _P]),
     "bmx_slot_prefetch_copy": (_I, [ctypes.POINTER(SlotTable), _I, _I, _I, _P]),
+    "bmx_copy_agent_create": (_I, [ctypes.POINTER(SlotTable), _P, _P, ctypes.POINTER(_P)]),
+    "bmx_copy_agent_destroy": (_I, [_P]),
+    "bmx_copy_agent_status": (_I, [_P, _P]),
+    "bmx_slot_step_agent": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _I, _I64, _I, ctypes.POINTER(_I64), _P]),
+    "bmx_slot_prefetch_agent": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _I, _I64, _I, ctypes.POINTER(_I64), _P]),
+    "bmx_copy_wait": (_I, [_P, _I64, _I, _P]),
+    "bmx_copy_wait_layer": (_I, [_P, _I, _I, _P]),
     "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
     "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }

@@ -9,6 +9,7 @@ the layer's expert products wait for those copies only in their staged part (MoE
 admits a later layer's guessed experts ahead of its step (the reference's layer-ahead routing guess, engine/nv2.py:
 450-487) with copies on the same side stream. No host synchronisation anywhere."""
 import ctypes
+import weakref
 
 import torch
 
@@ -16,9 +17,13 @@ from . import _lib as L
 
 
 class ExpertSlots:
-    def __init__(self, layers, S, maxj=32, disabled=()):
+    def __init__(self, layers, S, maxj=32, disabled=(), copies="kernel"):
         """layers: one ExpertTable per layer (same H, I, E and record geometry); S slots; maxj admissions per step;
-        disabled: slot indices never used."""
+        disabled: slot indices never used. copies: "kernel" (a copy kernel on the side stream reads the homes) or
+        "dma" (a host thread of the library issues them on the DMA engines, which leaves the other kernels their
+        memory bandwidth; the layer's stages wait on the copies with a small polling kernel)."""
+        if copies not in ("kernel", "dma"):
+            raise ValueError("ExpertSlots: copies must be 'kernel' or 'dma'")
         t0 = layers[0]
         for t in layers:
             if (t.H, t.I, t.E, t.rec, t.off_u, t.off_d) != (t0.H, t0.I, t0.E, t0.rec, t0.off_u, t0.off_d):
@@ -53,6 +58,38 @@ class ExpertSlots:
         self.copied = [None] * self.L        # event: copies of the layer's last step done
         self.pf_copied = [None, None]        # event per prefetch job buffer: its last copies done
         self.pf_calls = 0
+        self.copies = copies
+        self.agent = None
+        self.seq = [0] * self.L               # dma: sequence number of each layer's last step
+        if copies == "dma":
+            homes = (ctypes.c_uint64 * (self.L * self.E))(*[t.addr[e][0] for t in layers for e in range(t.E)])
+            nb = (ctypes.c_int64 * (self.L * self.E * 3))(*[t.mat_bytes(e, m) for t in layers for e in range(t.E)
+                                                            for m in range(3)])
+            ag = ctypes.c_void_p()
+            L.check(L.lib().bmx_copy_agent_create(ctypes.byref(self.struct), homes, nb, ctypes.byref(ag)),
+                    "bmx_copy_agent_create")
+            self.agent = ag
+            self._finalizer = weakref.finalize(self, ExpertSlots._destroy_agent, ag.value)
+
+    @staticmethod
+    def _destroy_agent(ptr):
+        try:
+            torch.cuda.synchronize()
+        finally:
+            L.lib().bmx_copy_agent_destroy(ctypes.c_void_p(ptr))
+
+    def close(self):
+        """Stop the copy agent (dma): synchronises the device first."""
+        if self.agent is not None:
+            self._finalizer()
+            self.agent = None
+
+    def agent_status(self):
+        """dma: (records, copies, bytes copied, gate / up mark, down mark, a wait ran out of time); raises if a copy
+        failed or a wait ran out of time."""
+        st = (ctypes.c_int64 * 6)()
+        L.check(L.lib().bmx_copy_agent_status(self.agent, st), "bmx_copy_agent_status")
+        return tuple(st)
 
     def step(self, li, sel, first=0, admit=True):
         """CLOCK step of layer li over the picks sel (int64 device tensor) on the current stream, then the copies of
@@ -60,6 +97,13 @@ class ExpertSlots:
         if sel.dtype != torch.int64 or not sel.is_contiguous():
             sel = sel.long().contiguous()
         cur = torch.cuda.current_stream()
+        if self.agent is not None:
+            q = ctypes.c_int64()
+            L.check(L.lib().bmx_slot_step_agent(ctypes.byref(self.struct), self.agent, li,
+                                                ctypes.c_void_p(sel.data_ptr()), sel.numel(), int(first), int(admit),
+                                                ctypes.byref(q), ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_step_agent")
+            self.seq[li] = q.value
+            return None
         L.check(L.lib().bmx_slot_step(ctypes.byref(self.struct), li, ctypes.c_void_p(sel.data_ptr()), sel.numel(),
                                       int(first), int(admit), ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_step")
         stepped = torch.cuda.Event()
@@ -86,11 +130,18 @@ class ExpertSlots:
         if n > 512:
             raise ValueError("ExpertSlots.prefetch: at most 512 guesses")
         cur = torch.cuda.current_stream()
+        lim = self.maxj if limit is None else int(limit)
+        if self.agent is not None:
+            q = ctypes.c_int64()
+            L.check(L.lib().bmx_slot_prefetch_agent(ctypes.byref(self.struct), self.agent, li,
+                                                    ctypes.c_void_p(guess.data_ptr()), n, int(first), lim,
+                                                    ctypes.byref(q), ctypes.c_void_p(cur.cuda_stream)),
+                    "bmx_slot_prefetch_agent")
+            return None
         b = self.pf_calls & 1
         self.pf_calls += 1
         if self.pf_copied[b] is not None:      # the buffer's previous copies read its jobs while they run
             cur.wait_event(self.pf_copied[b])
-        lim = self.maxj if limit is None else int(limit)
         L.check(L.lib().bmx_slot_prefetch(ctypes.byref(self.struct), li, ctypes.c_void_p(guess.data_ptr()), n,
                                           int(first), lim, b, ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_prefetch")
         admitted = torch.cuda.Event()
@@ -107,6 +158,12 @@ class ExpertSlots:
     def wait_copies(self, li, stream=None, part="all"):
         """Order `stream` (default: current) after the copies of layer li's last step: part "gate_up" (the admitted
         experts' gate and up matrices), "down" or "all"."""
+        if self.agent is not None:
+            if self.seq[li]:
+                st = stream or torch.cuda.current_stream()
+                L.check(L.lib().bmx_copy_wait_layer(self.agent, li, 0 if part == "gate_up" else 1,
+                                                    ctypes.c_void_p(st.cuda_stream)), "bmx_copy_wait_layer")
+            return
         if self.copied[li] is not None:
             ev = self.copied[li][0 if part == "gate_up" else 1]
             (stream or torch.cuda.current_stream()).wait_event(ev)

@@ -60,9 +60,18 @@ int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const
 int launch_zero_i32(int32_t* p, int n, hipStream_t s);
 
 // slots.hip
-int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s);
+// A step's or prefetch's admissions published to the copy agent (fine-grained host memory): the payload, then seq with a
+// system-scope release store.
+struct SlotPub {
+    int32_t seq, li, n, kind;     // kind: 0 step, 1 prefetch
+    int32_t pairs[2 * 64];        // (expert, slot) of each admission
+};
+// need (with pub, steps only): need[li] = the last record layer li's next products depend on (seq when the step admitted
+// experts, seq - 1 when it did not: its prefetched hits came with earlier records)
+int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
+                     SlotPub* pub = nullptr, int32_t seq = 0, int32_t* need = nullptr);
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
-                         hipStream_t s);
+                         hipStream_t s, SlotPub* pub = nullptr, int32_t seq = 0);
 int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStream_t s);
 
 // moe_prefill.hip (same ws / stage conventions; ws layout [xt][part_gu][act rows][part_dn])

@@ -2,6 +2,8 @@
 //
 // Semantics follow the reference's ec_step_k (engine/ec.py:16-76) with one contract fixed: misses are admitted in
 // ascending expert order (the reference collects them with atomics, in no fixed order).
+#include <cstdlib>
+
 #include "bmx_common.hpp"
 #include "bmx_internal.hpp"
 
@@ -17,6 +19,9 @@ struct SlotArgs {
     int li, n, admit;
     int pf;       // 0: a step; 1: a prefetch into job buffer `buf` with at most `limit` candidates
     int limit, buf;
+    SlotPub* pub; // or null: the admissions are also published to the copy agent under sequence number seq
+    int32_t seq;
+    int32_t* need;   // steps with pub: need[li] = the last record the layer's products depend on
 };
 
 __device__ __forceinline__ int tile_bytes_dev(int fmt)
@@ -122,19 +127,21 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     }
 
     // admissions: one wave sweeps the CLOCK hand 64 slots at a time. Within a chunk every slot is probed once, so taking
-    // the first candidate and clearing the reference bits of the unpinned slots before it is the sequential sweep.
+    // the first candidate and clearing the reference bits of the unpinned slots before it is the sequential sweep. A
+    // prefetch sweeps gently: referenced slots keep their bits, and its admissions start without one.
     if (wave == 0)
     {
         int32_t* jobs = a.pf ? prefetch_jobs(t, a.buf) + 1 : t.jobs;
         int hand = t.ctl[0], nj = 0, novictim = 0, evicted = 0, wasted = 0;
         const int chunk = S < 64 ? S : 64;
+        const int maxp = a.pf ? S : 2 * S;      // a prefetch passes referenced slots without clearing: one revolution
         for (int k = 0; a.admit && S > 0 && k < nmiss && nj < t.maxj; ++k)
         {
             const int ex = miss[k];
             int found = -1, probes = 0;
-            while (probes < 2 * S)
+            while (probes < maxp)
             {
-                const int nv = min(chunk, 2 * S - probes);
+                const int nv = min(chunk, maxp - probes);
                 int idx = hand + lane;
                 if (idx >= S) idx -= S;
                 const bool valid = lane < nv;
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                 const bool cand = valid && !skip && !rb;
                 const uint64_t cb = __ballot(cand);
                 const int upto = cb ? (__ffsll((long long)cb) - 1) : nv;
-                if (valid && lane < upto && !skip && rb) refb[idx] = 0;
+                if (!a.pf && valid && lane < upto && !skip && rb) refb[idx] = 0;
                 if (cb)
                 {
                     found = hand + upto;
@@ -177,7 +184,7 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                 }
                 t.owner[s] = a.li * E + ex;
                 slotof[ex] = s;
-                refb[s] = 1;
+                refb[s] = a.pf ? 0 : 1;     // a prefetched expert keeps no hit bit until a step uses it
                 pin[s] = epoch;
                 t.pfl[s] = a.pf;
                 bmx_expert* tab = reinterpret_cast<bmx_expert*>(t.tables[a.li]);
@@ -188,11 +195,24 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                 jobs[2 * nj] = ex;
                 jobs[2 * nj + 1] = s;
                 if (!a.pf) t.fresh[ex] = 1;
+                if (a.pub)
+                {
+                    a.pub->pairs[2 * nj] = ex;
+                    a.pub->pairs[2 * nj + 1] = s;
+                }
             }
             ++nj;
         }
         if (lane == 0)
         {
+            if (a.pub)
+            {
+                a.pub->li = a.li;
+                a.pub->n = nj;
+                a.pub->kind = a.pf;
+                __hip_atomic_store(&a.pub->seq, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (!a.pf && a.need) a.need[a.li] = nj > 0 ? a.seq : a.seq - 1;
+            }
             if (a.admit && S > 0) t.ctl[0] = hand;
             if (a.pf)
             {
@@ -269,7 +289,8 @@ static int check_table(const bmx_slot_table* t, const char* who)
     return BMX_OK;
 }
 
-int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s)
+int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
+                     SlotPub* pub, int32_t seq, int32_t* need)
 {
     int rc = check_table(t, "bmx_slot_step");
     if (rc) return rc;
@@ -284,12 +305,15 @@ int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n,
     a.pf = 0;
     a.limit = 0;
     a.buf = 0;
+    a.pub = pub;
+    a.seq = seq;
+    a.need = need;
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
     return check_launch("bmx_slot_step");
 }
 
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
-                         hipStream_t s)
+                         hipStream_t s, SlotPub* pub, int32_t seq)
 {
     int rc = check_table(t, "bmx_slot_prefetch");
     if (rc) return rc;
@@ -306,8 +330,21 @@ int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, in
     a.pf = 1;
     a.limit = limit;
     a.buf = buf;
+    a.pub = pub;
+    a.seq = seq;
+    a.need = nullptr;
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
     return check_launch("bmx_slot_prefetch");
+}
+
+// workgroups per copy job (BMX_SLOT_COPY_WGS, 1..256): reads of pinned host memory wait microseconds on the link, so a
+// few workgroups with several loads in flight per thread keep it busy; more only queue behind it and hold back the
+// kernels of other streams
+static int copy_wgs()
+{
+    const char* v = getenv("BMX_SLOT_COPY_WGS");
+    const int n = v ? atoi(v) : 64;
+    return n < 1 ? 1 : n > 256 ? 256 : n;
 }
 
 int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStream_t s)
@@ -319,7 +356,7 @@ int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStre
     if (mats < 0 || mats > 7) return set_error(BMX_ERR_ARG, "%s: bad matrix mask %d", who, mats);
     if (buf > 1) return set_error(BMX_ERR_ARG, "%s: bad buffer %d", who, buf);
     if (t->maxj == 0 || mats == 0) return BMX_OK;
-    hipLaunchKernelGGL(k_slot_copy, dim3(64, (unsigned)t->maxj), dim3(256), 0, s, *t, li, mats, buf);
+    hipLaunchKernelGGL(k_slot_copy, dim3((unsigned)copy_wgs(), (unsigned)t->maxj), dim3(256), 0, s, *t, li, mats, buf);
     return check_launch(who);
 }
 

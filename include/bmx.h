@@ -233,8 +233,11 @@ int bmx_slot_copy_mats(const bmx_slot_table* t, int li, int mats, bmx_stream_t s
 /* Layer-ahead prefetch (the reference's next-layer routing guess, engine/nv2.py:450-487, whose picks it hands on as
  * prefetch hints, engine/kernels/nv2/nv2_dev.cu:75-85 and nv2_host.cpp:1046-1056): the first `limit` distinct guesses
  * sel[n] (n <= 512, best first, ids outside [first, first + E) ignored) that are not resident in layer li are admitted
- * in that order, at most maxj, by the step's CLOCK sweep within the current step counter (slots the last step pinned
- * stay pinned and the counter does not advance; hits and reference bits of resident guesses are left alone). Jobs go to
+ * in that order, at most maxj, within the current step counter (slots the last step pinned stay pinned and the counter
+ * does not advance) by a gentle CLOCK sweep: the first enabled, unpinned slot from the hand whose reference bit is
+ * clear, passing referenced slots without clearing their bits (at most S probes; a guess that finds none ends the
+ * prefetch); admitted with the bit clear, so a wrong guess is the next victim. Resident guesses and every reference bit
+ * are left alone. Jobs go to
  * prefetch buffer buf (0 or 1), never to the step's, so the copies of the last step may still be in flight. Stream
  * order: after the step of the layer being computed; the copies (bmx_slot_prefetch_copy) on the same side stream as
  * the step copies, before the next step's copies; the next prefetch into the same buffer after those copies. A
@@ -243,6 +246,34 @@ int bmx_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n
                       bmx_stream_t stream);
 /* The copies of prefetch buffer buf's jobs of layer li (matrices in mats, as bmx_slot_copy_mats). */
 int bmx_slot_prefetch_copy(const bmx_slot_table* t, int li, int buf, int mats, bmx_stream_t stream);
+/* ---- copy agent ----
+ * The slot table's home -> slot copies on the DMA engines, issued by a host thread (the reference's host-side staging,
+ * engine/kernels/nv2/nv2_host.cpp:1558-1593, fed by picks the device publishes to mapped host memory,
+ * engine/kernels/nv2/nv2_dev.cu:23-95). bmx_slot_step_agent / bmx_slot_prefetch_agent run the step / prefetch and publish
+ * its admissions under the next sequence number (*seq); the agent's thread hands each published record, in order, to
+ * the SDMA engines (per admission the gate / up part, then the down matrices) and marks each part done; bmx_copy_wait
+ * orders a stream after a record's part (0 gate / up, 1 down) with a one-wave kernel that polls the mark (bounded: after
+ * 5 s it gives up and bmx_copy_agent_status reports it). A kernel reading pinned host memory at link speed holds back
+ * HBM-bound kernels on other streams; the DMA engines do not. Calls on one agent come from one host thread, its steps on
+ * one stream. home[L * E]: each expert's record address (pinned host or device memory; gate at 0, up at off_u, down at
+ * off_d, as the slots); mat_bytes[L * E * 3]: its trellis bytes. */
+typedef struct bmx_copy_agent bmx_copy_agent;
+int bmx_copy_agent_create(const bmx_slot_table* t, const uint64_t* home, const int64_t* mat_bytes,
+                          bmx_copy_agent** agent);
+int bmx_copy_agent_destroy(bmx_copy_agent* agent);
+/* stats (or NULL) [6]: records, copies, bytes copied, gate / up mark, down mark, a wait ran out of time; returns an
+ * error if a copy failed or a wait ran out of time. */
+int bmx_copy_agent_status(const bmx_copy_agent* agent, int64_t* stats);
+int bmx_slot_step_agent(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const int64_t* sel, int n,
+                        int64_t first, int admit, int64_t* seq, bmx_stream_t stream);
+int bmx_slot_prefetch_agent(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const int64_t* sel, int n,
+                            int64_t first, int limit, int64_t* seq, bmx_stream_t stream);
+int bmx_copy_wait(bmx_copy_agent* agent, int64_t seq, int part, bmx_stream_t stream);
+/* Orders a stream after what layer li's products need from the copies (part 0 gate / up, 1 down): its last step's
+ * record when that step admitted experts, else the records before it (the prefetches its hits came from); the step
+ * leaves the target on the device, so a layer whose experts are in place waits for nothing in flight. */
+int bmx_copy_wait_layer(bmx_copy_agent* agent, int li, int part, bmx_stream_t stream);
+
 /* Host-planned staging: n copies src[i] -> dst[i] of bytes[i] (hipMemcpyAsync, e.g. pinned host -> slot), in order on
  * stream (the reference's stage_layer, engine/kernels/nv2/nv2_host.cpp:1558-1593). */
 int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream);

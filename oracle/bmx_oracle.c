@@ -568,7 +568,8 @@ int bmxo_dispatch(const int64_t* sel, int T, int topk, int E, int64_t first, int
  * 2 S steps; the victim's owner goes back home (slotof = -1). */
 /* the CLOCK admission of the misses miss[nmiss] of layer li (ec_step_k, engine/ec.py:40-76, with misses taken in the
  * order given): each takes the first slot from the hand that is enabled, not pinned in `epoch` and whose reference bit is
- * clear, clearing the bits it passes; a miss that finds none in 2 S probes ends the admissions. */
+ * clear, clearing the bits it passes; a miss that finds none in 2 S probes ends the admissions. A prefetch (pf) sweeps
+ * gently: it passes referenced slots without clearing their bits (so at most S probes) and admits with the bit clear. */
 static int clock_admit(bmxo_slots* t, int li, const int* miss, int nmiss, int maxj, int epoch, int pf, int32_t* jobs,
                        int32_t* evicted, int32_t* fresh, int64_t* stats)
 {
@@ -578,12 +579,16 @@ static int clock_admit(bmxo_slots* t, int li, const int* miss, int nmiss, int ma
     {
         const int e = miss[k];
         int found = -1;
-        for (int step = 0; step < 2 * S; ++step)
+        for (int step = 0; step < (pf ? S : 2 * S); ++step)
         {
             const int s = hand;
             hand = (hand + 1 == S) ? 0 : hand + 1;
             if (t->pin[s] == epoch || t->pin[s] < 0) continue;
-            if (t->refb[s]) { t->refb[s] = 0; continue; }
+            if (t->refb[s])
+            {
+                if (!pf) t->refb[s] = 0;
+                continue;
+            }
             found = s;
             break;
         }
@@ -598,7 +603,7 @@ static int clock_admit(bmxo_slots* t, int li, const int* miss, int nmiss, int ma
         evicted[nj] = old;
         t->owner[s] = li * E + e;
         t->slotof[(size_t)li * E + e] = s;
-        t->refb[s] = 1;
+        t->refb[s] = !pf;
         t->pin[s] = epoch;
         t->pfl[s] = pf;
         if (fresh) fresh[e] = 1;

@@ -97,8 +97,11 @@ typedef struct {
 int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int admit, int maxj, int32_t* jobs,
                    int32_t* evicted, int32_t* fresh, int64_t* stats);
 /* layer-ahead prefetch into layer li's slots: the first `limit` distinct in-range picks of sel[n] (rank order) that are
- * not resident are admitted in that order, at most maxj, by the same CLOCK sweep as a step but within the current epoch
- * (slots pinned by the last step stay pinned; the epoch does not advance); hits and hit bits are left alone. */
+ * not resident are admitted in that order, at most maxj, within the current epoch (slots pinned by the last step stay
+ * pinned; the epoch does not advance) by a gentle CLOCK sweep: the first enabled, unpinned slot from the hand whose
+ * reference bit is clear, passing referenced slots without clearing their bits (at most S probes; a guess that finds
+ * none ends the prefetch); admitted with the bit clear, so a wrong guess is the next victim. Resident guesses and every
+ * reference bit are left alone. */
 int bmxo_slot_prefetch(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int limit, int maxj,
                        int32_t* jobs, int32_t* evicted, int64_t* stats);
 

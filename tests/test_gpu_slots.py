@@ -123,10 +123,11 @@ def test_slot_prefetch_matches_oracle(cuda, oracle, S, maxj):
         assert st[5] > 0 and st[6] > 0
 
 
-def test_slot_copies_deliver_home_bytes(cuda):
+@pytest.mark.parametrize("copies", ["kernel", "dma"])
+def test_slot_copies_deliver_home_bytes(cuda, copies):
     import bmx
     layers = small_layers(2, 12, 256, 128, 30, "host", fmts=(bmx.TF_K2, bmx.TF_K25, bmx.TF_K4))
-    slots = bmx.ExpertSlots(layers, 7, maxj=6)
+    slots = bmx.ExpertSlots(layers, 7, maxj=6, copies=copies)
     rng = np.random.default_rng(5)
     for step in range(12):
         li = step % 2
@@ -151,18 +152,29 @@ def test_slot_copies_deliver_home_bytes(cuda):
             checked += 1
     say("resident experts checked", checked)
     assert checked == 7
+    if copies == "dma":
+        import time
+        t0 = time.time()
+        while slots.agent_status()[4] < 12 and time.time() - t0 < 2.0:   # a last step without admissions needs no wait
+            time.sleep(0.001)
+        rec, ncopies, nbytes, gu, dn, late = slots.agent_status()
+        say("agent records", rec, "copies", ncopies, "bytes", nbytes)
+        assert rec == 12 and gu == dn == 12 and late == 0 and ncopies == 2 * slots.stats()[2]
+        slots.close()
 
 
-def test_layer_with_staged_experts_matches_resident(cuda):
+@pytest.mark.parametrize("copies", ["kernel", "dma"])
+def test_layer_with_staged_experts_matches_resident(cuda, copies):
     """The same layers computed with every expert resident in device memory and with homes in pinned host memory staged
-    through a small slot table (hits, admissions copied on the side stream, and misses left at home when maxj runs
-    out): identical outputs, bit for bit, on the GEMV, mid-size and prefill paths."""
+    through a small slot table (hits, admissions copied on the side stream by a kernel or by the copy agent on the DMA
+    engines, and misses left at home when maxj runs out): identical outputs, bit for bit, on the GEMV, mid-size and
+    prefill paths."""
     import bmx
     from bmx import synth
     Lyr, E, H, I, topk = 3, 24, 512, 256, 4
     dev_layers = small_layers(Lyr, E, H, I, 50, "device")
     host_layers = small_layers(Lyr, E, H, I, 50, "host")
-    slots = bmx.ExpertSlots(host_layers, 9, maxj=3)
+    slots = bmx.ExpertSlots(host_layers, 9, maxj=3, copies=copies)
     kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
     ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
     st_layers = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(Lyr)]
@@ -183,9 +195,13 @@ def test_layer_with_staged_experts_matches_resident(cuda):
             assert torch.equal(sel, sel2) and torch.equal(got, want)
     h, m, adm, novic, ev = slots.stats()[:5]
     assert m > 0 and adm > 0 and ev > 0 and m > adm      # misses, admissions, evictions and unadmitted misses all ran
+    if copies == "dma":
+        say("agent", slots.agent_status())
+        slots.close()
 
 
-def test_prefetch_keeps_outputs(cuda):
+@pytest.mark.parametrize("copies", ["kernel", "dma"])
+def test_prefetch_keeps_outputs(cuda, copies):
     """A decode loop over a stack of layers with homes in pinned host memory, each layer's step followed by a prefetch
     of the next layer's guessed experts (its router on noisy logits: right and wrong guesses) before the layer's
     products: outputs identical, bit for bit, to the same layers with every expert resident; prefetched experts are
@@ -195,7 +211,7 @@ def test_prefetch_keeps_outputs(cuda):
     Lyr, E, H, I, topk = 4, 24, 512, 256, 4
     dev_layers = small_layers(Lyr, E, H, I, 80, "device")
     host_layers = small_layers(Lyr, E, H, I, 80, "host")
-    slots = bmx.ExpertSlots(host_layers, 10, maxj=3)
+    slots = bmx.ExpertSlots(host_layers, 10, maxj=3, copies=copies)
     kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
     ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
     st_layers = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(Lyr)]
@@ -219,6 +235,9 @@ def test_prefetch_keeps_outputs(cuda):
         say("prefetch token", tok, "stats", slots.stats())
     h, m, adm, novic, ev, pfa, pfu, pfw = slots.stats()
     assert pfa > 0 and pfu > 0 and pfw > 0
+    if copies == "dma":
+        say("agent", slots.agent_status())
+        slots.close()
 
 
 def test_stage_async_copies(cuda):

@@ -173,34 +173,34 @@ def test_slot_disabled_slots_never_used(oracle):
 
 def test_slot_prefetch_known_answer(oracle):
     """Layer-ahead prefetch: candidates are the distinct in-range guesses that are not resident, in rank order, capped
-    at `limit`; they take CLOCK victims within the current epoch (the last step's slots stay pinned, the epoch does not
-    advance); a later step's first hit on a prefetched slot counts as used and marks the expert fresh; a prefetched
-    expert evicted before any use counts as wasted."""
-    st = oracle.SlotTable(L=2, E=8, S=5)
+    at `limit`; they take slots within the current epoch (the last step's slots stay pinned, the epoch does not
+    advance) by a gentle sweep that passes referenced slots without clearing their bits and admits with the bit clear;
+    a later step's first hit on a prefetched slot counts as used and marks the expert fresh; a prefetched expert evicted
+    before any use counts as wasted."""
+    st = oracle.SlotTable(L=2, E=8, S=6)
     st.step(1, [3])                                         # epoch 1: L1 e3 -> slot 0
     st.step(0, [1, 4])                                      # epoch 2: L0 e1 -> 1, e4 -> 2; hand 3
     jobs, ev = st.prefetch(1, [3, 6, 6, 9, 2, 5], limit=2)  # 3 resident, 6 dup, 9 out of range: [6, 2]
     assert jobs.tolist() == [[6, 3], [2, 4]] and ev.tolist() == [-1, -1]
-    assert st.epoch == 2 and st.hand == 0 and st.pin[3] == st.pin[4] == 2 and st.pfl.tolist() == [0, 0, 0, 1, 1]
+    assert st.epoch == 2 and st.hand == 5 and st.pin[3] == st.pin[4] == 2
+    assert st.pfl.tolist() == [0, 0, 0, 1, 1, 0] and st.refb.tolist() == [1, 1, 1, 0, 0, 0]
     assert st.stats.tolist() == [0, 3, 3, 0, 0, 2, 0, 0]
-    jobs, _ = st.prefetch(1, [5, 7], limit=4)               # slot 0 only (all others pinned in epoch 2): L1 e3 out
-    assert jobs.tolist() == [[5, 0]] and st.slotof[8 + 3] == -1 and st.pin[0] == 2
-    jobs, _ = st.prefetch(1, [7], limit=4)                  # every slot pinned in epoch 2: no victim, nothing counted
-    assert jobs.size == 0 and st.stats[3] == 0 and st.hand == 1
+    jobs, _ = st.prefetch(1, [5, 7], limit=4)               # 5 -> slot 5; 7: slot 0 referenced, the rest pinned
+    assert jobs.tolist() == [[5, 5]] and st.hand == 0 and st.refb[0] == 1 and st.slotof[8 + 3] == 0
     jobs, ev = st.step(1, [2, 6, 0])                        # epoch 3: 2, 6 prefetched hits; 0 misses
-    # hand 1: slot 1 (L0 e1) and 2 (L0 e4) lose their bits, 3 and 4 pinned, slot 0 (L1 e5) loses its bit, slot 1 taken
-    assert jobs.tolist() == [[0, 1]] and ev.tolist() == [1]
+    # hand 0: slots 0-2 lose their bits, 3 and 4 are pinned, slot 5 (L1 e5, prefetched, never used, bit clear) taken
+    assert jobs.tolist() == [[0, 5]] and ev.tolist() == [8 + 5]
     assert np.flatnonzero(st.fresh).tolist() == [0, 2, 6]
-    assert st.stats.tolist() == [2, 4, 4, 0, 2, 3, 2, 0] and st.pfl.tolist() == [1, 0, 0, 0, 0]
-    jobs, ev = st.step(0, [5, 6])                           # epoch 4: slot 2 (L0 e4), then slot 0 (L1 e5, never used)
-    assert jobs.tolist() == [[5, 2], [6, 0]] and ev.tolist() == [4, 8 + 5]
-    assert st.stats.tolist() == [2, 6, 6, 0, 4, 3, 2, 1] and st.pfl.tolist() == [0, 0, 0, 0, 0]
+    assert st.stats.tolist() == [2, 4, 4, 0, 1, 3, 2, 1] and st.pfl.tolist() == [0] * 6
+    jobs, ev = st.step(0, [5, 6])                           # epoch 4: slot 0 (L1 e3), slot 1 (L0 e1)
+    assert jobs.tolist() == [[5, 0], [6, 1]] and ev.tolist() == [8 + 3, 1]
+    assert st.stats.tolist() == [2, 6, 6, 0, 3, 3, 2, 1]
     _check_maps(st)
 
 
 def test_slot_prefetch_properties_random(oracle):
     """Random steps and prefetches: a prefetch never advances the epoch, never moves a slot the last step pinned, never
-    changes hit / miss counts, admits a prefix (in rank order) of the distinct non-resident guesses, and every expert it
+    changes a reference bit or the hit / miss counts, admits a prefix (in rank order) of the distinct non-resident guesses, and every expert it
     admitted is a hit, marked fresh, at the next step of its layer."""
     rng = np.random.default_rng(1)
     L, E, S = 3, 24, 12
@@ -212,7 +212,7 @@ def test_slot_prefetch_properties_random(oracle):
         lj = int(rng.integers(L))
         guess = rng.integers(-2, E + 2, int(rng.integers(0, 12)))
         limit, maxj = int(rng.integers(1, 8)), int(rng.integers(1, 8))
-        epoch, stats0 = st.epoch, st.stats.copy()
+        epoch, stats0, refb0 = st.epoch, st.stats.copy(), st.refb.copy()
         pinned = {s: int(st.owner[s]) for s in range(S) if st.pin[s] == epoch}
         want, seen = [], set()
         for g in guess:
@@ -224,6 +224,7 @@ def test_slot_prefetch_properties_random(oracle):
         jobs, ev = st.prefetch(lj, guess, limit=limit, maxj=maxj)
         _check_maps(st)
         assert st.epoch == epoch and st.pin[5] == -1 and st.owner[5] == -1
+        assert np.array_equal(st.refb, refb0)               # victims had clear bits; nothing else is touched
         assert all(st.owner[s] == o for s, o in pinned.items())
         assert np.array_equal(st.stats[[0, 1, 2, 3, 6]], stats0[[0, 1, 2, 3, 6]])
         got = jobs[:, 0].tolist()
