@@ -164,6 +164,7 @@ def bench_c4(args):
             log(f"bench c4: layer {li} built")
     lg_all = torch.from_numpy(np.stack(lgs)).to(dev)            # [NL, NTOK, E] fp16
     PF = args.prefetch
+    AH = args.prefetch_ahead if args.copies == "dma" else 1
     if PF:
         # layer-ahead guesses: layer li routes its logits plus noise (a stand-in for its router on the previous layer's
         # MoE input); routed inside the timed region like the real picks
@@ -223,11 +224,11 @@ def bench_c4(args):
                 copied_gu[li].record(side)
                 bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 4, ctypes.c_void_p(side.cuda_stream)), "slot copy")
                 copied_dn[li].record(side)
-            if PF and li + 1 < NL and DMA:
-                lgq = ctypes.c_void_p(lg_guess.data_ptr() + ((li + 1) * NTOK + tok) * E * 2)
-                bmx._lib.check(L.bmx_router_topk(lgq, P(biases[li + 1]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0,
-                                                 P(gsel), P(gw), sp), "guess router")
-                bmx._lib.check(L.bmx_slot_prefetch_agent(tstruct, slots.agent, li + 1, P(gsel), topk, 0, PF,
+            if PF and li + AH < NL and DMA:
+                lgq = ctypes.c_void_p(lg_guess.data_ptr() + ((li + AH) * NTOK + tok) * E * 2)
+                bmx._lib.check(L.bmx_router_topk(lgq, P(biases[li + AH]), 1, E, topk, 1, 1, c["score"], 1, c["scale"],
+                                                 0, P(gsel), P(gw), sp), "guess router")
+                bmx._lib.check(L.bmx_slot_prefetch_agent(tstruct, slots.agent, li + AH, P(gsel), topk, 0, PF,
                                                          ctypes.byref(pseq), sp), "slot prefetch")
             elif PF and li + 1 < NL:
                 b = li & 1
@@ -293,8 +294,8 @@ def bench_c4(args):
                                f"layer's top {per} experts by popularity", "tokens": 1, "layers": NL, "path": "decode",
                    "step": "per layer: router + slot step (copies " + ("by the copy agent on the DMA engines" if DMA else
                                                                "on a side stream") + ") + "
-                           + (f"next layer's guess (router on noisy logits) + slot prefetch of up to {PF} (copies on the "
-                              "side stream) + " if PF else "")
+                           + (f"guess of layer li + {AH} (router on noisy logits) + slot prefetch of up to {PF} + "
+                              if PF else "")
                            + "dispatch + gate/up (resident, then staged) + down + combine"},
         "us_per_token": round(ms * 1e3, 3), "us_per_layer": round(ms * 1e3 / NL, 3),
         "slot_stats_per_token": {"hits": d[0] / args.steps, "misses": d[1] / args.steps, "admitted": d[2] / args.steps,
@@ -302,7 +303,7 @@ def bench_c4(args):
                                  "prefetched": d[5] / args.steps, "prefetch_used": d[6] / args.steps,
                                  "prefetch_wasted": d[7] / args.steps},
         "copies": args.copies,
-        "prefetch": {"limit": PF, "guess_noise": args.guess_noise,
+        "prefetch": {"limit": PF, "guess_noise": args.guess_noise, "ahead": AH,
                      "precision": round(d[6] / max(1, d[5]), 4)} if PF else None,
         "hit_rate": round(d[0] / max(1, d[0] + d[1]), 4),
         "staged_bytes_per_token": staged / args.steps,
@@ -328,7 +329,9 @@ def main():
                     help="expert-products path (auto: the library's choice for the batch)")
     ap.add_argument("--prefetch", type=int, default=0, metavar="N",
                     help="c4: layer-ahead prefetch of up to N guessed experts of the next layer per layer (0: off)")
-    ap.add_argument("--copies", choices=["kernel", "dma"], default="kernel",
+    ap.add_argument("--prefetch-ahead", type=int, default=1, metavar="D",
+                    help="c4 prefetch: layer li prefetches the guess of layer li + D")
+    ap.add_argument("--copies", choices=["kernel", "dma"], default="dma",
                     help="c4: slot copies by a kernel on a side stream or by the copy agent on the DMA engines")
     ap.add_argument("--guess-noise", type=float, default=1.0, metavar="SIGMA",
                     help="c4 prefetch: the next layer's guess routes its own logits plus N(0, SIGMA) noise")

@@ -97,9 +97,9 @@ static void agent_fail(bmx_copy_agent* a, int code)
     __atomic_store_n(&a->sh->flags[2], 1, __ATOMIC_RELEASE);
 }
 
-// The agent thread: records in sequence order; per record the gate / up copies under one signal, the down copies under a
-// second that waits for the first (and the first waits for the previous record's last); flags stored in record order
-// once each part's signal has reached zero.
+// The agent thread: records in sequence order; per step record the gate / up copies under one signal, the down copies
+// under a second that waits for the first (and the first waits for the previous record's last); per prefetch record one
+// copy per admission; flags stored in record order once each part's signal has reached zero.
 static void agent_loop(bmx_copy_agent* a)
 {
     std::vector<hsa_signal_t> sigs(AG_SIGNALS);
@@ -169,7 +169,22 @@ static void agent_loop(bmx_copy_agent* a)
                 e_[nj] = e;
                 s_[nj++] = s;
             }
-            if (nj > 0)
+            if (nj > 0 && r->kind == 1)
+            {
+                // a prefetch: nothing waits for its gate / up alone, so one copy per admission (fewer DMA commands)
+                const int gs = sig_next;
+                sig_next = (sig_next + 2) % AG_SIGNALS;
+                hsa_signal_store_relaxed(sigs[gs], nj);
+                for (int j = 0; j < nj; ++j)
+                {
+                    const size_t k = (size_t)li * E + e_[j];
+                    copy(a->slot_base[s_[j]], a->home[k], (int64_t)off_d + a->bytes[k * 3 + 2], a->home_host[k], gs, last);
+                }
+                last = gs;
+                pending.push_back({gs, 0, seq});
+                pending.push_back({-1, 1, seq});      // retires after the part before it
+            }
+            else if (nj > 0)
             {
                 const int gs = sig_next, ds = (sig_next + 1) % AG_SIGNALS;
                 sig_next = (sig_next + 2) % AG_SIGNALS;
