@@ -7,8 +7,9 @@ from .layer import MoELayer
 from .slots import ExpertSlots
 from . import ops
 from . import store
+from . import cpu_lane
 from .store import ExpertStore
 
-__all__ = ["ExpertTable", "ExpertSlots", "ExpertStore", "MoELayer", "ops", "store", "lib", "BmxError", "TF_K2", "TF_K25", "TF_K3", "TF_K4", "TILE_BYTES",
+__all__ = ["ExpertTable", "ExpertSlots", "ExpertStore", "MoELayer", "ops", "store", "cpu_lane", "lib", "BmxError", "TF_K2", "TF_K25", "TF_K3", "TF_K4", "TILE_BYTES",
            "SCORE_SIGMOID", "SCORE_SOFTMAX", "ACT_SILU", "ACT_GELU", "ACT_RELU2", "ACT_SILU_OAI", "PATH_AUTO",
            "PATH_DECODE", "PATH_MID", "PATH_PREFILL", "_lib"]

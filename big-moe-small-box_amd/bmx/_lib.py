@@ -39,6 +39,10 @@ class SlotTable(ctypes.Structure):
                                   "tables", "pjobs", "pfl")]
 
 
+class CpuExpert(ctypes.Structure):
+    _fields_ = [("tr", _P * 3), ("suh", _P * 3), ("svh", _P * 3), ("fmt", ctypes.c_int32 * 3), ("reserved", ctypes.c_int32)]
+
+
 class RouterDesc(ctypes.Structure):
     _fields_ = [("score_fn", ctypes.c_int32), ("renorm", ctypes.c_int32), ("n_group", ctypes.c_int32),
                 ("topk_group", ctypes.c_int32), ("scale", ctypes.c_float), ("reserved", ctypes.c_int32), ("bias", _P)]
@@ -83,6 +87,10 @@ SIGNATURES = {
     "bmx_slot_prefetch_agent": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _I, _I64, _I, ctypes.POINTER(_I64), _P]),
     "bmx_copy_wait": (_I, [_P, _I64, _I, _P]),
     "bmx_copy_wait_layer": (_I, [_P, _I, _I, _P]),
+    "bmx_cpu_expert_rows": (_I, [ctypes.POINTER(CpuExpert), _I, _I, _P, _I, _I, _I, _I, _I, _I, ctypes.c_float, _P, _I]),
+    "bmx_decode_splits": (_I, [ctypes.POINTER(MoeDesc), _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "bmx_cpu_dot2": (_I, [_P, _P, _P, _P, _I]),
+    "bmx_dot2_f32_f16": (_I, [_P, _P, _P, _P, _I, _P]),
     "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
     "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }

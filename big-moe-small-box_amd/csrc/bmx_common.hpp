@@ -292,7 +292,16 @@ __device__ __forceinline__ float sigmoid_fixed(float x)
     return __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
 }
 
+// tanh t = 1 - 2 / (exp(2 t) + 1) on the fixed-sequence exp
+__device__ __forceinline__ float tanh_fixed(float t)
+{
+    const float e = exp_fixed(__fmul_rn(2.0f, t));
+    return __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(e, 1.0f)));
+}
+
 // ---- activations (exllamav3 act_gate semantics, engine/kernels/x16/x16_dev.cu:68-112) ----------------------------------
+// Evaluated with the fixed-sequence exp and correctly rounded operations in a stated order (no hardware approximations),
+// so that a host CPU reproduces every bit (the CPU expert lane).
 __device__ __forceinline__ float act_gate(int act, int gated, float g, float u, float limit)
 {
     if (act == BMX_ACT_SILU_OAI)
@@ -302,24 +311,29 @@ __device__ __forceinline__ float act_gate(int act, int gated, float g, float u, 
             g = fminf(g, limit);
             u = fminf(fmaxf(u, -limit), limit);
         }
-        const float glu = g / (1.0f + __expf(-1.702f * g));
-        return (u + 1.0f) * glu;
+        const float glu = __fdiv_rn(g, __fadd_rn(1.0f, exp_fixed(__fmul_rn(-1.702f, g))));
+        return __fmul_rn(__fadd_rn(u, 1.0f), glu);
     }
     float x;
     if (!gated) x = fmaxf(0.0f, u);
-    else if (act == BMX_ACT_SILU) x = g / (1.0f + __expf(-g));
+    else if (act == BMX_ACT_SILU) x = __fdiv_rn(g, __fadd_rn(1.0f, exp_fixed(-g)));
     else if (act == BMX_ACT_GELU)
     {
-        const float t = 0.797884560803f * (g + 0.044715f * g * g * g);
-        x = 0.5f * g * (1.0f + tanhf(t));
+        const float g3 = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, g), g), g);
+        const float t = __fmul_rn(0.797884560803f, __fadd_rn(g, g3));
+        x = __fmul_rn(__fmul_rn(0.5f, g), __fadd_rn(1.0f, tanh_fixed(t)));
     }
-    else { x = fmaxf(0.0f, g); x = x * x; }
+    else
+    {
+        x = fmaxf(0.0f, g);
+        x = __fmul_rn(x, x);
+    }
     if (limit != 0.0f)
     {
         u = fminf(fmaxf(u, -limit), limit);
         x = fminf(x, limit);
     }
-    return x * u;
+    return __fmul_rn(x, u);
 }
 
 }  // namespace bmx

@@ -50,6 +50,7 @@ struct DecodePlan {
     size_t part_gu_bytes, part_dn_bytes, counters;
 };
 DecodePlan decode_plan(const MoeShape& m);
+int decode_gu_grouped(const MoeShape& m);     // 1: the gate / up epilogue sums the k-splits in four interleaved groups
 size_t decode_ws_bytes(const MoeShape& m);
 // ws layout: [part_gu][part_dn][act rows (used when act_rows == NULL)]; stages: 1 = gate/up, 2 = down (+ combine)
 int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,

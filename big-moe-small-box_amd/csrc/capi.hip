@@ -192,6 +192,35 @@ int bmx_rows_per_group(int T, int topk, int path)
     return path_rows_per_group(p, T);
 }
 
+int bmx_decode_splits(const bmx_moe_desc* desc, int T, int* ks_gu, int* ks_dn, int* grouped_gu)
+{
+    int rc = check_desc(desc, "bmx_decode_splits");
+    if (rc) return rc;
+    if (T <= 0 || !ks_gu || !ks_dn || !grouped_gu) return set_error(BMX_ERR_ARG, "bmx_decode_splits: bad arguments");
+    const MoeShape m = shape_of(desc, T);
+    const DecodePlan p = decode_plan(m);
+    *ks_gu = p.KS_gu;
+    *ks_dn = p.KS_dn;
+    *grouped_gu = decode_gu_grouped(m);
+    return BMX_OK;
+}
+
+static __global__ void k_dot2(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    out[i] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a[i]), __builtin_bit_cast(f16x2, b[i]), c[i], false);
+}
+
+int bmx_dot2_f32_f16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, bmx_stream_t stream)
+{
+    if (n < 0 || (n && (!a || !b || !c || !out))) return set_error(BMX_ERR_ARG, "bmx_dot2_f32_f16: bad arguments");
+    if (n == 0) return BMX_OK;
+    hipLaunchKernelGGL(k_dot2, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream), a, b, c,
+                       out, n);
+    return check_launch("bmx_dot2_f32_f16");
+}
+
 int bmx_resolve_path(int T, int topk, int path) { return T < 0 || topk <= 0 ? -1 : resolve_path(path, T, topk); }
 
 size_t bmx_experts_workspace(const bmx_moe_desc* desc, int T, int path)

@@ -538,6 +538,12 @@ int launch_epilogue(const GvArgs& a, int stage, hipStream_t s)
     return BMX_OK;
 }
 
+int decode_gu_grouped(const MoeShape& m)
+{
+    const DecodePlan p = decode_plan(m);
+    return (long)p.R_max * p.NB < EP_SMALL ? 1 : 0;     // k_gu_epi_w and the one-token down prologue: gu_epi_wave
+}
+
 // ---- plan ------------------------------------------------------------------------------------------------------------
 // BMX_ACT_IN_DOWN=0 keeps the separate gate / up epilogue kernel for one-token calls
 static bool act_in_down_allowed()

@@ -274,6 +274,30 @@ int bmx_copy_wait(bmx_copy_agent* agent, int64_t seq, int part, bmx_stream_t str
  * leaves the target on the device, so a layer whose experts are in place waits for nothing in flight. */
 int bmx_copy_wait_layer(bmx_copy_agent* agent, int li, int part, bmx_stream_t stream);
 
+/* ---- CPU expert lane ----
+ * One expert's y rows (fp32 [nr][H]: the down projection after svh, what BMX_STAGE_COMBINE sums in slot order) for nr
+ * fp16 input rows [nr][H], computed on host cores bit for bit as the GPU decode path (BMX_PATH_DECODE) computes them for
+ * the same rows (the reference's CPU lane, engine/kernels/nv2/nv2_host.cpp and docs/x16.md:1-133, is near-exact; this
+ * one is exact: the device kernels sum in a fixed order, their activation is a fixed sequence of IEEE operations, and
+ * v_dot2_f32_f16's rounding is emulated). ks_gu, ks_dn and grouped_gu are the device's plan for the call being matched
+ * (bmx_decode_splits). Host memory only; threads = worker threads over output columns. Slow: a replay, not a kernel. */
+typedef struct bmx_cpu_expert {
+    const uint8_t* tr[3];      /* host trellis of gate, up, down */
+    const uint16_t* suh[3];    /* host fp16 input scales */
+    const uint16_t* svh[3];    /* host fp16 output scales */
+    int32_t fmt[3];
+    int32_t reserved;
+} bmx_cpu_expert;
+int bmx_cpu_expert_rows(const bmx_cpu_expert* ex, int H, int I, const uint16_t* x_fp16, int nr, int ks_gu, int ks_dn,
+                        int grouped_gu, int act, int gated, float act_limit, float* y_rows, int threads);
+/* The device plan of a decode-path call of T tokens: k-splits of the gate / up and down GEMVs, and whether the gate / up
+ * epilogue sums the splits in four interleaved groups (small launches) or in sequence. */
+int bmx_decode_splits(const bmx_moe_desc* desc, int T, int* ks_gu, int* ks_dn, int* grouped_gu);
+/* out[i] = a[i].lo * b[i].lo + a[i].hi * b[i].hi + c[i] (fp16 pairs, fp32): bmx_cpu_dot2 emulates the device's
+ * v_dot2_f32_f16 on the host; bmx_dot2_f32_f16 runs the instruction (device arrays), to check the emulation. */
+int bmx_cpu_dot2(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n);
+int bmx_dot2_f32_f16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, bmx_stream_t stream);
+
 /* Host-planned staging: n copies src[i] -> dst[i] of bytes[i] (hipMemcpyAsync, e.g. pinned host -> slot), in order on
  * stream (the reference's stage_layer, engine/kernels/nv2/nv2_host.cpp:1558-1593). */
 int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream);
