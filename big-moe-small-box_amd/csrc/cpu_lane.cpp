@@ -300,38 +300,43 @@ const TilePos& tile_pos()
     return tp;
 }
 
-// dense fp16 of a trellis matrix [k/16][n/16] tiles, column-major: Wt[n][k]
-void dequant(const uint8_t* tr, int fmt, int K, int N, uint16_t* W)
+// dense fp16 of a trellis matrix [k/16][n/16] tiles, column-major: Wt[n][k]; tile-rows [kt0, kt1)
+void dequant_rows(const uint8_t* tr, int fmt, int K, int N, uint16_t* W, int kt0, int kt1)
 {
     const Fmt F = fmt_of(fmt);
     const int ring = 256 * F.KA + 16 * __builtin_popcount(F.MASK);
-    int S[256];
+    int start[256];                                   // first bit of each state, wrapped into [0, ring)
     {
         int acc = 0;
         for (int i = 0; i < 256; ++i)
         {
             acc += F.KA + (int)((F.MASK >> (i & 15)) & 1u);
-            S[i] = acc;
+            start[i] = ((acc - 16) % ring + ring) % ring;
         }
     }
     const Codebook& cb = codebook();
     const TilePos& tp = tile_pos();
     const int tn = N / 16;
-    for (int kt = 0; kt < K / 16; ++kt)
+    uint8_t bytes[128 + 4];                           // the ring MSB-first as bytes, its first 4 bytes repeated after it
+    for (int kt = kt0; kt < kt1; ++kt)
         for (int nt = 0; nt < tn; ++nt)
         {
             const uint8_t* t = tr + ((size_t)kt * tn + nt) * F.TB;
-            uint32_t words[32];
-            std::memcpy(words, t, F.TB);
-            auto bit = [&](int b) -> uint32_t {
-                b %= ring;
-                if (b < 0) b += ring;
-                return (words[b >> 5] >> (31 - (b & 31))) & 1u;
-            };
+            for (int w = 0; w < F.TB / 4; ++w)
+            {
+                uint32_t v;
+                std::memcpy(&v, t + 4 * w, 4);
+                bytes[4 * w] = (uint8_t)(v >> 24);
+                bytes[4 * w + 1] = (uint8_t)(v >> 16);
+                bytes[4 * w + 2] = (uint8_t)(v >> 8);
+                bytes[4 * w + 3] = (uint8_t)v;
+            }
+            std::memcpy(bytes + F.TB, bytes, 4);
             for (int p = 0; p < 256; ++p)
             {
-                uint32_t st = 0;
-                for (int j = 0; j < 16; ++j) st = (st << 1) | bit(S[p] - 16 + j);
+                const int b = start[p], i = b >> 3;
+                const uint32_t v = ((uint32_t)bytes[i] << 16) | ((uint32_t)bytes[i + 1] << 8) | bytes[i + 2];
+                const uint32_t st = (v >> (8 - (b & 7))) & 0xffffu;
                 W[(size_t)(nt * 16 + tp.col[p]) * K + kt * 16 + tp.row[p]] = cb.w[st];
             }
         }
@@ -375,6 +380,24 @@ void gemv_parts(const uint16_t* W, int K, int N, const uint16_t* x, int nr, int 
 }
 
 template <typename F>
+void parallel_range(int n, int threads, F fn)
+{
+    if (threads <= 1 || n < 2)
+    {
+        fn(0, n);
+        return;
+    }
+    std::vector<std::thread> th;
+    const int blk = (n + threads - 1) / threads;
+    for (int a = 0; a < n; a += blk)
+    {
+        const int b = a + blk < n ? a + blk : n;
+        th.emplace_back([=] { fn(a, b); });
+    }
+    for (auto& t : th) t.join();
+}
+
+template <typename F>
 void parallel_cols(int N, int threads, F fn)
 {
     if (threads <= 1 || N < 256)
@@ -409,9 +432,11 @@ extern "C" int bmx_cpu_expert_rows(const bmx_cpu_expert* ex, int H, int I, const
     if (threads < 1) threads = 1;
     // weights
     std::vector<uint16_t> Wg((size_t)H * I), Wu((size_t)H * I), Wd((size_t)I * H);
-    dequant(ex->tr[0], ex->fmt[0], H, I, Wg.data());
-    dequant(ex->tr[1], ex->fmt[1], H, I, Wu.data());
-    dequant(ex->tr[2], ex->fmt[2], I, H, Wd.data());
+    parallel_range(H / 16, threads, [&](int a, int b) {
+        dequant_rows(ex->tr[0], ex->fmt[0], H, I, Wg.data(), a, b);
+        dequant_rows(ex->tr[1], ex->fmt[1], H, I, Wu.data(), a, b);
+    });
+    parallel_range(I / 16, threads, [&](int a, int b) { dequant_rows(ex->tr[2], ex->fmt[2], I, H, Wd.data(), a, b); });
     // input rotation per matrix
     std::vector<uint16_t> xg((size_t)nr * H), xu((size_t)nr * H);
     for (int mat = 0; mat < 2; ++mat)

@@ -138,3 +138,49 @@ def test_layer_with_cpu_experts_bitexact(cuda):
     got = bmx.ops.combine(torch.from_numpy(yh).to(cuda), routes, w, H)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_cpu_lane_rows_bitexact_sequential_splits(cuda):
+    """A launch large enough that the gate / up epilogue sums the k-splits in sequence (not in four groups): rows of
+    two experts from the lane against the GPU's, bit for bit."""
+    import bmx
+    from bmx import cpu_lane
+    H, I, E, topk, T = 256, 4096, 8, 3, 171
+    tab = bmx.ExpertTable.random(H, I, E, [(2, 0, 3), (1, 1, 1)] * 4, seed=11, device=cuda)
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16)).to(cuda)
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16)).to(cuda)
+    sel, w = bmx.ops.router_topk(lg, topk, None, 1, 1, bmx.SCORE_SIGMOID, True, 1.0)
+    desc = tab.desc(topk)
+    routes = bmx.ops.dispatch(sel, E, 0, False, bmx.lib().bmx_rows_per_group(T, topk, bmx.PATH_DECODE))
+    y, _ = bmx.ops.moe_experts(desc, x, routes, path=bmx.PATH_DECODE)
+    torch.cuda.synchronize()
+    ks_gu, ks_dn, grouped = cpu_lane.decode_splits(desc, T)
+    say("sequential case splits", ks_gu, ks_dn, "grouped", grouped)
+    assert grouped == 0
+    y = y.cpu().numpy()
+    rt = routes.row_token.cpu().numpy()
+    offs = routes.offsets.cpu().numpy()
+    xs = x.cpu().numpy()
+    for e in (0, 1):
+        r0, r1 = int(offs[e]), int(offs[e + 1])
+        r1 = min(r1, r0 + 24)
+        yc = cpu_lane.expert_rows(tab.host_expert(e), H, I, xs[rt[r0:r1]], ks_gu, ks_dn, grouped, threads=16)
+        assert (yc.view(np.uint32) == y[r0:r1].view(np.uint32)).all(), e
+        say("expert", e, "rows bit-identical", r1 - r0)
+
+
+def test_cpu_lane_time_c2_expert(cuda):
+    """Reported, not asserted: one C2-shaped expert (H 4096, I 1536, K 3) for one token on the host's cores."""
+    import time
+    import os
+    import bmx
+    from bmx import cpu_lane
+    H, I = 4096, 1536
+    tab = bmx.ExpertTable.random(H, I, 1, (bmx.TF_K3,) * 3, seed=2, device=cuda)
+    ex = tab.host_expert(0)
+    x = np.random.default_rng(2).standard_normal((1, H)).astype(np.float16)
+    th = min(16, os.cpu_count() or 1)
+    t0 = time.perf_counter()
+    cpu_lane.expert_rows(ex, H, I, x, 16, 4, 1, threads=th)
+    say(f"cpu lane: one C2 expert, one token, {th} threads: {(time.perf_counter() - t0) * 1e3:.1f} ms")
