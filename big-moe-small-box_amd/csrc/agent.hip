@@ -131,6 +131,7 @@ static void agent_loop(bmx_copy_agent* a)
         a->copies.fetch_add(1, std::memory_order_relaxed);
         a->copied_bytes.fetch_add(n, std::memory_order_relaxed);
     };
+    auto last_work = std::chrono::steady_clock::now();
     for (;;)
     {
         bool idle = true;
@@ -216,8 +217,14 @@ static void agent_loop(bmx_copy_agent* a)
         if (idle)
         {
             if (a->stop.load(std::memory_order_acquire) && pending.empty()) break;
-            __builtin_ia32_pause();
+            // spin while records keep coming (a decode step publishes one per layer); after 2 ms without any, poll
+            // every 50 us so an idle table does not hold a core
+            const auto now = std::chrono::steady_clock::now();
+            if (pending.empty() && now - last_work > std::chrono::milliseconds(2))
+                std::this_thread::sleep_for(std::chrono::microseconds(50));
+            else __builtin_ia32_pause();
         }
+        else last_work = std::chrono::steady_clock::now();
     }
     for (auto& g : sigs) hsa_signal_destroy(g);
 }
