@@ -123,10 +123,10 @@ def test_slot_prefetch_matches_oracle(cuda, oracle, S, maxj):
         assert st[5] > 0 and st[6] > 0
 
 
-@pytest.mark.parametrize("copies", ["kernel", "dma"])
-def test_slot_copies_deliver_home_bytes(cuda, copies):
+@pytest.mark.parametrize("copies,home", [("kernel", "host"), ("dma", "host"), ("dma", "device")])
+def test_slot_copies_deliver_home_bytes(cuda, copies, home):
     import bmx
-    layers = small_layers(2, 12, 256, 128, 30, "host", fmts=(bmx.TF_K2, bmx.TF_K25, bmx.TF_K4))
+    layers = small_layers(2, 12, 256, 128, 30, home, fmts=(bmx.TF_K2, bmx.TF_K25, bmx.TF_K4))
     slots = bmx.ExpertSlots(layers, 7, maxj=6, copies=copies)
     rng = np.random.default_rng(5)
     for step in range(12):
@@ -145,10 +145,10 @@ def test_slot_copies_deliver_home_bytes(cuda, copies):
             s = slotof[li, e]
             if s < 0:
                 continue
-            home = layers[li].arena[e].numpy()
+            rec = layers[li].arena[e].cpu().numpy()
             for m, off in enumerate((0, t0.off_u, t0.off_d)):
                 nb = layers[li].mat_bytes(e, m)
-                assert np.array_equal(arena[s, off:off + nb], home[off:off + nb]), (li, e, m)
+                assert np.array_equal(arena[s, off:off + nb], rec[off:off + nb]), (li, e, m)
             checked += 1
     say("resident experts checked", checked)
     assert checked == 7
