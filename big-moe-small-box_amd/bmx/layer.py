@@ -7,7 +7,8 @@ Names and argument meaning follow the reference:
   run_bszN(z, sel, rw) -> out [bsz, H] fp32                                     exllamav3 bc.run_bszN, engine/nv2.py:634
   cpu_split_combine(fhs, cpu_partial, cpu_pending, shape) -> fhs                engine/tiers.py:730-739
   combine(fhs) -> fhs                                                           engine/nv2.py:489-493 (Nv2.combine)
-Every call enqueues on torch's current stream; nothing synchronises the host.
+Every call enqueues on torch's current stream; nothing synchronises the host (verify_on_cpu, a host-side check with
+the exact CPU lane, excepted).
 """
 import ctypes
 
@@ -105,6 +106,37 @@ class MoELayer:
         stage(L.STAGE_COMBINE)
         self._routes = routes
         return out
+
+    def verify_on_cpu(self, z, sel, rw, threads=16, y_rows=None):
+        """Recompute every expert row of a decode-path call on the host with the exact CPU lane and compare it with the
+        GPU's, bit for bit (a check for silent corruption: the two must agree exactly). Synchronises. Returns the
+        mismatching (row, expert) pairs; y_rows: the GPU's rows to check (default: computed here)."""
+        import numpy as np
+        from . import cpu_lane
+        x = z.view(-1, self.hidden_size)
+        if x.dtype != torch.float16 or not x.is_contiguous():
+            x = x.half().contiguous()
+        T = x.shape[0]
+        sel = sel.view(T, -1).long().contiguous()
+        routes = ops.dispatch(sel, self.num_local_experts, self.routing_first, self.table.has_shared,
+                              L.lib().bmx_rows_per_group(T, self.num_experts_per_tok, L.PATH_DECODE))
+        if y_rows is None:
+            y_rows, _ = ops.moe_experts(self.desc, x, routes, L.PATH_DECODE)
+        ks_gu, ks_dn, grouped = cpu_lane.decode_splits(self.desc, T)
+        y = y_rows.cpu().numpy()
+        offs = routes.offsets.cpu().numpy()
+        rt = routes.row_token.cpu().numpy()
+        xs = x.cpu().numpy()
+        bad = []
+        for e in range(self.num_local_experts + (1 if self.table.has_shared else 0)):
+            r0, r1 = int(offs[e]), int(offs[e + 1])
+            if r1 <= r0:
+                continue
+            yc = cpu_lane.expert_rows(self.table.host_expert(e), self.hidden_size, self.intermediate_size, xs[rt[r0:r1]],
+                                      ks_gu, ks_dn, grouped, self.act, self.gated, self.act_limit, threads)
+            for i in np.flatnonzero((yc.view(np.uint32) != y[r0:r1].view(np.uint32)).any(1)):
+                bad.append((r0 + int(i), e))
+        return bad
 
     def cpu_split_combine(self, fhs, cpu_partial=None, cpu_pending=False, shape=None):
         if cpu_pending and cpu_partial is not None:

@@ -184,3 +184,24 @@ def test_cpu_lane_time_c2_expert(cuda):
     t0 = time.perf_counter()
     cpu_lane.expert_rows(ex, H, I, x, 16, 4, 1, threads=th)
     say(f"cpu lane: one C2 expert, one token, {th} threads: {(time.perf_counter() - t0) * 1e3:.1f} ms")
+
+
+def test_layer_verify_on_cpu_finds_a_flipped_bit(cuda):
+    """MoELayer.verify_on_cpu: the GPU's expert rows agree with the exact CPU lane; one flipped low bit in a copy of the
+    GPU's rows (planted on the host) is reported at its row."""
+    import bmx
+    H, I, E, topk, T = 512, 256, 12, 4, 3
+    tab = bmx.ExpertTable.random(H, I, E, (bmx.TF_K3, bmx.TF_K2, bmx.TF_K4), shared=True, seed=21, device=cuda)
+    layer = bmx.MoELayer(tab, topk, score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0, act=bmx.ACT_GELU)
+    rng = np.random.default_rng(21)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16)).to(cuda)
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16)).to(cuda)
+    sel, w = layer.routing_fn(T, None, x, {"logits": lg})
+    assert layer.verify_on_cpu(x, sel, w) == []
+    routes = bmx.ops.dispatch(sel, E, 0, True, bmx.lib().bmx_rows_per_group(T, topk, bmx.PATH_DECODE))
+    y, _ = bmx.ops.moe_experts(layer.desc, x, routes, path=bmx.PATH_DECODE)
+    yb = y.cpu().numpy().copy()
+    r = 5
+    yb.view(np.uint32)[r, 100] ^= 1
+    bad = layer.verify_on_cpu(x, sel, w, y_rows=torch.from_numpy(yb))
+    assert [b[0] for b in bad] == [r]
