@@ -70,3 +70,16 @@ def test_cpu_lane_rejects_bad_splits():
     from bmx import cpu_lane
     with pytest.raises(bmx.BmxError, match="k-splits"):
         cpu_lane.expert_rows(host_expert(256, 128, (2, 2, 2), 1), 256, 128, np.zeros((1, 256), np.float16), 3, 1, 1)
+
+
+@pytest.mark.parametrize("fmts,ks", [((2, 0, 3), (2, 1)), ((1, 1, 1), (1, 2)), ((3, 2, 0), (4, 2))])
+def test_cpu_lane_vector_equals_scalar(monkeypatch, fmts, ks):
+    """The AVX-512 path (8 output columns per step) gives the scalar path's bits (where the host has AVX-512)."""
+    from bmx import cpu_lane
+    H, I = 512, 256
+    ex = host_expert(H, I, fmts, seed=sum(fmts) * 7 + ks[0])
+    x = np.random.default_rng(ks[0]).standard_normal((5, H)).astype(np.float16) * np.float16(4.0)
+    y_vec = cpu_lane.expert_rows(ex, H, I, x, ks[0], ks[1], 1, 2, True, 0.0, threads=3)
+    monkeypatch.setenv("BMX_CPU_LANE_SCALAR", "1")
+    y_sca = cpu_lane.expert_rows(ex, H, I, x, ks[0], ks[1], 1, 2, True, 0.0, threads=3)
+    assert np.array_equal(y_vec.view(np.uint32), y_sca.view(np.uint32))
