@@ -30,16 +30,8 @@
 
 namespace bmx {
 
-constexpr int AG_RING = 64;      // published records in flight (a layer's step waits on its own record's copies)
 constexpr int AG_PENDING = 256;  // parts in flight
 constexpr int AG_SIGNALS = 2 * AG_PENDING;   // a signal is reused only after every part issued after it has retired
-
-// flags[0] gate / up done, flags[1] down done (sequence numbers); flags[2] abort (the waits end at once); flags[3]
-// set by a wait that ran out of time
-struct AgentShared {
-    int32_t flags[4];
-    SlotPub ring[AG_RING];
-};
 
 }  // namespace bmx
 
@@ -170,6 +162,8 @@ static void agent_loop(bmx_copy_agent* a)
                 e_[nj] = e;
                 s_[nj++] = s;
             }
+            // the ring slot may be written again (by record next + AG_RING) from here on
+            __atomic_store_n(&a->sh->consumed, (int32_t)next, __ATOMIC_RELEASE);
             if (nj > 0 && r->kind == 1)
             {
                 // a prefetch: nothing waits for its gate / up alone, so one copy per admission (fewer DMA commands)
@@ -373,8 +367,8 @@ int bmx_slot_step_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, cons
     if (!a || !seq) return set_error(BMX_ERR_ARG, "bmx_slot_step_agent: null agent or seq");
     const int64_t q = a->next_seq + 1;
     if (li < 0 || li >= a->t.L) return set_error(BMX_ERR_ARG, "bmx_slot_step_agent: bad layer %d", li);
-    const int rc = launch_slot_step(t, li, sel, n, first, admit, static_cast<hipStream_t>(stream),
-                                    &a->sh_dev->ring[q % AG_RING], (int32_t)q, a->need);
+    const int rc = launch_slot_step(t, li, sel, n, first, admit, static_cast<hipStream_t>(stream), a->sh_dev, (int32_t)q,
+                                    a->need, a->wait_ticks);
     if (rc) return rc;
     a->next_seq = q;
     *seq = q;
@@ -386,8 +380,8 @@ int bmx_slot_prefetch_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, 
 {
     if (!a || !seq) return set_error(BMX_ERR_ARG, "bmx_slot_prefetch_agent: null agent or seq");
     const int64_t q = a->next_seq + 1;
-    const int rc = launch_slot_prefetch(t, li, sel, n, first, limit, 0, static_cast<hipStream_t>(stream),
-                                        &a->sh_dev->ring[q % AG_RING], (int32_t)q);
+    const int rc = launch_slot_prefetch(t, li, sel, n, first, limit, 0, static_cast<hipStream_t>(stream), a->sh_dev,
+                                        (int32_t)q, a->wait_ticks);
     if (rc) return rc;
     a->next_seq = q;
     *seq = q;

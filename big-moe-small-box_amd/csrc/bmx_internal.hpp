@@ -67,12 +67,24 @@ struct SlotPub {
     int32_t seq, li, n, kind;     // kind: 0 step, 1 prefetch
     int32_t pairs[2 * 64];        // (expert, slot) of each admission
 };
-// need (with pub, steps only): need[li] = the last record layer li's next products depend on (seq when the step admitted
-// experts, seq - 1 when it did not: its prefetched hits came with earlier records)
+constexpr int AG_RING = 64;       // records in the ring: record q lives in ring[q % AG_RING]
+// The memory a copy agent shares with the kernels. flags[0] gate / up done, flags[1] down done (sequence numbers);
+// flags[2] abort (the waits end at once); flags[3] set by a wait that ran out of time. consumed: the last record the
+// agent has read out of the ring (its slot may be written again by record consumed + AG_RING).
+struct AgentShared {
+    int32_t flags[4];
+    int32_t consumed;
+    int32_t pad[3];
+    SlotPub ring[AG_RING];
+};
+// Publishing (sh != null): the step writes ring[seq % AG_RING] once the agent has consumed record seq - AG_RING, waiting
+// at most wait_limit wall-clock ticks (then it sets flags[3] and publishes nothing). need (steps only): need[li] = the
+// last record layer li's next products depend on (seq when the step admitted experts, seq - 1 when it did not: its
+// prefetched hits came with earlier records)
 int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
-                     SlotPub* pub = nullptr, int32_t seq = 0, int32_t* need = nullptr);
+                     AgentShared* sh = nullptr, int32_t seq = 0, int32_t* need = nullptr, int64_t wait_limit = 0);
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
-                         hipStream_t s, SlotPub* pub = nullptr, int32_t seq = 0);
+                         hipStream_t s, AgentShared* sh = nullptr, int32_t seq = 0, int64_t wait_limit = 0);
 int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStream_t s);
 
 // moe_prefill.hip (same ws / stage conventions; ws layout [xt][part_gu][act rows][part_dn])

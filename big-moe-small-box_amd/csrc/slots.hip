@@ -19,10 +19,33 @@ struct SlotArgs {
     int li, n, admit;
     int pf;       // 0: a step; 1: a prefetch into job buffer `buf` with at most `limit` candidates
     int limit, buf;
-    SlotPub* pub; // or null: the admissions are also published to the copy agent under sequence number seq
+    AgentShared* sh;  // or null: the admissions are also published to the copy agent's ring under sequence number seq
     int32_t seq;
-    int32_t* need;   // steps with pub: need[li] = the last record the layer's products depend on
+    int32_t* need;    // steps that publish: need[li] = the last record the layer's products depend on
+    int64_t wait_limit;   // wall-clock ticks a publish waits for its ring slot
 };
+
+// Until the agent has read record seq - AG_RING out of the ring slot seq will reuse (bounded; false: the agent aborted,
+// a wait ran out of time, or this one did, which it records in flags[3]). One lane.
+__device__ bool ring_slot_free(AgentShared* sh, int32_t seq, int64_t limit)
+{
+    const int32_t want = seq - AG_RING;
+    const int64_t t0 = wall_clock64();
+    for (;;)
+    {
+        const int32_t c = __hip_atomic_load(&sh->consumed, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        if ((int32_t)(c - want) >= 0) return true;
+        if (__hip_atomic_load(&sh->flags[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
+            __hip_atomic_load(&sh->flags[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM))
+            return false;
+        if (wall_clock64() - t0 > limit)
+        {
+            __hip_atomic_store(&sh->flags[3], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
 
 __device__ __forceinline__ int tile_bytes_dev(int fmt)
 {
@@ -132,6 +155,13 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     if (wave == 0)
     {
         int32_t* jobs = a.pf ? prefetch_jobs(t, a.buf) + 1 : t.jobs;
+        SlotPub* pub = nullptr;
+        if (a.sh)
+        {
+            int ok = 0;
+            if (lane == 0) ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
+            if (__shfl(ok, 0)) pub = &a.sh->ring[a.seq % AG_RING];
+        }
         int hand = t.ctl[0], nj = 0, novictim = 0, evicted = 0, wasted = 0;
         const int chunk = S < 64 ? S : 64;
         const int maxp = a.pf ? S : 2 * S;      // a prefetch passes referenced slots without clearing: one revolution
@@ -195,22 +225,22 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                 jobs[2 * nj] = ex;
                 jobs[2 * nj + 1] = s;
                 if (!a.pf) t.fresh[ex] = 1;
-                if (a.pub)
+                if (pub)
                 {
-                    a.pub->pairs[2 * nj] = ex;
-                    a.pub->pairs[2 * nj + 1] = s;
+                    pub->pairs[2 * nj] = ex;
+                    pub->pairs[2 * nj + 1] = s;
                 }
             }
             ++nj;
         }
         if (lane == 0)
         {
-            if (a.pub)
+            if (pub)
             {
-                a.pub->li = a.li;
-                a.pub->n = nj;
-                a.pub->kind = a.pf;
-                __hip_atomic_store(&a.pub->seq, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+                pub->li = a.li;
+                pub->n = nj;
+                pub->kind = a.pf;
+                __hip_atomic_store(&pub->seq, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
                 if (!a.pf && a.need) a.need[a.li] = nj > 0 ? a.seq : a.seq - 1;
             }
             if (a.admit && S > 0) t.ctl[0] = hand;
@@ -290,7 +320,7 @@ static int check_table(const bmx_slot_table* t, const char* who)
 }
 
 int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
-                     SlotPub* pub, int32_t seq, int32_t* need)
+                     AgentShared* sh, int32_t seq, int32_t* need, int64_t wait_limit)
 {
     int rc = check_table(t, "bmx_slot_step");
     if (rc) return rc;
@@ -305,15 +335,16 @@ int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n,
     a.pf = 0;
     a.limit = 0;
     a.buf = 0;
-    a.pub = pub;
+    a.sh = sh;
     a.seq = seq;
     a.need = need;
+    a.wait_limit = wait_limit;
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
     return check_launch("bmx_slot_step");
 }
 
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
-                         hipStream_t s, SlotPub* pub, int32_t seq)
+                         hipStream_t s, AgentShared* sh, int32_t seq, int64_t wait_limit)
 {
     int rc = check_table(t, "bmx_slot_prefetch");
     if (rc) return rc;
@@ -330,9 +361,10 @@ int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, in
     a.pf = 1;
     a.limit = limit;
     a.buf = buf;
-    a.pub = pub;
+    a.sh = sh;
     a.seq = seq;
     a.need = nullptr;
+    a.wait_limit = wait_limit;
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
     return check_launch("bmx_slot_prefetch");
 }

@@ -123,6 +123,60 @@ def test_slot_prefetch_matches_oracle(cuda, oracle, S, maxj):
         assert st[5] > 0 and st[6] > 0
 
 
+def resident_bytes_match(slots, layers):
+    """Every resident expert's slot holds its home record's gate / up / down bytes; returns how many were checked."""
+    L, E = len(layers), layers[0].E
+    slotof = slots.slotof.cpu().numpy().reshape(L, E)
+    arena = slots.arena.cpu().numpy()
+    t0 = layers[0]
+    checked = 0
+    for li in range(L):
+        for e in range(E):
+            s = slotof[li, e]
+            if s < 0:
+                continue
+            rec = layers[li].arena[e].cpu().numpy()
+            for m, off in enumerate((0, t0.off_u, t0.off_d)):
+                nb = layers[li].mat_bytes(e, m)
+                assert np.array_equal(arena[s, off:off + nb], rec[off:off + nb]), (li, e, m)
+            checked += 1
+    say("resident experts checked", checked)
+    return checked
+
+
+def test_agent_ring_wraps_without_waits(cuda):
+    """Three times the agent's 64-record ring of steps and prefetches published back to back, no layer waiting in
+    between: every record is handed over in order (a step only reuses a ring slot the agent has read), and the slots
+    end up holding their homes' bytes."""
+    import time
+    import bmx
+    layers = small_layers(2, 12, 256, 128, 40, "host", fmts=(bmx.TF_K3, bmx.TF_K2, bmx.TF_K4))
+    slots = bmx.ExpertSlots(layers, 7, maxj=6, copies="dma")
+    rng = np.random.default_rng(9)
+    records = 0
+    for step in range(96):
+        li = step % 2
+        slots.step(li, torch.from_numpy(rng.integers(0, 12, 5).astype(np.int64)).cuda())
+        slots.prefetch(1 - li, torch.from_numpy(rng.permutation(12)[:3].astype(np.int64)).cuda(), limit=2)
+        records += 2
+    slots.wait_copies(0)
+    slots.wait_copies(1)
+    torch.cuda.synchronize()
+    t0 = time.time()
+    while slots.agent_status()[0] < records and time.time() - t0 < 2.0:
+        time.sleep(0.001)
+    rec, ncopies, nbytes, gu, dn, late = slots.agent_status()
+    say("agent records", rec, "copies", ncopies, "bytes", nbytes, "flags", gu, dn, late)
+    assert rec == records and late == 0
+    t0 = time.time()
+    while slots.agent_status()[4] < records and time.time() - t0 < 2.0:
+        time.sleep(0.001)
+    assert slots.agent_status()[3] == slots.agent_status()[4] == records
+    torch.cuda.synchronize()
+    assert resident_bytes_match(slots, layers) == 7
+    slots.close()
+
+
 @pytest.mark.parametrize("copies,home", [("kernel", "host"), ("dma", "host"), ("dma", "device")])
 def test_slot_copies_deliver_home_bytes(cuda, copies, home):
     import bmx
@@ -136,22 +190,7 @@ def test_slot_copies_deliver_home_bytes(cuda, copies, home):
     slots.wait_copies(0)
     slots.wait_copies(1)
     torch.cuda.synchronize()
-    slotof = slots.slotof.cpu().numpy().reshape(2, 12)
-    arena = slots.arena.cpu().numpy()
-    t0 = layers[0]
-    checked = 0
-    for li in range(2):
-        for e in range(12):
-            s = slotof[li, e]
-            if s < 0:
-                continue
-            rec = layers[li].arena[e].cpu().numpy()
-            for m, off in enumerate((0, t0.off_u, t0.off_d)):
-                nb = layers[li].mat_bytes(e, m)
-                assert np.array_equal(arena[s, off:off + nb], rec[off:off + nb]), (li, e, m)
-            checked += 1
-    say("resident experts checked", checked)
-    assert checked == 7
+    assert resident_bytes_match(slots, layers) == 7
     if copies == "dma":
         import time
         t0 = time.time()
