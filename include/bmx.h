@@ -253,7 +253,9 @@ int bmx_slot_prefetch_copy(const bmx_slot_table* t, int li, int buf, int mats, b
  * its admissions under the next sequence number (*seq); the agent's thread hands each published record, in order, to
  * the SDMA engines (per admission the gate / up part, then the down matrices) and marks each part done; bmx_copy_wait
  * orders a stream after a record's part (0 gate / up, 1 down) with a one-wave kernel that polls the mark (bounded: after
- * 5 s it gives up and bmx_copy_agent_status reports it). A kernel reading pinned host memory at link speed holds back
+ * 5 s it gives up and bmx_copy_agent_status reports it). The records go through a ring of 64 in host memory: a step or
+ * prefetch writes its slot only once the agent has read the record 64 before it (bounded the same way; publishing
+ * nothing and reporting it when the limit passes). A kernel reading pinned host memory at link speed holds back
  * HBM-bound kernels on other streams; the DMA engines do not. Calls on one agent come from one host thread, its steps on
  * one stream. home[L * E]: each expert's record address (pinned host or device memory; gate at 0, up at off_u, down at
  * off_d, as the slots); mat_bytes[L * E * 3]: its trellis bytes. */
