@@ -272,13 +272,20 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const int col = cb * 128 + 8 * j;
-    float gu[16];
-    sum_splits<4, 4>(a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j, (size_t)a.R_max * a.NB * 256, a.KS_gu, gu);
     float g[8], v[8];
+    if (a.gu_half)
+    {
+        const uint16_t* hp = reinterpret_cast<const uint16_t*>(a.part_gu) + ((size_t)r * a.NB + cb) * 256 + 8 * j;
+        unpack8(ldg4(hp), g);
+        unpack8(ldg4(hp + 128), v);
+    }
+    else
+    {
+        float gu[16];
+        sum_splits<4, 4>(a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j, (size_t)a.R_max * a.NB * 256, a.KS_gu, gu);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) { g[i] = gu[i]; v[i] = gu[8 + i]; }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(g[i])); v[i] = h2f(f2h_r(v[i])); }
+        for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(gu[i])); v[i] = h2f(f2h_r(gu[8 + i])); }
+    }
     had128_x8(g);
     had128_x8(v);
     float svg[8], svu[8], sud[8];
@@ -307,20 +314,31 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
 {
     const int lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
     const int nrows = a.offsets[a.NE], e = a.row_expert[r];
-    const size_t stride = (size_t)a.R_max * a.NB * 256;
-    const float* p = a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j + (size_t)q * stride;
-    float gu[16];
-    sum_splits<4, B>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
+    float g[8], v[8];
+    if (a.gu_half)
+    {
+        // one fp16 split: every lane group loads the same values
+        const uint16_t* hp = reinterpret_cast<const uint16_t*>(a.part_gu) + ((size_t)r * a.NB + cb) * 256 + 8 * j;
+        unpack8(ldg4(hp), g);
+        unpack8(ldg4(hp + 128), v);
+        if (r >= nrows) return;
+    }
+    else
+    {
+        const size_t stride = (size_t)a.R_max * a.NB * 256;
+        const float* p = a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j + (size_t)q * stride;
+        float gu[16];
+        sum_splits<4, B>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor16_f(gu[i]);
+        for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor16_f(gu[i]);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor32_f(gu[i]);
-    if (r >= nrows) return;
+        for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor32_f(gu[i]);
+        if (r >= nrows) return;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(gu[i])); v[i] = h2f(f2h_r(gu[8 + i])); }
+    }
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const int col = cb * 128 + 8 * j;
-    float g[8], v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(gu[i])); v[i] = h2f(f2h_r(gu[8 + i])); }
     had128_x8(g);
     had128_x8(v);
     float svg[8], svu[8], sud[8];
@@ -663,6 +681,7 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
     // for: the down GEMV computes the activation of its k-range itself, once per output block instead of once, for
     // one launch and one round trip through memory fewer. Worth it up to 16 output blocks (H <= 2048: 31.0 -> 29.6 us
     // for a 64-expert top-8 layer of H 2048, I 768); at 32 blocks the repeated epilogue costs what it saves.
+    a.gu_half = 0;
     a.act_in_down = rows_per_group_of(m.T) == 1 && (stages & (1 << BMX_STAGE_ACT)) && (stages & (1 << BMX_STAGE_DOWN)) &&
                     !act_rows && m.H / 128 <= 16 && act_in_down_allowed();
     switch (rows_per_group_of(m.T))

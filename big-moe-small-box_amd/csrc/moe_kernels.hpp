@@ -32,6 +32,8 @@ struct GvArgs {
     const int32_t* fresh;      // [E] admitted-this-step flags of the expert-slot table, or null
     int filter;                // gate / up groups: 0 all, 1 experts not fresh, 2 fresh experts only
     int act_in_down;           // the down GEMV computes its input rows from the gate / up partials (one-row groups)
+    int gu_half;               // part_gu holds one split as fp16 [row][128-column block][matrix][128], each value the
+                               // epilogue's own rounding of that split's sum (RN of 0.0f + product): same bits downstream
 };
 
 // group filter of the split gate / up stages (the shared expert, index E, is never fresh)

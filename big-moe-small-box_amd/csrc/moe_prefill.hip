@@ -373,7 +373,9 @@ __global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
                 if (row >= nr) continue;
                 const size_t r = (size_t)(r0 + row);
                 if (DOWN) a.part_dn[(r * a.NBH + cbo) * 128 + col] = acc[mb][nb][v];
-                else a.part_gu[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] = acc[mb][nb][v];
+                else
+                    reinterpret_cast<uint16_t*>(a.part_gu)[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] =
+                        f2h_r(0.0f + acc[mb][nb][v]);
             }
         }
     }
@@ -633,6 +635,7 @@ int launch_mid_experts(const MoeShape& m, const void* x, const bmx_routes* r, fl
     a.fresh = m.fresh;
     a.filter = 0;
     a.act_in_down = 0;
+    a.gu_half = 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);
@@ -693,6 +696,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.fresh = m.fresh;
     a.filter = 0;
     a.act_in_down = 0;
+    a.gu_half = 1;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);
