@@ -339,8 +339,8 @@ def main():
                     help="run one plain device copy of MIB MiB first (scale reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the layer shards by experts "
-              f"across GPUs only in design, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: measures one GPU; --gpus {args.gpus} is not supported (sharding the layer's experts across "
+              f"GPUs is not implemented)", file=sys.stderr)
         sys.exit(2)
 
     if args.config == "c4":
