@@ -30,7 +30,7 @@ enum bmx_status {
     BMX_ERR_ARG = 1,         /* invalid argument (shape, format, null pointer, unsupported size) */
     BMX_ERR_HIP = 2,         /* a HIP runtime call failed (launch, copy, event) */
     BMX_ERR_WORKSPACE = 3,   /* workspace smaller than the matching *_workspace() query */
-    BMX_ERR_UNSUPPORTED = 4  /* valid request this build does not implement */
+    BMX_ERR_UNSUPPORTED = 4  /* valid request the library does not implement */
 };
 
 /* EXL3 trellis formats: the reference's TF_K2 / TF_K25 / TF_K3 numbering (engine/kernels/nv2/ft_n135.h:78-81) plus

@@ -1,8 +1,8 @@
 /*
  * CPU oracle for the routed-expert MoE layer: TEST INFRASTRUCTURE ONLY.
  *
- * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library, and only as the checker.
- * The product path (libbmx.so) never links, calls or falls back to it.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library, and only as a reference
+ * to check against. The product path (libbmx.so) never links, calls or falls back to it.
  *
  * Plain C99 restatement of the arithmetic of the reference's hot path (Big-MoE-Small-Box + exllamav3 1.6.6 semantics):
  * EXL3 trellis state extraction (integer and fractional K), the tensor-core tile permutation, the mul1 codebook, the

@@ -1,7 +1,7 @@
 """CPU oracle for the routed-expert MoE layer: TEST INFRASTRUCTURE ONLY.
 
-Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, and only as the checker. The
-product (libbmx.so and the bmx package) never imports, links or falls back to it.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, and only as a reference to
+check against. The product (libbmx.so and the bmx package) never imports, links or falls back to it.
 
 Two independent restatements of the reference's EXL3 decode live here:
   * liboracle.so (bmx_oracle.c): the C oracle for decode, rotations, expert, layer, router, dispatch and slot table;
