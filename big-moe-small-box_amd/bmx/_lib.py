@@ -83,6 +83,7 @@ SIGNATURES = {
     "bmx_copy_agent_create": (_I, [ctypes.POINTER(SlotTable), _P, _P, ctypes.POINTER(_P)]),
     "bmx_copy_agent_destroy": (_I, [_P]),
     "bmx_copy_agent_status": (_I, [_P, _P]),
+    "bmx_copy_agent_control": (_I, [_P, _I, _I64]),
     "bmx_slot_step_agent": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _I, _I64, _I, ctypes.POINTER(_I64), _P]),
     "bmx_slot_prefetch_agent": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _I, _I64, _I, ctypes.POINTER(_I64), _P]),
     "bmx_copy_wait": (_I, [_P, _I64, _I, _P]),

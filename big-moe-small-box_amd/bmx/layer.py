@@ -55,7 +55,7 @@ class MoELayer:
     # ---- engine hook: residency before the experts run ----
     def layer(self, li, sel, w, z, bsz):
         if self.slots is not None:
-            self.slots.step(li, sel, self.routing_first)
+            self.slots.step(li, sel, True, first=self.routing_first)
         return sel, w, False
 
     # ---- experts + combine ----

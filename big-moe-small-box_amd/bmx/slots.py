@@ -17,11 +17,12 @@ from . import _lib as L
 
 
 class ExpertSlots:
-    def __init__(self, layers, S, maxj=32, disabled=(), copies="kernel"):
+    def __init__(self, layers, S, maxj=32, disabled=(), copies="kernel", first=0):
         """layers: one ExpertTable per layer (same H, I, E and record geometry); S slots; maxj admissions per step;
         disabled: slot indices never used. copies: "kernel" (a copy kernel on the side stream reads the homes) or
         "dma" (a host thread of the library issues them on the DMA engines, which leaves the other kernels their
-        memory bandwidth; the layer's stages wait on the copies with a small polling kernel)."""
+        memory bandwidth; the layer's stages wait on the copies with a small polling kernel). first: global id of
+        local expert 0 (routing_first), held here as the reference's Pool holds it (engine/tiers.py:272)."""
         if copies not in ("kernel", "dma"):
             raise ValueError("ExpertSlots: copies must be 'kernel' or 'dma'")
         t0 = layers[0]
@@ -29,6 +30,7 @@ class ExpertSlots:
             if (t.H, t.I, t.E, t.rec, t.off_u, t.off_d) != (t0.H, t0.I, t0.E, t0.rec, t0.off_u, t0.off_d):
                 raise ValueError("ExpertSlots: layers must share H, I, E and the record geometry")
         self.layers, self.L, self.E, self.S, self.maxj = layers, len(layers), t0.E, S, maxj
+        self.first = int(first)
         dev = t0.device
         i32 = dict(dtype=torch.int32, device=dev)
         self.arena = torch.empty((max(S, 1), t0.rec), dtype=torch.uint8, device=dev)
@@ -56,6 +58,7 @@ class ExpertSlots:
                                   P(self.pjobs), P(self.pfl))
         self.side = torch.cuda.Stream(device=dev)
         self.copied = [None] * self.L        # event: copies of the layer's last step done
+        self.last_copied = None              # event: copies of the last step (any layer) done: they read its job buffer
         self.pf_copied = [None, None]        # event per prefetch job buffer: its last copies done
         self.pf_calls = 0
         self.copies = copies
@@ -86,16 +89,24 @@ class ExpertSlots:
 
     def agent_status(self):
         """dma: (records, copies, bytes copied, gate / up mark, down mark, a wait ran out of time); raises if a copy
-        failed or a wait ran out of time."""
+        failed, the agent aborted or a wait ran out of time (final: the slot contents of copies that had not completed
+        are not trusted, so the layer calls since the failure are to be discarded)."""
         st = (ctypes.c_int64 * 6)()
         L.check(L.lib().bmx_copy_agent_status(self.agent, st), "bmx_copy_agent_status")
         return tuple(st)
 
-    def step(self, li, sel, first=0, admit=True):
-        """CLOCK step of layer li over the picks sel (int64 device tensor) on the current stream, then the copies of
-        its admissions on the side stream."""
+    def check(self):
+        """Raise if the copy agent has failed (dma; a host read of shared memory, no synchronisation)."""
+        if self.agent is not None:
+            L.check(L.lib().bmx_copy_agent_status(self.agent, None), "ExpertSlots")
+
+    def step(self, li, sel, admit=True, *, first=None):
+        """CLOCK step of layer li over the picks sel (int64 device tensor of global ids) on the current stream, then the
+        copies of its admissions on the side stream: Pool.step(li, sel, admit) (engine/tiers.py:360-373). first
+        overrides the table's routing_first for this call. Raises if the copy agent has failed."""
         if sel.dtype != torch.int64 or not sel.is_contiguous():
             sel = sel.long().contiguous()
+        first = self.first if first is None else int(first)
         cur = torch.cuda.current_stream()
         if self.agent is not None:
             q = ctypes.c_int64()
@@ -104,6 +115,8 @@ class ExpertSlots:
                                                 ctypes.byref(q), ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_step_agent")
             self.seq[li] = q.value
             return None
+        if self.last_copied is not None:       # the previous step's copies read the job buffer this step rewrites
+            cur.wait_event(self.last_copied)
         L.check(L.lib().bmx_slot_step(ctypes.byref(self.struct), li, ctypes.c_void_p(sel.data_ptr()), sel.numel(),
                                       int(first), int(admit), ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_step")
         stepped = torch.cuda.Event()
@@ -117,15 +130,17 @@ class ExpertSlots:
             ev.record(self.side)
             evs.append(ev)
         self.copied[li] = tuple(evs)
+        self.last_copied = evs[1]
         return evs[1]
 
-    def prefetch(self, li, guess, first=0, limit=None):
+    def prefetch(self, li, guess, limit=None, *, first=None):
         """Layer-ahead prefetch into layer li's slots: the first `limit` (default maxj) distinct guesses (int64 device
         tensor, best first) that are not resident are admitted on the current stream without advancing the step counter
         (the slots the last step pinned stay pinned) and copied on the side stream, ahead of layer li's step. A hint
         only: layer li's next step hands the prefetched experts it uses to the staged part, so results never change."""
         if guess.dtype != torch.int64 or not guess.is_contiguous():
             guess = guess.long().contiguous()
+        first = self.first if first is None else int(first)
         n = guess.numel()
         if n > 512:
             raise ValueError("ExpertSlots.prefetch: at most 512 guesses")
@@ -159,6 +174,7 @@ class ExpertSlots:
         """Order `stream` (default: current) after the copies of layer li's last step: part "gate_up" (the admitted
         experts' gate and up matrices), "down" or "all"."""
         if self.agent is not None:
+            self.check()
             if self.seq[li]:
                 st = stream or torch.cuda.current_stream()
                 L.check(L.lib().bmx_copy_wait_layer(self.agent, li, 0 if part == "gate_up" else 1,
@@ -171,12 +187,12 @@ class ExpertSlots:
     def desc(self, li, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0):
         return self.layers[li].desc(topk, first, act, gated, act_limit, fresh=self.fresh)
 
-    def warm(self, li, experts, first=0):
+    def warm(self, li, experts):
         """Admit the given local experts of layer li (steps over maxj of them at a time) and wait for their copies."""
         experts = list(experts)
         for i in range(0, len(experts), max(1, self.maxj)):
-            sel = torch.as_tensor(experts[i:i + self.maxj], dtype=torch.int64, device=self.arena.device) + first
-            self.step(li, sel, first)
+            sel = torch.as_tensor(experts[i:i + self.maxj], dtype=torch.int64, device=self.arena.device) + self.first
+            self.step(li, sel, True)
             self.wait_copies(li)
 
     def stage_async(self, src, dst, nbytes, stream=None):

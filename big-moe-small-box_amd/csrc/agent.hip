@@ -46,11 +46,13 @@ struct bmx_copy_agent {
     bool hsa_up = false;
     bmx::AgentShared* sh = nullptr;      // fine-grained host memory (host address)
     bmx::AgentShared* sh_dev = nullptr;  // the same memory's device address
-    int32_t* need = nullptr;             // device [L]: the record each layer's products wait for
+    int64_t* need = nullptr;             // device [L]: the record each layer's products wait for
     int64_t next_seq = 0;                // last sequence number handed out (caller's thread)
     int64_t wait_ticks = 0;              // wait limit in wall-clock ticks
+    int64_t ticks_per_us = 0;
     std::thread th;
     std::atomic<bool> stop{false};
+    std::atomic<bool> hold{false};       // the thread reads no new record while set (bmx_copy_agent_control)
     std::atomic<int> error{0};
     std::atomic<int64_t> records{0}, copies{0};
     std::atomic<int64_t> copied_bytes{0};
@@ -59,17 +61,17 @@ struct bmx_copy_agent {
 namespace bmx {
 
 // waits until flag `part` reaches seq (or, with need, need[0]: what the layer's last step left there); bounded
-__global__ __launch_bounds__(64) void k_copy_wait(AgentShared* sh, int part, int32_t seq, const int32_t* need,
+__global__ __launch_bounds__(64) void k_copy_wait(AgentShared* sh, int part, int64_t seq, const int64_t* need,
                                                   int64_t limit)
 {
     if (threadIdx.x != 0) return;
     if (need) seq = need[0];
-    if (seq <= 0) return;
+    if (seq <= 0) return;      // sequence numbers start at 1 and never wrap (64-bit): nothing published yet
     const int64_t t0 = wall_clock64();
     for (;;)
     {
-        const int32_t v = __hip_atomic_load(&sh->flags[part], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-        if ((int32_t)(v - seq) >= 0) return;
+        const int64_t v = __hip_atomic_load(&sh->flags[part], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (v >= seq) return;
         if (__hip_atomic_load(&sh->flags[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
             __hip_atomic_load(&sh->flags[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM))
             return;
@@ -104,7 +106,7 @@ static void agent_loop(bmx_copy_agent* a)
     struct Pending {
         int sig;        // index into sigs, -1: nothing to wait for
         int part;
-        int32_t seq;
+        int64_t seq;
     };
     std::deque<Pending> pending;
     int sig_next = 0, last = -1;          // last: signal of the most recent part issued
@@ -142,11 +144,12 @@ static void agent_loop(bmx_copy_agent* a)
             idle = false;
         }
         // the next record, if published and if two parts fit
-        SlotPub* r = &a->sh->ring[next % AG_RING];
-        if ((int)pending.size() + 2 <= AG_PENDING && __atomic_load_n(&r->seq, __ATOMIC_ACQUIRE) == (int32_t)next)
+        SlotPub* r = &a->sh->ring[ring_index(next)];
+        if ((int)pending.size() + 2 <= AG_PENDING && !a->hold.load(std::memory_order_acquire) &&
+            __atomic_load_n(&r->seq, __ATOMIC_ACQUIRE) == next)
         {
             const int n = r->n, li = r->li;
-            const int32_t seq = (int32_t)next;
+            const int64_t seq = next;
             const bool ok = n >= 0 && n <= a->t.maxj && li >= 0 && li < a->t.L;
             if (!ok) agent_fail(a, BMX_ERR_ARG);
             int nj = 0;
@@ -163,7 +166,7 @@ static void agent_loop(bmx_copy_agent* a)
                 s_[nj++] = s;
             }
             // the ring slot may be written again (by record next + AG_RING) from here on
-            __atomic_store_n(&a->sh->consumed, (int32_t)next, __ATOMIC_RELEASE);
+            __atomic_store_n(&a->sh->consumed, next, __ATOMIC_RELEASE);
             if (nj > 0 && r->kind == 1)
             {
                 // a prefetch: nothing waits for its gate / up alone, so one copy per admission (fewer DMA commands)
@@ -303,6 +306,7 @@ int bmx_copy_agent_create(const bmx_slot_table* t, const uint64_t* home, const i
         hipDeviceGetAttribute(&bus, hipDeviceAttributePciBusId, a->device) != hipSuccess ||
         hipDeviceGetAttribute(&dev, hipDeviceAttributePciDeviceId, a->device) != hipSuccess)
         return fail(BMX_ERR_HIP, "device query");
+    a->ticks_per_us = (int64_t)rate_khz / 1000 > 0 ? (int64_t)rate_khz / 1000 : 1;
     a->wait_ticks = (int64_t)rate_khz * 1000 * 5;      // 5 s
     if (hsa_init() != HSA_STATUS_SUCCESS) return fail(BMX_ERR_HIP, "hsa_init");
     a->hsa_up = true;
@@ -322,8 +326,8 @@ int bmx_copy_agent_create(const bmx_slot_table* t, const uint64_t* home, const i
     void* pd = nullptr;
     if (hipHostGetDevicePointer(&pd, p, 0) != hipSuccess) return fail(BMX_ERR_HIP, "host ring device address");
     a->sh_dev = static_cast<AgentShared*>(pd);
-    if (hipMalloc(&a->need, (size_t)t->L * sizeof(int32_t)) != hipSuccess ||
-        hipMemset(a->need, 0, (size_t)t->L * sizeof(int32_t)) != hipSuccess)
+    if (hipMalloc(&a->need, (size_t)t->L * sizeof(int64_t)) != hipSuccess ||
+        hipMemset(a->need, 0, (size_t)t->L * sizeof(int64_t)) != hipSuccess)
         return fail(BMX_ERR_HIP, "layer wait targets");
     a->th = std::thread(agent_loop, a);
     *out = a;
@@ -343,6 +347,25 @@ int bmx_copy_agent_destroy(bmx_copy_agent* a)
     return err ? set_error(err, "bmx_copy_agent_destroy: the agent had failed") : BMX_OK;
 }
 
+// the failure visible to the host, as a status (0: none)
+static int agent_failure(const bmx_copy_agent* a, const char* who)
+{
+    if (a->error.load()) return set_error(a->error.load(), "%s: copy agent failed (a copy failed or a record was malformed)", who);
+    if (__atomic_load_n(&a->sh->flags[2], __ATOMIC_ACQUIRE))
+        return set_error(BMX_ERR_HIP, "%s: copy agent aborted", who);
+    if (__atomic_load_n(&a->sh->flags[3], __ATOMIC_ACQUIRE))
+        return set_error(BMX_ERR_HIP, "%s: a copy wait ran out of time (slot contents since then are not trusted)", who);
+    return BMX_OK;
+}
+
+int bmx_copy_agent_control(bmx_copy_agent* a, int hold, int64_t wait_limit_us)
+{
+    if (!a) return set_error(BMX_ERR_ARG, "bmx_copy_agent_control: null agent");
+    if (hold >= 0) a->hold.store(hold != 0, std::memory_order_release);
+    if (wait_limit_us > 0) a->wait_ticks = wait_limit_us * a->ticks_per_us;
+    return BMX_OK;
+}
+
 int bmx_copy_agent_status(const bmx_copy_agent* a, int64_t* stats)
 {
     if (!a) return set_error(BMX_ERR_ARG, "bmx_copy_agent_status: null agent");
@@ -355,10 +378,7 @@ int bmx_copy_agent_status(const bmx_copy_agent* a, int64_t* stats)
         stats[4] = __atomic_load_n(&a->sh->flags[1], __ATOMIC_ACQUIRE);
         stats[5] = __atomic_load_n(&a->sh->flags[3], __ATOMIC_ACQUIRE);
     }
-    if (a->error.load()) return set_error(a->error.load(), "copy agent: a copy failed or a record was malformed");
-    if (__atomic_load_n(&a->sh->flags[3], __ATOMIC_ACQUIRE))
-        return set_error(BMX_ERR_HIP, "copy agent: a wait ran out of time");
-    return BMX_OK;
+    return agent_failure(a, "bmx_copy_agent_status");
 }
 
 int bmx_slot_step_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, const int64_t* sel, int n, int64_t first,
@@ -367,8 +387,10 @@ int bmx_slot_step_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, cons
     if (!a || !seq) return set_error(BMX_ERR_ARG, "bmx_slot_step_agent: null agent or seq");
     const int64_t q = a->next_seq + 1;
     if (li < 0 || li >= a->t.L) return set_error(BMX_ERR_ARG, "bmx_slot_step_agent: bad layer %d", li);
-    const int rc = launch_slot_step(t, li, sel, n, first, admit, static_cast<hipStream_t>(stream), a->sh_dev, (int32_t)q,
-                                    a->need, a->wait_ticks);
+    int rc = agent_failure(a, "bmx_slot_step_agent");
+    if (rc) return rc;
+    rc = launch_slot_step(t, li, sel, n, first, admit, static_cast<hipStream_t>(stream), a->sh_dev, q, a->need,
+                          a->wait_ticks);
     if (rc) return rc;
     a->next_seq = q;
     *seq = q;
@@ -380,8 +402,10 @@ int bmx_slot_prefetch_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, 
 {
     if (!a || !seq) return set_error(BMX_ERR_ARG, "bmx_slot_prefetch_agent: null agent or seq");
     const int64_t q = a->next_seq + 1;
-    const int rc = launch_slot_prefetch(t, li, sel, n, first, limit, 0, static_cast<hipStream_t>(stream), a->sh_dev,
-                                        (int32_t)q, a->wait_ticks);
+    int rc = agent_failure(a, "bmx_slot_prefetch_agent");
+    if (rc) return rc;
+    rc = launch_slot_prefetch(t, li, sel, n, first, limit, 0, static_cast<hipStream_t>(stream), a->sh_dev, q,
+                              a->wait_ticks);
     if (rc) return rc;
     a->next_seq = q;
     *seq = q;
@@ -393,7 +417,7 @@ int bmx_copy_wait(bmx_copy_agent* a, int64_t seq, int part, bmx_stream_t stream)
     if (!a) return set_error(BMX_ERR_ARG, "bmx_copy_wait: null agent");
     if (part < 0 || part > 1 || seq <= 0 || seq > a->next_seq)
         return set_error(BMX_ERR_ARG, "bmx_copy_wait: bad part %d or sequence number %lld", part, (long long)seq);
-    hipLaunchKernelGGL(k_copy_wait, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), a->sh_dev, part, (int32_t)seq,
+    hipLaunchKernelGGL(k_copy_wait, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), a->sh_dev, part, seq,
                        nullptr, a->wait_ticks);
     return check_launch("bmx_copy_wait");
 }
@@ -403,7 +427,7 @@ int bmx_copy_wait_layer(bmx_copy_agent* a, int li, int part, bmx_stream_t stream
     if (!a) return set_error(BMX_ERR_ARG, "bmx_copy_wait_layer: null agent");
     if (part < 0 || part > 1 || li < 0 || li >= a->t.L)
         return set_error(BMX_ERR_ARG, "bmx_copy_wait_layer: bad part %d or layer %d", part, li);
-    hipLaunchKernelGGL(k_copy_wait, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), a->sh_dev, part, 0,
+    hipLaunchKernelGGL(k_copy_wait, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), a->sh_dev, part, (int64_t)0,
                        a->need + li, a->wait_ticks);
     return check_launch("bmx_copy_wait_layer");
 }

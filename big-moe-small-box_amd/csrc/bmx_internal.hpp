@@ -62,29 +62,33 @@ int launch_zero_i32(int32_t* p, int n, hipStream_t s);
 
 // slots.hip
 // A step's or prefetch's admissions published to the copy agent (fine-grained host memory): the payload, then seq with a
-// system-scope release store.
+// system-scope release store. Sequence numbers are 64-bit and start at 1: they never wrap.
 struct SlotPub {
-    int32_t seq, li, n, kind;     // kind: 0 step, 1 prefetch
+    int64_t seq;
+    int32_t li, n, kind, pad;     // kind: 0 step, 1 prefetch
     int32_t pairs[2 * 64];        // (expert, slot) of each admission
 };
 constexpr int AG_RING = 64;       // records in the ring: record q lives in ring[q % AG_RING]
+__host__ __device__ inline int ring_index(int64_t seq) { return (int)((uint64_t)seq % AG_RING); }
 // The memory a copy agent shares with the kernels. flags[0] gate / up done, flags[1] down done (sequence numbers);
 // flags[2] abort (the waits end at once); flags[3] set by a wait that ran out of time. consumed: the last record the
-// agent has read out of the ring (its slot may be written again by record consumed + AG_RING).
+// agent has read out of the ring (its slot may be written again by record consumed + AG_RING). Once flags[2] or
+// flags[3] is set, steps admit nothing (every expert they see runs from its home) and publish nothing, and the host
+// entry points of the agent report the failure.
 struct AgentShared {
-    int32_t flags[4];
-    int32_t consumed;
-    int32_t pad[3];
+    int64_t flags[4];
+    int64_t consumed;
+    int64_t pad[3];
     SlotPub ring[AG_RING];
 };
 // Publishing (sh != null): the step writes ring[seq % AG_RING] once the agent has consumed record seq - AG_RING, waiting
-// at most wait_limit wall-clock ticks (then it sets flags[3] and publishes nothing). need (steps only): need[li] = the
-// last record layer li's next products depend on (seq when the step admitted experts, seq - 1 when it did not: its
-// prefetched hits came with earlier records)
+// at most wait_limit wall-clock ticks (then it sets flags[3]). need (steps only): need[li] = the last record layer li's
+// next products depend on (seq when the step admitted experts, seq - 1 when it did not: its prefetched hits came with
+// earlier records)
 int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
-                     AgentShared* sh = nullptr, int32_t seq = 0, int32_t* need = nullptr, int64_t wait_limit = 0);
+                     AgentShared* sh = nullptr, int64_t seq = 0, int64_t* need = nullptr, int64_t wait_limit = 0);
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
-                         hipStream_t s, AgentShared* sh = nullptr, int32_t seq = 0, int64_t wait_limit = 0);
+                         hipStream_t s, AgentShared* sh = nullptr, int64_t seq = 0, int64_t wait_limit = 0);
 int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStream_t s);
 
 // moe_prefill.hip (same ws / stage conventions; ws layout [xt][part_gu][act rows][part_dn])

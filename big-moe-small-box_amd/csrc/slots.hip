@@ -20,24 +20,28 @@ struct SlotArgs {
     int pf;       // 0: a step; 1: a prefetch into job buffer `buf` with at most `limit` candidates
     int limit, buf;
     AgentShared* sh;  // or null: the admissions are also published to the copy agent's ring under sequence number seq
-    int32_t seq;
-    int32_t* need;    // steps that publish: need[li] = the last record the layer's products depend on
+    int64_t seq;
+    int64_t* need;    // steps that publish: need[li] = the last record the layer's products depend on
     int64_t wait_limit;   // wall-clock ticks a publish waits for its ring slot
 };
 
+__device__ __forceinline__ bool agent_failed(AgentShared* sh)
+{
+    return __hip_atomic_load(&sh->flags[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
+           __hip_atomic_load(&sh->flags[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Until the agent has read record seq - AG_RING out of the ring slot seq will reuse (bounded; false: the agent aborted,
 // a wait ran out of time, or this one did, which it records in flags[3]). One lane.
-__device__ bool ring_slot_free(AgentShared* sh, int32_t seq, int64_t limit)
+__device__ bool ring_slot_free(AgentShared* sh, int64_t seq, int64_t limit)
 {
-    const int32_t want = seq - AG_RING;
+    const int64_t want = seq - AG_RING;
     const int64_t t0 = wall_clock64();
     for (;;)
     {
-        const int32_t c = __hip_atomic_load(&sh->consumed, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-        if ((int32_t)(c - want) >= 0) return true;
-        if (__hip_atomic_load(&sh->flags[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
-            __hip_atomic_load(&sh->flags[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM))
-            return false;
+        if (agent_failed(sh)) return false;
+        const int64_t c = __hip_atomic_load(&sh->consumed, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (c >= want) return true;
         if (wall_clock64() - t0 > limit)
         {
             __hip_atomic_store(&sh->flags[3], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -156,16 +160,20 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     {
         int32_t* jobs = a.pf ? prefetch_jobs(t, a.buf) + 1 : t.jobs;
         SlotPub* pub = nullptr;
+        int admit = a.admit;
         if (a.sh)
         {
+            // a failed agent (aborted, or a wait ran out of time) copies nothing more: admit nothing, so every expert
+            // this step sees runs from its home, and publish nothing
             int ok = 0;
             if (lane == 0) ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
-            if (__shfl(ok, 0)) pub = &a.sh->ring[a.seq % AG_RING];
+            if (__shfl(ok, 0)) pub = &a.sh->ring[ring_index(a.seq)];
+            else admit = 0;
         }
         int hand = t.ctl[0], nj = 0, novictim = 0, evicted = 0, wasted = 0;
         const int chunk = S < 64 ? S : 64;
         const int maxp = a.pf ? S : 2 * S;      // a prefetch passes referenced slots without clearing: one revolution
-        for (int k = 0; a.admit && S > 0 && k < nmiss && nj < t.maxj; ++k)
+        for (int k = 0; admit && S > 0 && k < nmiss && nj < t.maxj; ++k)
         {
             const int ex = miss[k];
             int found = -1, probes = 0;
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                 __hip_atomic_store(&pub->seq, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
                 if (!a.pf && a.need) a.need[a.li] = nj > 0 ? a.seq : a.seq - 1;
             }
-            if (a.admit && S > 0) t.ctl[0] = hand;
+            if (admit && S > 0) t.ctl[0] = hand;
             if (a.pf)
             {
                 prefetch_jobs(t, a.buf)[0] = nj;
@@ -320,7 +328,7 @@ static int check_table(const bmx_slot_table* t, const char* who)
 }
 
 int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
-                     AgentShared* sh, int32_t seq, int32_t* need, int64_t wait_limit)
+                     AgentShared* sh, int64_t seq, int64_t* need, int64_t wait_limit)
 {
     int rc = check_table(t, "bmx_slot_step");
     if (rc) return rc;
@@ -344,7 +352,7 @@ int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n,
 }
 
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
-                         hipStream_t s, AgentShared* sh, int32_t seq, int64_t wait_limit)
+                         hipStream_t s, AgentShared* sh, int64_t seq, int64_t wait_limit)
 {
     int rc = check_table(t, "bmx_slot_prefetch");
     if (rc) return rc;

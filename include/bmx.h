@@ -264,8 +264,15 @@ int bmx_copy_agent_create(const bmx_slot_table* t, const uint64_t* home, const i
                           bmx_copy_agent** agent);
 int bmx_copy_agent_destroy(bmx_copy_agent* agent);
 /* stats (or NULL) [6]: records, copies, bytes copied, gate / up mark, down mark, a wait ran out of time; returns an
- * error if a copy failed or a wait ran out of time. */
+ * error if a copy failed, the agent aborted or a wait ran out of time. Such a failure is final: from then on the steps
+ * admit nothing (the experts they see run from their homes), bmx_slot_step_agent / bmx_slot_prefetch_agent return the
+ * error without launching, and the slot contents of admissions whose copies had not completed are not trusted (the
+ * layer calls that read them are to be discarded). Sequence numbers are 64-bit and never wrap. */
 int bmx_copy_agent_status(const bmx_copy_agent* agent, int64_t* stats);
+/* Failure-path control (the reference's controller has no counterpart; for tests that force a failure from the host):
+ * hold >= 0 sets whether the agent's thread reads new records (1: it stops reading, so the waits run into their limit);
+ * wait_limit_us > 0 sets the limit of the device-side waits launched after the call (default 5 s). */
+int bmx_copy_agent_control(bmx_copy_agent* agent, int hold, int64_t wait_limit_us);
 int bmx_slot_step_agent(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const int64_t* sel, int n,
                         int64_t first, int admit, int64_t* seq, bmx_stream_t stream);
 int bmx_slot_prefetch_agent(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const int64_t* sel, int n,

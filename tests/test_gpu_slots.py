@@ -61,19 +61,19 @@ def test_slot_step_matches_oracle(cuda, oracle, S, maxj, disabled):
     import bmx
     Lyr, E = 3, 16
     layers = small_layers(Lyr, E, 256, 128, 10, "device")
-    slots = bmx.ExpertSlots(layers, S, maxj=maxj, disabled=disabled)
+    first = 7
+    slots = bmx.ExpertSlots(layers, S, maxj=maxj, disabled=disabled, first=first)
     ref = oracle.SlotTable(Lyr, E, S)
     for s in disabled:
         ref.pin[s] = -1
     rng = np.random.default_rng(S * 100 + maxj)
-    first = 7
     for step in range(40):
         li = int(rng.integers(0, Lyr))
         n = int(rng.integers(0, 12))
         sel = rng.integers(0, E + 3, n) + first - 1            # a few ids outside [first, first + E): dropped
         admit = bool(rng.random() < 0.85)
         say("slot step", step, "layer", li, "picks", n, "admit", admit)
-        slots.step(li, torch.from_numpy(sel.astype(np.int64)).cuda(), first, admit)
+        slots.step(li, torch.from_numpy(sel.astype(np.int64)).cuda(), admit)     # Pool.step(li, sel, admit)
         jobs, ev = ref.step(li, sel.astype(np.int64), first, admit, maxj)
         fresh_want = np.zeros(E, np.int32)
         fresh_want[jobs[:, 0]] = 1
@@ -91,19 +91,19 @@ def test_slot_prefetch_matches_oracle(cuda, oracle, S, maxj):
     import bmx
     Lyr, E = 3, 20
     layers = small_layers(Lyr, E, 256, 128, 20, "device")
-    slots = bmx.ExpertSlots(layers, S, maxj=maxj, disabled=(2,) if S else ())
+    first = 3
+    slots = bmx.ExpertSlots(layers, S, maxj=maxj, disabled=(2,) if S else (), first=first)
     ref = oracle.SlotTable(Lyr, E, S)
     if S:
         ref.pin[2] = -1
     rng = np.random.default_rng(S * 10 + maxj)
-    first = 3
     fresh_want = np.zeros(E, np.int32)
     for it in range(60):
         li = int(rng.integers(0, Lyr))
         if rng.random() < 0.5:
             sel = rng.integers(0, E + 2, int(rng.integers(0, 10))) + first - 1
             say("slot step", it, "layer", li, "picks", sel.size)
-            slots.step(li, torch.from_numpy(sel.astype(np.int64)).cuda(), first)
+            slots.step(li, torch.from_numpy(sel.astype(np.int64)).cuda())
             jobs, _ = ref.step(li, sel.astype(np.int64), first, True, maxj)
             fresh_want = ref.fresh.copy()
         else:
@@ -111,7 +111,7 @@ def test_slot_prefetch_matches_oracle(cuda, oracle, S, maxj):
             limit = int(rng.integers(0, 6))
             b = slots.pf_calls & 1
             say("slot prefetch", it, "layer", li, "guesses", g.size, "limit", limit, "buffer", b)
-            slots.prefetch(li, torch.from_numpy(g.astype(np.int64)).cuda(), first, limit)
+            slots.prefetch(li, torch.from_numpy(g.astype(np.int64)).cuda(), limit)
             jobs, _ = ref.prefetch(li, g.astype(np.int64), first, limit, maxj)
             torch.cuda.synchronize()
             pj = slots.pjobs.cpu().numpy()[b * (1 + 2 * maxj):]
@@ -289,3 +289,35 @@ def test_stage_async_copies(cuda):
     slots.stage_async(src, dst, [t.rec] * 4)
     torch.cuda.synchronize()
     assert torch.equal(slots.arena.cpu(), t.arena.clone())
+
+
+def test_agent_failure_is_reported(cuda):
+    """A copy wait that runs out of time, forced from the host (the agent's thread holds back from reading records, the
+    wait limit is 20 ms; every kernel still ends by itself): a step queued behind the failed wait admits nothing, so its
+    experts run from their homes, and the host calls after it raise instead of handing out results computed on slots
+    whose copies never ran."""
+    import bmx
+    layers = small_layers(1, 12, 256, 128, 90, "host")
+    slots = bmx.ExpertSlots(layers, 6, maxj=4, copies="dma")
+    lib = bmx.lib()
+    bmx._lib.check(lib.bmx_copy_agent_control(slots.agent, 1, 20000), "bmx_copy_agent_control")
+    # picks made before the first launch: a host-to-device copy made later would wait for the 20 ms wait
+    p01, p23, p4 = (torch.tensor(e, dtype=torch.int64, device="cuda") for e in ((0, 1), (2, 3), (4,)))
+    torch.cuda.synchronize()
+    say("agent failure: step admitting 0, 1 with the agent held")
+    slots.step(0, p01)                              # admitted and published, never copied
+    slots.wait_copies(0, part="gate_up")           # gives up on the device after 20 ms
+    slots.step(0, p23)                              # launched before the wait gave up
+    torch.cuda.synchronize()
+    say("agent failure: stats", slots.stats(), "ctl", slots.ctl.tolist())
+    assert int(slots.ctl[2].item()) == 0
+    assert int(slots.slotof[2].item()) == -1 and int(slots.slotof[3].item()) == -1
+    assert int(slots.slotof[0].item()) >= 0 and int(slots.slotof[1].item()) >= 0
+    with pytest.raises(bmx.BmxError, match="ran out of time"):
+        slots.check()
+    with pytest.raises(bmx.BmxError, match="ran out of time"):
+        slots.step(0, p4)
+    with pytest.raises(bmx.BmxError, match="ran out of time"):
+        slots.wait_copies(0)
+    bmx._lib.check(lib.bmx_copy_agent_control(slots.agent, 0, 0), "bmx_copy_agent_control")
+    slots.close()
