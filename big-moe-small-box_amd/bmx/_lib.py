@@ -75,6 +75,7 @@ SIGNATURES = {
     "bmx_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "bmx_moe_layer_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_layer": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
+    "bmx_moe_layer_scratch": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _I, _P]),
     "bmx_slot_step": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, _I64, _I, _P]),
     "bmx_slot_copy": (_I, [ctypes.POINTER(SlotTable), _I, _P]),
     "bmx_slot_copy_mats": (_I, [ctypes.POINTER(SlotTable), _I, _I, _P]),

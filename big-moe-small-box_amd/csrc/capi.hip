@@ -7,6 +7,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 namespace bmx {
 
 static thread_local char g_err[512] = "";
@@ -128,6 +130,36 @@ static int launch_experts(int path, const MoeShape& m, const void* x, const bmx_
     if (path == BMX_PATH_MID)
         return launch_mid_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
     return launch_decode_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
+}
+
+// ---- the allocation-free layer call's workspace ----
+// A file-scope device array: every GPU the library runs on holds its own copy for the life of the process. Host code
+// never passes the array's name to a kernel (on the host it is a stand-in symbol, not a device address): the address
+// of the current device's copy comes from hipGetSymbolAddress, once per device, at that device's first call.
+static __device__ __align__(256) uint8_t scratch[BMX_SCRATCH_BYTES];
+constexpr int SCRATCH_DEVICES = 64;
+static void* g_scratch[SCRATCH_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int scratch_of_current_device(void** out)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(BMX_ERR_HIP, "bmx_moe_layer_scratch: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= SCRATCH_DEVICES)
+        return set_error(BMX_ERR_UNSUPPORTED, "bmx_moe_layer_scratch: device %d (at most %d devices)", dev, SCRATCH_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev])
+    {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(BMX_ERR_HIP, "bmx_moe_layer_scratch: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                             hipGetErrorString(e));
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return BMX_OK;
 }
 
 }  // namespace bmx
@@ -355,6 +387,25 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
     }
     if (rc) return rc;
     return launch_experts(p, m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
+}
+
+int bmx_moe_layer_scratch(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16,
+                          const void* logits_fp16, int T, int64_t* sel, void* w_fp16, float* out, int path,
+                          bmx_stream_t stream)
+{
+    int rc = check_desc(desc, "bmx_moe_layer_scratch");
+    if (rc) return rc;
+    if (T < 0 || resolve_path(path, T, desc->topk) < 0)
+        return set_error(BMX_ERR_ARG, "bmx_moe_layer_scratch: bad T (%d) or path (%d)", T, path);
+    const size_t need = bmx_moe_workspace(desc, T, path);
+    if (need > (size_t)BMX_SCRATCH_BYTES)
+        return set_error(BMX_ERR_WORKSPACE, "bmx_moe_layer_scratch: this call needs %zu bytes of workspace, more than the "
+                         "%zu of the library's scratch array (call bmx_moe_layer with a workspace instead)", need,
+                         (size_t)BMX_SCRATCH_BYTES);
+    void* ws = nullptr;
+    rc = scratch_of_current_device(&ws);
+    if (rc) return rc;
+    return bmx_moe_layer(desc, router, x_fp16, logits_fp16, T, sel, w_fp16, out, ws, BMX_SCRATCH_BYTES, path, stream);
 }
 
 }  // extern "C"

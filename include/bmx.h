@@ -154,6 +154,18 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
                   int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
                   bmx_stream_t stream);
 
+/* The same layer call with no workspace argument and no allocation: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The workspace is the library's own file-scope device array of BMX_SCRATCH_BYTES per GPU (held until the process
+ * ends); calls whose bmx_moe_layer_workspace exceeds it fail with BMX_ERR_WORKSPACE (decode and mid-size batches fit,
+ * large prefill chunks do not). Every call on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be ordered by the caller. Nothing in the array needs to start at zero (each
+ * call writes every value it reads). Results are bit-identical to bmx_moe_layer's. */
+#define BMX_SCRATCH_BYTES (64u << 20)
+int bmx_moe_layer_scratch(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16,
+                          const void* logits_fp16, int T, int64_t* sel, void* w_fp16, float* out, int path,
+                          bmx_stream_t stream);
+
 /* Expert products only, on given routes (from bmx_dispatch with rows_per_group = bmx_rows_per_group(T, topk, path)):
  * y_rows fp32 [R, H] (expert output of each dispatch row), act_rows fp16 [R, I] (the rotated down input) or NULL.
  * bmx_resolve_path: the path (DECODE or PREFILL) that `path` selects for T tokens of topk picks, -1 if invalid. */

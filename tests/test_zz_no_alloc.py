@@ -1,0 +1,84 @@
+"""bmx_moe_layer_scratch, the layer call that allocates nothing (its workspace is the library's own device array),
+against bmx_moe_layer with a caller workspace, through the C ABI: routes and outputs bit-identical on two calls in a
+row, the second on a smaller batch (the array keeps the first call's contents); a call whose workspace exceeds the
+array is refused on the host."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def P(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def layer_call(layer, x, lg, path, scratch):
+    import bmx
+    lib = bmx.lib()
+    T, k, H = x.shape[0], layer.num_experts_per_tok, layer.hidden_size
+    sel = torch.full((T, k), -5, dtype=torch.int64, device=x.device)
+    w = torch.zeros((T, k), dtype=torch.float16, device=x.device)
+    out = torch.full((T, H), float("nan"), dtype=torch.float32, device=x.device)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    d, r = ctypes.byref(layer.desc), ctypes.byref(layer.router)
+    if scratch:
+        rc = lib.bmx_moe_layer_scratch(d, r, P(x), P(lg), T, P(sel), P(w), P(out), path, s)
+        bmx._lib.check(rc, "bmx_moe_layer_scratch")
+    else:
+        need = lib.bmx_moe_layer_workspace(d, T, path)
+        ws = torch.full((max(need, 1),), 0xA5, dtype=torch.uint8, device=x.device)    # no zero start assumed
+        rc = lib.bmx_moe_layer(d, r, P(x), P(lg), T, P(sel), P(w), P(out), P(ws), ws.numel(), path, s)
+        bmx._lib.check(rc, "bmx_moe_layer")
+    return sel, w, out
+
+
+def make_layer(cfg, E, cuda):
+    import bmx
+    from bmx import synth
+    c = synth.CONFIGS[cfg]
+    tab = synth.table(cfg, seed=21, device=cuda, E=E)
+    _, _, bias = synth.inputs(cfg, T=1, seed=22, device=cuda)
+    if bias is not None:
+        bias = bias[:E].contiguous()
+    layer = bmx.MoELayer(tab, c["topk"], score=c["score"], bias=bias, n_group=c["n_group"], topk_group=c["topk_group"],
+                         renorm=c["renorm"], scale=c["scale"])
+    return layer
+
+
+@pytest.mark.parametrize("cfg,E,T1,T2,path", [("c2", 288, 8, 1, 0), ("c2", 64, 16, 3, 3), ("c5", 64, 16, 2, 3),
+                                              ("c1", 64, 4, 1, 1), ("c3", 64, 24, 5, 2)])
+def test_scratch_layer_matches_workspace_layer(cuda, cfg, E, T1, T2, path):
+    from bmx import synth
+    layer = make_layer(cfg, E, cuda)
+    for call, T in enumerate((T1, T2)):
+        x, lg, _ = synth.inputs(cfg, T=T, seed=30 + call, device=cuda)
+        lg = lg[:, :E].contiguous()
+        say("scratch layer", cfg, "E", E, "call", call, "T", T, "path", path)
+        a = layer_call(layer, x, lg, path, scratch=True)
+        b = layer_call(layer, x, lg, path, scratch=False)
+        torch.cuda.synchronize()
+        for u, v, name in zip(a, b, ("sel", "w", "out")):
+            assert torch.equal(u, v), (cfg, call, name)
+        assert torch.isfinite(a[2]).all()
+
+
+def test_scratch_layer_refuses_oversized_calls(cuda):
+    import bmx
+    layer = make_layer("c2", 64, cuda)
+    lib = bmx.lib()
+    T = 8192
+    need = lib.bmx_moe_layer_workspace(ctypes.byref(layer.desc), T, bmx.PATH_PREFILL)
+    assert need > (64 << 20)
+    dummy = torch.zeros(16, dtype=torch.uint8, device=cuda)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.bmx_moe_layer_scratch(ctypes.byref(layer.desc), ctypes.byref(layer.router), P(dummy), P(dummy), T,
+                                   P(dummy), P(dummy), P(dummy), bmx.PATH_PREFILL, s)
+    assert rc == bmx._lib.BMX_ERR_WORKSPACE
+    assert "scratch array" in lib.bmx_last_error().decode()
