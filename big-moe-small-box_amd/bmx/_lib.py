@@ -8,7 +8,7 @@ LIB_PATH = os.path.join(HERE, "libbmx.so")
 BMX_OK, BMX_ERR_ARG, BMX_ERR_HIP, BMX_ERR_WORKSPACE, BMX_ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 TF_K2, TF_K25, TF_K3, TF_K4 = 0, 1, 2, 3
 TILE_BYTES = {TF_K2: 64, TF_K25: 80, TF_K3: 96, TF_K4: 128}
-SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSP = 0, 1, 2
 ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
 PATH_AUTO, PATH_DECODE, PATH_PREFILL, PATH_MID = 0, 1, 2, 3
 STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT, STAGE_PREP = 0, 1, 2, 3, 4, 5
@@ -28,7 +28,7 @@ class Expert(ctypes.Structure):
 class MoeDesc(ctypes.Structure):
     _fields_ = [("H", ctypes.c_int32), ("I", ctypes.c_int32), ("E", ctypes.c_int32), ("topk", ctypes.c_int32),
                 ("first", ctypes.c_int64), ("act", ctypes.c_int32), ("gated", ctypes.c_int32),
-                ("act_limit", ctypes.c_float), ("experts", _P), ("shared", _P), ("fresh", _P)]
+                ("act_limit", ctypes.c_float), ("experts", _P), ("shared", _P), ("fresh", _P), ("shared_gate", _P)]
 
 
 class SlotTable(ctypes.Structure):
@@ -45,7 +45,8 @@ class CpuExpert(ctypes.Structure):
 
 class RouterDesc(ctypes.Structure):
     _fields_ = [("score_fn", ctypes.c_int32), ("renorm", ctypes.c_int32), ("n_group", ctypes.c_int32),
-                ("topk_group", ctypes.c_int32), ("scale", ctypes.c_float), ("reserved", ctypes.c_int32), ("bias", _P)]
+                ("topk_group", ctypes.c_int32), ("scale", ctypes.c_float), ("reserved", ctypes.c_int32), ("bias", _P),
+                ("weight", _P)]
 
 
 class Routes(ctypes.Structure):
@@ -60,6 +61,7 @@ SIGNATURES = {
     "bmx_tile_bytes": (_I, [_I]),
     "bmx_exl3_dequant": (_I, [_P, _I, _I, _I, _P, _P]),
     "bmx_router_topk": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _I64, _P, _P, _P]),
+    "bmx_router_logits": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "bmx_groups_max": (_I, [_I, _I, _I, _I, _I]),
     "bmx_dispatch_workspace": (_SZ, [_I, _I, _I]),
     "bmx_dispatch": (_I, [_P, _I, _I, _I, _I64, _I, _I, ctypes.POINTER(Routes), _P, _SZ, _P]),

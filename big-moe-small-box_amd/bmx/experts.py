@@ -126,12 +126,18 @@ class ExpertTable:
             self._table = raw.to(self.device)
         return self._table
 
-    def desc(self, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0, fresh=None):
+    def desc(self, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0, fresh=None, shared_gate=None):
+        """bmx_moe_desc of the layer; shared_gate: fp16 [H] device tensor scaling the shared expert's output by
+        sigmoid(x . shared_gate), or None (weight 1)."""
         t = self.table()
         es = ctypes.sizeof(L.Expert)
         shared = t.data_ptr() + self.E * es if self.has_shared else None
+        if shared_gate is not None and (shared_gate.dtype != torch.float16 or shared_gate.numel() != self.H or
+                                        not shared_gate.is_cuda or not shared_gate.is_contiguous()):
+            raise ValueError("shared_gate must be a contiguous fp16 device tensor of H elements")
         return L.MoeDesc(self.H, self.I, self.E, topk, first, act, int(gated), act_limit, t.data_ptr(), shared,
-                         fresh.data_ptr() if fresh is not None else None)
+                         fresh.data_ptr() if fresh is not None else None,
+                         shared_gate.data_ptr() if shared_gate is not None else None)
 
     def host_expert(self, e):
         """numpy copies of one expert (trellis per matrix, scales, formats) for the oracle."""

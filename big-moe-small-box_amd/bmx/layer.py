@@ -19,8 +19,15 @@ from . import ops
 
 
 class MoELayer:
+    """One MoE layer's experts on the HIP library. table: the layer's ExpertTable; topk, first (routing_first); router:
+    score (SCORE_SOFTMAX / SCORE_SIGMOID / SCORE_SQRTSP), selection bias fp32 [E], group limit, renorm, scale
+    (routed_scaling_factor); activation, gated, act_limit; router_weight: fp16 [E, H] gate weight (checkpoint layout),
+    used when no logits are given; shared_gate: fp16 [H] gate vector of the shared expert (its output scaled by
+    sigmoid(x . shared_gate)) or None; slots / li: an ExpertSlots table and this layer's index in it."""
+
     def __init__(self, table, topk, first=0, score=L.SCORE_SIGMOID, bias=None, n_group=1, topk_group=1, renorm=True,
-                 scale=1.0, act=L.ACT_SILU, gated=True, act_limit=0.0, router_weight=None, slots=None, li=0):
+                 scale=1.0, act=L.ACT_SILU, gated=True, act_limit=0.0, router_weight=None, slots=None, li=0,
+                 shared_gate=None):
         self.table = table
         self.num_experts_per_tok = topk
         self.routing_first = first
@@ -29,20 +36,31 @@ class MoELayer:
         self.score, self.bias, self.n_group, self.topk_group = score, bias, n_group, topk_group
         self.renorm, self.scale = renorm, scale
         self.act, self.gated, self.act_limit = act, gated, act_limit
-        self.router_weight = router_weight        # fp16 [H, E] or None (logits passed in params["logits"])
+        if router_weight is not None and (router_weight.dtype != torch.float16 or not router_weight.is_cuda or
+                                          tuple(router_weight.shape) != (table.E, table.H) or
+                                          not router_weight.is_contiguous()):
+            raise ValueError(f"router_weight must be a contiguous fp16 device tensor [E, H] = [{table.E}, {table.H}]")
+        self.router_weight = router_weight        # fp16 [E, H] or None (logits passed in params["logits"])
+        self.shared_gate = shared_gate
         self.slots, self.li = slots, li           # optional ExpertSlots (expert-slot table) and this layer's index
-        self.desc = table.desc(topk, first, act, gated, act_limit)
-        self.slot_desc = slots.desc(li, topk, first, act, gated, act_limit) if slots is not None else None
+        self.desc = table.desc(topk, first, act, gated, act_limit, shared_gate=shared_gate)
+        self.slot_desc = (slots.desc(li, topk, first, act, gated, act_limit, shared_gate=shared_gate)
+                          if slots is not None else None)
         self.router = L.RouterDesc(score, int(renorm), n_group, topk_group, scale, 0,
-                                   bias.data_ptr() if bias is not None else None)
+                                   bias.data_ptr() if bias is not None else None,
+                                   router_weight.data_ptr() if router_weight is not None else None)
         self._ws = None
         self.out_bszn = None
 
     # ---- router ----
     def router_logits(self, z):
+        """fp16 [T, E] router logits of the MoE input z, projected on the GPU (bmx_router_logits)."""
         if self.router_weight is None:
             raise ValueError("MoELayer: no router weight; pass params['logits']")
-        return torch.matmul(z.view(-1, self.hidden_size), self.router_weight)
+        x = z.view(-1, self.hidden_size)
+        if x.dtype != torch.float16 or not x.is_contiguous():
+            x = x.half().contiguous()
+        return ops.router_logits(x, self.router_weight)
 
     def routing_fn(self, bsz, cfg, z, params):
         logits = params.get("logits") if params else None
@@ -147,12 +165,13 @@ class MoELayer:
         return fhs if fhs.is_contiguous() else fhs.contiguous()
 
     def forward(self, z, logits=None, path=L.PATH_AUTO):
-        if logits is not None and self.slots is None:
-            # the whole call in one library entry (router + dispatch fused at decode sizes)
+        if (logits is not None or self.router_weight is not None) and self.slots is None:
+            # the whole call in one library entry (router + dispatch fused at decode sizes; the router projection of z
+            # first when no logits are given)
             x = z.view(-1, self.hidden_size)
             if x.dtype != torch.float16 or not x.is_contiguous():
                 x = x.half().contiguous()
-            lg = logits.view(x.shape[0], -1).to(torch.float16).contiguous()
+            lg = logits.view(x.shape[0], -1).to(torch.float16).contiguous() if logits is not None else None
             need = L.lib().bmx_moe_layer_workspace(self.desc, x.shape[0], path)
             if self._ws is None or self._ws.numel() < need:
                 self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)

@@ -45,6 +45,19 @@ def router_topk(logits, topk, bias=None, n_group=1, topk_group=1, score=L.SCORE_
     return sel, w
 
 
+def router_logits(z, weight):
+    """Router projection on the MFMA units: z fp16 [T, H], weight fp16 [E, H] (the gate weight as checkpoints store it)
+    -> logits fp16 [T, E] = RN16(z weight^T), fp32 accumulation."""
+    _need(z, torch.float16, "z"); _need(weight, torch.float16, "router weight")
+    T, H = z.shape
+    E = weight.shape[0]
+    if weight.shape[1] != H:
+        raise ValueError(f"router weight {tuple(weight.shape)} does not match H = {H}")
+    out = torch.empty((T, E), dtype=torch.float16, device=z.device)
+    check(lib().bmx_router_logits(_ptr(z), _ptr(weight), T, H, E, _ptr(out), _stream()), "bmx_router_logits")
+    return out
+
+
 class RoutesBuf:
     """Dispatch outputs (device int32 tensors) and the ctypes struct pointing at them."""
 
@@ -142,8 +155,11 @@ def combine(y_rows, routes, w, H):
 
 
 def moe_layer(desc, router, x, logits, path=L.PATH_AUTO, workspace=None):
-    """Router + dispatch + experts + combine from logits fp16 [T, E] -> (out fp32 [T, H], sel, w)."""
-    _need(x, torch.float16, "x"); _need(logits, torch.float16, "logits")
+    """Router + dispatch + experts + combine from logits fp16 [T, E] (None: projected from x with the router descriptor's
+    weight) -> (out fp32 [T, H], sel, w)."""
+    _need(x, torch.float16, "x")
+    if logits is not None:
+        _need(logits, torch.float16, "logits")
     T = x.shape[0]
     sel = torch.empty((T, desc.topk), dtype=torch.int64, device=x.device)
     w = torch.empty((T, desc.topk), dtype=torch.float16, device=x.device)

@@ -184,8 +184,8 @@ class ExpertSlots:
             ev = self.copied[li][0 if part == "gate_up" else 1]
             (stream or torch.cuda.current_stream()).wait_event(ev)
 
-    def desc(self, li, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0):
-        return self.layers[li].desc(topk, first, act, gated, act_limit, fresh=self.fresh)
+    def desc(self, li, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0, shared_gate=None):
+        return self.layers[li].desc(topk, first, act, gated, act_limit, fresh=self.fresh, shared_gate=shared_gate)
 
     def warm(self, li, experts):
         """Admit the given local experts of layer li (steps over maxj of them at a time) and wait for their copies."""

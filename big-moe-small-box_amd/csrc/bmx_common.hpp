@@ -263,6 +263,10 @@ __device__ __forceinline__ u32x4 pack8_r(const float (&v)[8])
 }
 
 // ---- fixed-sequence fp32 exp (the router's; the oracle evaluates the same sequence) ----------------------------------
+// Cody-Waite argument reduction (W. J. Cody and W. Waite, Software Manual for the Elementary Functions, 1980):
+// n = rint(x / ln 2), r = x - n ln 2 with ln 2 split into a high part of 17 significant bits and a low part (the split
+// SLEEF's expf uses: 0.693145751953125 + 1.428606765330187e-06); exp(r) by the Taylor polynomial of degree 7 in Horner
+// form (|r| <= ln 2 / 2); 2^n applied as two exact power-of-two factors, so a subnormal result rounds once.
 __device__ __forceinline__ float exp_fixed(float x)
 {
     if (x != x) return x;
@@ -290,6 +294,50 @@ __device__ __forceinline__ float sigmoid_fixed(float x)
 {
     const float e = exp_fixed(-x);
     return __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
+}
+
+// Correctly rounded fp32 square root. The hardware square root (v_sqrt_f32) is within 1 ulp but not correctly rounded;
+// the estimate is moved by one ulp while the Tuckerman test fails (Markstein, IA-64 and Elementary Functions, 2000):
+// y = RN(sqrt(a)) iff (y - u_lo / 2)^2 < a < (y + u / 2)^2, u / u_lo the spacing above / below y. The midpoints have
+// 25 significant bits, so they and their squares (50 bits) are exact in double; no a has its root exactly on a midpoint.
+__device__ __forceinline__ float sqrt_rn(float a)
+{
+    float y = __builtin_sqrtf(a);
+    if (!(a > 0.0f) || !(a < __builtin_huge_valf())) return y;       // 0, negative, inf, NaN: the hardware's result
+    const double d = (double)a;
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+    {
+        const uint32_t yb = __builtin_bit_cast(uint32_t, y);          // y > 0 and finite: neighbours by the bits
+        const float up = __builtin_bit_cast(float, yb + 1u), dn = __builtin_bit_cast(float, yb - 1u);
+        const double mh = 0.5 * ((double)y + (double)up), ml = 0.5 * ((double)y + (double)dn);
+        if (mh * mh < d) y = up;
+        else if (ml * ml > d) y = dn;
+    }
+    return y;
+}
+
+// sqrt(softplus(x)) = sqrt(max(x, 0) + log1p(exp(-|x|))), the DeepSeek-V4 router's score ("sqrtsoftplus"). log1p(e)
+// for e = exp(-|x|) in [0, 1] by the series log(1 + e) = 2 atanh(s) = 2 (s + s^3 / 3 + s^5 / 5 + ...), s = e / (2 + e)
+// <= 1/3 (Abramowitz and Stegun 4.1.27), nine terms (relative error below 1e-9 before rounding): no cancellation for
+// small e. Correctly rounded division and square root; the oracle evaluates the same sequence.
+__device__ __forceinline__ float sqrtsp_fixed(float x)
+{
+    if (x != x) return x;
+    const float e = exp_fixed(-fabsf(x));
+    const float s = __fdiv_rn(e, __fadd_rn(2.0f, e));
+    const float s2 = __fmul_rn(s, s);
+    float p = 1.0f / 17.0f;
+    p = __builtin_fmaf(p, s2, 1.0f / 15.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 13.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 11.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 9.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 7.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 5.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 3.0f);
+    p = __builtin_fmaf(p, s2, 1.0f);
+    const float l = __fmul_rn(__fmul_rn(2.0f, s), p);
+    return sqrt_rn(__fadd_rn(fmaxf(x, 0.0f), l));
 }
 
 // tanh t = 1 - 2 / (exp(2 t) + 1) on the fixed-sequence exp

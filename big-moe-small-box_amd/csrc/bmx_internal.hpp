@@ -20,6 +20,7 @@ int launch_dequant(const void* trellis, int fmt, int k, int n, void* out, hipStr
 int launch_router(const void* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,
                   int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w, hipStream_t s);
 
+int launch_router_logits(const void* z, const void* W, int T, int H, int E, void* logits, hipStream_t s);
 bool route_dispatch_small_fits(int T, int E, int topk);
 int launch_route_dispatch_small(const void* logits, const float* bias, int T, int E, int topk, int n_group,
                                 int topk_group, int score_fn, int renorm, float scale, int64_t first, int64_t* sel,
@@ -44,6 +45,7 @@ struct MoeShape {
     const bmx_expert* experts;
     const bmx_expert* shared_ex;
     const int32_t* fresh;
+    const uint16_t* shared_gate;   // fp16 [H] or null
 };
 struct DecodePlan {
     int KS_gu, KS_dn, NB, NBH, G_max, R_max;

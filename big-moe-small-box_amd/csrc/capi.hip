@@ -38,6 +38,8 @@ static int check_desc(const bmx_moe_desc* d, const char* who)
         return set_error(BMX_ERR_ARG, "%s: unsupported E=%d topk=%d", who, d->E, d->topk);
     if (!d->experts) return set_error(BMX_ERR_ARG, "%s: null expert table", who);
     if (d->act < BMX_ACT_SILU || d->act > BMX_ACT_SILU_OAI) return set_error(BMX_ERR_ARG, "%s: unknown activation %d", who, d->act);
+    if (reinterpret_cast<uintptr_t>(d->shared_gate) % 16)
+        return set_error(BMX_ERR_ARG, "%s: the shared expert's gate vector must be 16-byte aligned", who);
     return BMX_OK;
 }
 
@@ -47,6 +49,7 @@ static MoeShape shape_of(const bmx_moe_desc* d, int T)
     m.H = d->H; m.I = d->I; m.E = d->E; m.topk = d->topk; m.T = T; m.shared = d->shared ? 1 : 0;
     m.act = d->act; m.gated = d->gated; m.limit = d->act_limit; m.first = d->first;
     m.experts = d->experts; m.shared_ex = d->shared; m.fresh = d->fresh;
+    m.shared_gate = static_cast<const uint16_t*>(d->shared_gate);
     return m;
 }
 
@@ -188,6 +191,12 @@ int bmx_router_topk(const void* logits_fp16, const float* bias, int T, int E, in
 {
     return launch_router(logits_fp16, bias, T, E, topk, n_group, topk_group, score_fn, renorm, scale, first, sel,
                          w_fp16, static_cast<hipStream_t>(stream));
+}
+
+int bmx_router_logits(const void* z_fp16, const void* weight_fp16, int T, int H, int E, void* logits_fp16,
+                      bmx_stream_t stream)
+{
+    return launch_router_logits(z_fp16, weight_fp16, T, H, E, logits_fp16, static_cast<hipStream_t>(stream));
 }
 
 int bmx_groups_max(int T, int topk, int E, int shared, int rows_per_group)
@@ -348,7 +357,13 @@ int bmx_moe_forward(const bmx_moe_desc* desc, const void* x_fp16, int T, const i
     return launch_experts(p, m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
 }
 
-size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path) { return bmx_moe_workspace(desc, T, path); }
+// the layer call's workspace: bmx_moe_forward's, then the projected logits [T][E] fp16 (used when no logits are given)
+size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path)
+{
+    const size_t base = bmx_moe_workspace(desc, T, path);
+    if (!base) return 0;
+    return base + align_up((size_t)T * desc->E * 2, 256);
+}
 
 int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
                   int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
@@ -361,11 +376,19 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
     if (p < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: unknown path %d", path);
     if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: T < 0");
     if (T == 0) return BMX_OK;
-    if (!x_fp16 || !logits_fp16 || !sel || !w_fp16 || !out || !workspace)
-        return set_error(BMX_ERR_ARG, "bmx_moe_layer: null pointer");
-    const size_t need = bmx_moe_workspace(desc, T, path);
+    if (!x_fp16 || !sel || !w_fp16 || !out || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_layer: null pointer");
+    if (!logits_fp16 && !router->weight)
+        return set_error(BMX_ERR_ARG, "bmx_moe_layer: no logits and no router weight to project them with");
+    const size_t need = bmx_moe_layer_workspace(desc, T, path);
     if (workspace_bytes < need) return set_error(BMX_ERR_WORKSPACE, "bmx_moe_layer: workspace %zu < %zu", workspace_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!logits_fp16)
+    {
+        void* lg = static_cast<char*>(workspace) + bmx_moe_workspace(desc, T, path);
+        rc = launch_router_logits(x_fp16, router->weight, T, desc->H, desc->E, lg, s);
+        if (rc) return rc;
+        logits_fp16 = lg;
+    }
     const MoeShape m = shape_of(desc, T);
     const int rpg = path_rows_per_group(p, T);
     const RoutesLayout L = routes_layout(T, desc->topk, desc->E, m.shared, rpg);
@@ -397,7 +420,7 @@ int bmx_moe_layer_scratch(const bmx_moe_desc* desc, const bmx_router_desc* route
     if (rc) return rc;
     if (T < 0 || resolve_path(path, T, desc->topk) < 0)
         return set_error(BMX_ERR_ARG, "bmx_moe_layer_scratch: bad T (%d) or path (%d)", T, path);
-    const size_t need = bmx_moe_workspace(desc, T, path);
+    const size_t need = bmx_moe_layer_workspace(desc, T, path);
     if (need > (size_t)BMX_SCRATCH_BYTES)
         return set_error(BMX_ERR_WORKSPACE, "bmx_moe_layer_scratch: this call needs %zu bytes of workspace, more than the "
                          "%zu of the library's scratch array (call bmx_moe_layer with a workspace instead)", need,

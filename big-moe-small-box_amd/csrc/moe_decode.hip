@@ -430,8 +430,19 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
         const int r = a.offsets[a.E] + t;
         down_out8(a, r, cb, y);
         if (a.y_rows) store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
+        if (a.sh_gate)
+        {
+            const float g = shared_gate16(a.x + (size_t)t * a.H, a.sh_gate, a.H);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = o[i] + y[i];
+            for (int i = 0; i < 8; ++i)
+            {
+                const float p = g * y[i];
+                o[i] = o[i] + p;
+            }
+        }
+        else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = o[i] + y[i];
     }
     store8f(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
 }
@@ -468,6 +479,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
     }
     lds_barrier();
     if (k0) return;
+    const float g = (a.has_shared && a.sh_gate) ? shared_gate16(a.x + (size_t)t * a.H, a.sh_gate, a.H) : 1.0f;
     float o[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = 0.0f;
@@ -482,7 +494,14 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
             o[i] = o[i] + p;
         }
     }
-    if (a.has_shared)
+    if (a.has_shared && a.sh_gate)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            const float p = g * ys[a.topk][8 * j + i];
+            o[i] = o[i] + p;
+        }
+    else if (a.has_shared)
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = o[i] + ys[a.topk][8 * j + i];
     store8f(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
@@ -676,6 +695,7 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
     a.xt = nullptr;
     a.fresh = m.fresh;
+    a.sh_gate = m.shared_gate;
     a.filter = 0;
     // One-row groups (one token) with the activation and the down product in the same call and no act rows asked
     // for: the down GEMV computes the activation of its k-range itself, once per output block instead of once, for

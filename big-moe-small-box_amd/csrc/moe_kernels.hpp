@@ -34,7 +34,31 @@ struct GvArgs {
     int act_in_down;           // the down GEMV computes its input rows from the gate / up partials (one-row groups)
     int gu_half;               // part_gu holds one split as fp16 [row][128-column block][matrix][128], each value the
                                // epilogue's own rounding of that split's sum (RN of 0.0f + product): same bits downstream
+    const uint16_t* sh_gate;   // fp16 [H] or null: the shared expert's output is scaled by sigmoid(x[t] . sh_gate)
 };
+
+// The shared expert's gate of token t, sigmoid(x[t] . sh_gate), by the calling 16-lane group (every lane of the group
+// gets it): lane j sums x[h] sh_gate[h] over h = 128 b + 8 j + i, b ascending then i = 0 .. 7, one fp32 fma each (fp16
+// inputs are exact in fp32); the 16 lane sums are added by a butterfly over lane ^ 8, ^ 4, ^ 2, ^ 1 (each pair's sum is
+// the same on both lanes); then the fixed-sequence sigmoid. The oracle evaluates the same sequence.
+__device__ __forceinline__ float shared_gate16(const uint16_t* x, const uint16_t* g, int H)
+{
+    const int j = threadIdx.x & 15;
+    float acc = 0.0f;
+    for (int b = 0; b < H / 128; ++b)
+    {
+        float xv[8], gv[8];
+        unpack8(ldg4(x + 128 * b + 8 * j), xv);
+        unpack8(ldg4(g + 128 * b + 8 * j), gv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = __builtin_fmaf(xv[i], gv[i], acc);
+    }
+    acc = acc + dpp_f<0x128>(acc);     // lane ^ 8 (row_ror:8)
+    acc = acc + dpp_xor4(acc);
+    acc = acc + dpp_f<0x4E>(acc);      // lane ^ 2
+    acc = acc + dpp_f<0xB1>(acc);      // lane ^ 1
+    return sigmoid_fixed(acc);
+}
 
 // group filter of the split gate / up stages (the shared expert, index E, is never fresh)
 __device__ __forceinline__ bool group_skipped(const GvArgs& a, int e)

@@ -633,6 +633,7 @@ int launch_mid_experts(const MoeShape& m, const void* x, const bmx_routes* r, fl
     a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
     a.fresh = m.fresh;
+    a.sh_gate = m.shared_gate;
     a.filter = 0;
     a.act_in_down = 0;
     a.gu_half = 0;
@@ -694,6 +695,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
     a.fresh = m.fresh;
+    a.sh_gate = m.shared_gate;
     a.filter = 0;
     a.act_in_down = 0;
     a.gu_half = 1;

@@ -316,7 +316,7 @@ __device__ int route_token_wave(const RouterArgs& a, int t, TopkLds& L)
         if (a.score_fn == BMX_SCORE_SOFTMAX) sc[j] = e < E ? exp_fixed(__fsub_rn(ch[j], mx)) : 0.0f;
         else
         {
-            sc[j] = e < E ? sigmoid_fixed(ch[j]) : 0.0f;
+            sc[j] = e < E ? (a.score_fn == BMX_SCORE_SQRTSP ? sqrtsp_fixed(ch[j]) : sigmoid_fixed(ch[j])) : 0.0f;
             if (e < E) ch[j] = canon(a.bias ? __fadd_rn(sc[j], bias[j]) : sc[j]);
         }
     }
@@ -452,7 +452,7 @@ __device__ int route_token_wave(const RouterArgs& a, int t, TopkLds& L)
     else if (a.renorm) den = vsum;
     if (lane < a.topk)
     {
-        const float qv = (a.score_fn == BMX_SCORE_SIGMOID && !a.renorm) ? myscore : __fdiv_rn(myscore, den);
+        const float qv = (a.score_fn != BMX_SCORE_SOFTMAX && !a.renorm) ? myscore : __fdiv_rn(myscore, den);
         a.sel[(size_t)t * a.topk + lane] = (int64_t)mypick + a.first;
         a.w[(size_t)t * a.topk + lane] = f2h_r(__fmul_rn(qv, a.scale));
     }
@@ -715,7 +715,7 @@ static int check_router(int T, int E, int topk, int n_group, int topk_group, int
         return set_error(BMX_ERR_ARG, "bmx_router_topk: bad groups n_group=%d topk_group=%d (E=%d)", n_group, topk_group, E);
     if (n_group > 1 && topk > topk_group * (E / n_group))
         return set_error(BMX_ERR_ARG, "bmx_router_topk: topk %d exceeds the experts of %d groups", topk, topk_group);
-    if (score_fn != BMX_SCORE_SOFTMAX && score_fn != BMX_SCORE_SIGMOID)
+    if (score_fn != BMX_SCORE_SOFTMAX && score_fn != BMX_SCORE_SIGMOID && score_fn != BMX_SCORE_SQRTSP)
         return set_error(BMX_ERR_ARG, "bmx_router_topk: unknown score function %d", score_fn);
     if (T > 0 && (!logits || !sel || !w)) return set_error(BMX_ERR_ARG, "bmx_router_topk: null pointer");
     return BMX_OK;
@@ -782,6 +782,87 @@ int launch_route_dispatch_small(const void* logits, const float* bias, int T, in
         default: hipLaunchKernelGGL(k_route_dispatch_small<16>, grid, block, 0, s, a, d); break;
     }
     return check_launch("route + dispatch");
+}
+
+// ---- router projection: logits = z W^T on the MFMA units ----------------------------------------------------------------
+// logits[t][e] = RN16(sum_h z[t][h] W[e][h]): z fp16 [T][H] (the MoE input rows), W fp16 [E][H] (the router's gate weight
+// as checkpoints store it), fp32 accumulation. Both operands are k-contiguous, so each lane's MFMA fragment (8
+// consecutive k of one row of z or one row of W) is one 16-byte load. Workgroup = 32 tokens x 32 experts; its 4 waves
+// take the four quarters of H (two accumulators each, alternate k-steps), and the quarter sums are added in wave order.
+constexpr int RL_WAVES = 4;
+__global__ __launch_bounds__(RL_WAVES * 64) void k_router_logits(const uint16_t* __restrict__ z,
+                                                                 const uint16_t* __restrict__ W, int T, int H, int E,
+                                                                 uint16_t* __restrict__ out)
+{
+    __shared__ f32x4 red[RL_WAVES - 1][4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int neb = (E + 31) / 32;
+    const int tb = blockIdx.x / neb, eb = blockIdx.x % neb;
+    const int t = tb * 32 + (lane & 31), e = eb * 32 + (lane & 31);
+    const int kq = H / RL_WAVES;
+    const int k0 = wave * kq + 8 * (lane >> 5);
+    const bool tv = t < T, ev = e < E;
+    const uint16_t* zp = z + (size_t)(tv ? t : 0) * H + k0;
+    const uint16_t* wp = W + (size_t)(ev ? e : 0) * H + k0;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    f32x16 acc0 = {}, acc1 = {};
+    int k = 0;
+    for (; k + 32 <= kq; k += 32)
+    {
+        const u32x4 a0 = tv ? ldg4(zp + k) : zero, b0 = ev ? ldg4(wp + k) : zero;
+        const u32x4 a1 = tv ? ldg4(zp + k + 16) : zero, b1 = ev ? ldg4(wp + k + 16) : zero;
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a0), __builtin_bit_cast(f16x8, b0), acc0,
+                                                      0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a1), __builtin_bit_cast(f16x8, b1), acc1,
+                                                      0, 0, 0);
+    }
+    if (k < kq)
+    {
+        const u32x4 a0 = tv ? ldg4(zp + k) : zero, b0 = ev ? ldg4(wp + k) : zero;
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a0), __builtin_bit_cast(f16x8, b0), acc0,
+                                                      0, 0, 0);
+    }
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = acc0[v] + acc1[v];
+    if (wave > 0)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) red[wave - 1][q][lane] = f32x4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+    lds_barrier();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < RL_WAVES - 1; ++w)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const f32x4 r = red[w][q][lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[4 * q + i] = acc[4 * q + i] + r[i];
+        }
+    // accumulator element v of lane L: row 8 (v / 4) + 4 (L / 32) + v % 4 (token), column L % 32 (expert)
+    if (!ev) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+    {
+        const int tt = tb * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (tt < T) out[(size_t)tt * E + e] = f2h_r(acc[v]);
+    }
+}
+
+int launch_router_logits(const void* z, const void* W, int T, int H, int E, void* logits, hipStream_t s)
+{
+    if (T < 0 || E <= 0 || H <= 0 || H % 64)
+        return set_error(BMX_ERR_ARG, "bmx_router_logits: T (%d) >= 0, E (%d) > 0 and H (%d) a multiple of 64 required",
+                         T, E, H);
+    if (T == 0) return BMX_OK;
+    if (!z || !W || !logits) return set_error(BMX_ERR_ARG, "bmx_router_logits: null pointer");
+    if ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(W)) % 16)
+        return set_error(BMX_ERR_ARG, "bmx_router_logits: z and the weight must be 16-byte aligned");
+    const long nblk = (long)((T + 31) / 32) * ((E + 31) / 32);
+    if (nblk > 0x7fffffffL) return set_error(BMX_ERR_ARG, "bmx_router_logits: too many tiles");
+    hipLaunchKernelGGL(k_router_logits, dim3((unsigned)nblk), dim3(RL_WAVES * 64), 0, s, static_cast<const uint16_t*>(z),
+                       static_cast<const uint16_t*>(W), T, H, E, static_cast<uint16_t*>(logits));
+    return check_launch("bmx_router_logits");
 }
 
 }  // namespace bmx

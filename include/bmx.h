@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define BMX_ABI_VERSION 2
+#define BMX_ABI_VERSION 3
 
 typedef void* bmx_stream_t; /* hipStream_t */
 
@@ -37,8 +37,9 @@ enum bmx_status {
  * K 4. A tile is 16 x 16 weights in 32 K bytes; a matrix [k][n] is stored as tiles [k/16][n/16][32 K]. */
 enum bmx_trellis_fmt { BMX_TF_K2 = 0, BMX_TF_K25 = 1, BMX_TF_K3 = 2, BMX_TF_K4 = 3 };
 
-/* router score functions */
-enum bmx_score { BMX_SCORE_SOFTMAX = 0, BMX_SCORE_SIGMOID = 1 };
+/* router score functions: softmax, sigmoid, sqrt(softplus) (exllamav3's ROUTING_ACT_SIGMOID / ROUTING_ACT_SQRTSP as the
+ * reference selects them per layer, engine/nv2.py:146-148) */
+enum bmx_score { BMX_SCORE_SOFTMAX = 0, BMX_SCORE_SIGMOID = 1, BMX_SCORE_SQRTSP = 2 };
 
 /* expert activations, exllamav3's MOE_COOP_ACT_* numbering (engine/kernels/x16/x16_dev.cu:21-24) */
 enum bmx_act { BMX_ACT_SILU = 0, BMX_ACT_GELU = 1, BMX_ACT_RELU2 = 2, BMX_ACT_SILU_OAI = 3 };
@@ -73,6 +74,9 @@ typedef struct bmx_moe_desc {
     const bmx_expert* shared;    /* device [1] or NULL: shared expert, weight 1, added after the routed slots */
     const int32_t* fresh;        /* device [E] or NULL: 1 = expert admitted to a slot by the last slot-table step (its
                                     copy may still be in flight); read by BMX_STAGE_GATE_UP_RESIDENT / _STAGED */
+    const void* shared_gate;     /* device fp16 [H] or NULL: the shared expert's output is scaled by
+                                    sigmoid(x[t] . shared_gate) before it is added (x16_red_k's sh_gate_w,
+                                    engine/kernels/x16/x16_dev.cu:315-334, 375); NULL: weight 1 */
 } bmx_moe_desc;
 
 /* Dispatch output: rows grouped per expert, stable by (expert, token, slot). R = T * topk (+ T with a shared expert,
@@ -111,6 +115,13 @@ int bmx_router_topk(const void* logits_fp16, const float* bias, int T, int E, in
                     int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w_fp16,
                     bmx_stream_t stream);
 
+/* Router projection: logits fp16 [T, E] = RN16(z W^T), z fp16 [T, H] (the MoE input rows), weight fp16 [E, H] (the
+ * router's gate weight as checkpoints store it), fp32 accumulation on the MFMA units. The projection of exllamav3's
+ * routing kernel (routing_ds3_nogroup(z, gate_tensor, logits_out, ...), engine/nv2.py:484-485, whose logits_out is fp16).
+ * H a multiple of 64; z and weight 16-byte aligned. */
+int bmx_router_logits(const void* z_fp16, const void* weight_fp16, int T, int H, int E, void* logits_fp16,
+                      bmx_stream_t stream);
+
 /* ---- dispatch ----
  * Token-to-expert counting sort (the histogram + ascending compaction of nv_pub_k, engine/kernels/nv2/
  * nv2_dev.cu:23-95, as contiguous per-expert row segments). */
@@ -144,11 +155,14 @@ typedef struct bmx_router_desc {
     float scale;
     int32_t reserved;
     const float* bias;      /* device fp32 [E] or NULL */
+    const void* weight;     /* device fp16 [E, H] or NULL: the router's gate weight, projected from x when the layer call
+                               is given no logits (bmx_router_logits) */
 } bmx_router_desc;
 
 /* The whole layer call from router logits: router + dispatch (one kernel at decode sizes), expert products, combine.
  * The reference's per-layer sequence routing_fn -> Nv2.layer -> run_bszN -> cpu_split_combine (engine/tiers.py:707-739)
- * with the expert arithmetic of exllamav3. sel int64 [T, topk] and w fp16 [T, topk] receive the routing. */
+ * with the expert arithmetic of exllamav3. sel int64 [T, topk] and w fp16 [T, topk] receive the routing. logits_fp16
+ * NULL: the logits are projected from x with router->weight first (bmx_router_logits, into the workspace). */
 size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path);
 int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
                   int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,

@@ -326,9 +326,33 @@ void bmxo_expert_forward(const bmxo_expert* e, int H, int I, int act, int gated,
 /* Layer: each routed expert decoded once, run on every selected token that picks it; then per token the weighted sum
  * over slots k = 0 .. topk-1 in order (picks with weight 0 or outside [first, first + E) skipped), then + the shared
  * expert (engine/kernels/x16/x16_dev.cu:354-384; engine/kernels/nv2/ft_n135.h:869-896 sums in job order instead). */
-void bmxo_moe_forward(const bmxo_expert* experts, int E, int64_t first, const bmxo_expert* shared, int H, int I,
-                      int act, int gated, float limit, const uint16_t* x, int T, int topk, const int64_t* sel,
-                      const uint16_t* w, const int* rows, int nrows, float* out)
+/* The shared expert's gate sigmoid(x . g) (x16_red_k's sh_gate_w, engine/kernels/x16/x16_dev.cu:315-334) in the GPU
+ * combine's order: sixteen partial sums, partial j over h = 128 b + 8 j + i (b ascending, then i), one fmaf each; the
+ * sixteen added by a butterfly (pairs j, j ^ s for s = 8, 4, 2, 1); then the fixed-sequence sigmoid. */
+float bmxo_shared_gate(const uint16_t* x, const uint16_t* g, int H)
+{
+    float acc[16], nxt[16];
+    for (int j = 0; j < 16; ++j)
+    {
+        acc[j] = 0.0f;
+        for (int b = 0; b < H / 128; ++b)
+            for (int i = 0; i < 8; ++i)
+            {
+                const int h = 128 * b + 8 * j + i;
+                acc[j] = fmaf(bmxo_f16_to_f32(x[h]), bmxo_f16_to_f32(g[h]), acc[j]);
+            }
+    }
+    for (int s = 8; s >= 1; s >>= 1)
+    {
+        for (int j = 0; j < 16; ++j) nxt[j] = acc[j] + acc[j ^ s];
+        memcpy(acc, nxt, sizeof(acc));
+    }
+    return bmxo_sigmoid(acc[0]);
+}
+
+void bmxo_moe_forward(const bmxo_expert* experts, int E, int64_t first, const bmxo_expert* shared,
+                      const uint16_t* sh_gate, int H, int I, int act, int gated, float limit, const uint16_t* x, int T,
+                      int topk, const int64_t* sel, const uint16_t* w, const int* rows, int nrows, float* out)
 {
     const int nr = rows ? nrows : T;
     float* ys = (float*)calloc((size_t)nr * topk * H, 4);
@@ -384,7 +408,12 @@ void bmxo_moe_forward(const bmxo_expert* experts, int E, int64_t first, const bm
                 const float p = wk * ys[((size_t)ri * topk + k) * H + h];
                 o = o + p;
             }
-            if (shared) o = o + ysh[(size_t)ri * H + h];
+            if (shared && sh_gate)
+            {
+                const float p = bmxo_shared_gate(x + (size_t)t * H, sh_gate, H) * ysh[(size_t)ri * H + h];
+                o = o + p;
+            }
+            else if (shared) o = o + ysh[(size_t)ri * H + h];
             out[(size_t)ri * H + h] = o;
         }
     }
@@ -395,9 +424,11 @@ void bmxo_moe_forward(const bmxo_expert* experts, int E, int64_t first, const bm
 /* router                                                                                                           */
 /* ---------------------------------------------------------------------------------------------------------------- */
 
-/* exp(x) in fp32 by a fixed operation sequence (round-to-nearest-even range reduction, ln 2 split in two, degree-7
- * Taylor polynomial in Horner form on |r| <= ln2/2, exact scaling by powers of two). The HIP router evaluates the same
- * sequence, so both produce the same bits. Max relative error ~2 ulp, checked against libm in the tests. */
+/* exp(x) in fp32 by a fixed operation sequence: Cody-Waite range reduction (W. J. Cody and W. Waite, Software Manual
+ * for the Elementary Functions, 1980) with n = rint(x / ln 2) and ln 2 split in two (the high / low pair SLEEF's expf
+ * uses, 0.693145751953125 + 1.428606765330187e-06), the degree-7 Taylor polynomial of exp in Horner form on
+ * |r| <= ln2/2, exact scaling by powers of two. The HIP router evaluates the same sequence, so both produce the same
+ * bits. Max relative error ~2 ulp, checked against libm in the tests. */
 float bmxo_exp(float x)
 {
     if (x != x) return x;
@@ -432,6 +463,28 @@ float bmxo_sigmoid(float x)
     return 1.0f / d;
 }
 
+/* sqrt(softplus(x)) = sqrt(max(x, 0) + log1p(exp(-|x|))) by a fixed sequence: log1p(e) = 2 atanh(e / (2 + e)) as the
+ * odd series 2 (s + s^3/3 + ... + s^17/17) in Horner form over s^2 (Abramowitz and Stegun 4.1.27; s <= 1/3); correctly
+ * rounded division and square root. The HIP router evaluates the same sequence. */
+float bmxo_sqrtsp(float x)
+{
+    if (x != x) return x;
+    const float e = bmxo_exp(-fabsf(x));
+    const float s = e / (2.0f + e);
+    const float s2 = s * s;
+    float p = 1.0f / 17.0f;
+    p = fmaf(p, s2, 1.0f / 15.0f);
+    p = fmaf(p, s2, 1.0f / 13.0f);
+    p = fmaf(p, s2, 1.0f / 11.0f);
+    p = fmaf(p, s2, 1.0f / 9.0f);
+    p = fmaf(p, s2, 1.0f / 7.0f);
+    p = fmaf(p, s2, 1.0f / 5.0f);
+    p = fmaf(p, s2, 1.0f / 3.0f);
+    p = fmaf(p, s2, 1.0f);
+    const float l = (2.0f * s) * p;
+    return sqrtf(fmaxf(x, 0.0f) + l);
+}
+
 /* a ranks before b: larger value, then lower index (ties -> lower index: engine/kernels/nv2/nv2_host.cpp:917) */
 static int better(float va, int ia, float vb, int ib) { return va > vb || (va == vb && ia < ib); }
 
@@ -462,7 +515,11 @@ void bmxo_router(const uint16_t* logits, const float* bias, int T, int E, int to
         {
             const float l = canon(bmxo_f16_to_f32(lg[e]));
             if (score_fn == BMXO_SCORE_SOFTMAX) { sc[e] = bmxo_exp(l - mx); ch[e] = l; }
-            else { sc[e] = bmxo_sigmoid(l); ch[e] = canon(bias ? sc[e] + bias[e] : sc[e]); }
+            else
+            {
+                sc[e] = score_fn == BMXO_SCORE_SQRTSP ? bmxo_sqrtsp(l) : bmxo_sigmoid(l);
+                ch[e] = canon(bias ? sc[e] + bias[e] : sc[e]);
+            }
             ok[e] = 1;
             taken[e] = 0;
         }
@@ -509,7 +566,7 @@ void bmxo_router(const uint16_t* logits, const float* bias, int T, int E, int to
         else if (renorm) den = vsum;
         for (int k = 0; k < topk; ++k)
         {
-            const float q = (score_fn == BMXO_SCORE_SIGMOID && !renorm) ? vals[k] : vals[k] / den;
+            const float q = (score_fn != BMXO_SCORE_SOFTMAX && !renorm) ? vals[k] : vals[k] / den;
             const float v = q * scale;
             sel[(size_t)t * topk + k] = (int64_t)idx[k] + first;
             w[(size_t)t * topk + k] = bmxo_f32_to_f16(v);

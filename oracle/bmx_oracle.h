@@ -61,15 +61,19 @@ void bmxo_expert_forward(const bmxo_expert* e, int H, int I, int act, int gated,
 
 /* Full layer on a subset of tokens: out[ti][H] for tokens rows[ti] (rows == NULL: all T tokens).
  * sel int64 [T, topk] global ids (first .. first + E - 1; anything else is a dropped pick), w fp16 bits [T, topk].
- * shared: optional shared expert (weight 1), added after the routed slots. */
-void bmxo_moe_forward(const bmxo_expert* experts, int E, int64_t first, const bmxo_expert* shared, int H, int I,
-                      int act, int gated, float limit, const uint16_t* x, int T, int topk, const int64_t* sel,
-                      const uint16_t* w, const int* rows, int nrows, float* out);
+ * shared: optional shared expert, added after the routed slots with weight bmxo_shared_gate(x, sh_gate) when sh_gate
+ * (fp16 bits [H]) is given, else 1. */
+void bmxo_moe_forward(const bmxo_expert* experts, int E, int64_t first, const bmxo_expert* shared,
+                      const uint16_t* sh_gate, int H, int I, int act, int gated, float limit, const uint16_t* x, int T,
+                      int topk, const int64_t* sel, const uint16_t* w, const int* rows, int nrows, float* out);
+/* sigmoid(x . g) in the GPU combine's fixed order (x, g fp16 bits [H], H a multiple of 128) */
+float bmxo_shared_gate(const uint16_t* x, const uint16_t* g, int H);
 
 /* router */
-enum { BMXO_SCORE_SOFTMAX = 0, BMXO_SCORE_SIGMOID = 1 };
+enum { BMXO_SCORE_SOFTMAX = 0, BMXO_SCORE_SIGMOID = 1, BMXO_SCORE_SQRTSP = 2 };
 float bmxo_exp(float x);        /* the fixed-sequence fp32 exp the HIP router also evaluates */
 float bmxo_sigmoid(float x);
+float bmxo_sqrtsp(float x);     /* the fixed-sequence sqrt(softplus(x)) the HIP router also evaluates */
 /* logits fp16 bits [T, E]; bias fp32 [E] or NULL; n_group / topk_group (1 / 1 = no group limit);
  * out: sel int64 [T, topk] (global ids = local + first), w fp16 bits [T, topk] */
 void bmxo_router(const uint16_t* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,

@@ -23,7 +23,7 @@ TF_K2, TF_K25, TF_K3, TF_K4 = 0, 1, 2, 3
 TF_KA = {TF_K2: 2, TF_K25: 2, TF_K3: 3, TF_K4: 4}
 TF_MASK = {TF_K2: 0, TF_K25: 0xAAAA, TF_K3: 0, TF_K4: 0}
 TF_TB = {TF_K2: 64, TF_K25: 80, TF_K3: 96, TF_K4: 128}
-SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSP = 0, 1, 2
 ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
 
 _P = ctypes.c_void_p
@@ -58,10 +58,12 @@ def lib():
         L.bmxo_had128.argtypes = [_P]
         L.bmxo_prep.argtypes = [_P, _P, _I, _P]
         L.bmxo_expert_forward.argtypes = [_P, _I, _I, _I, _I, ctypes.c_float, _P, _P, _P, _P, _P]
-        L.bmxo_moe_forward.argtypes = [_P, _I, ctypes.c_int64, _P, _I, _I, _I, _I, ctypes.c_float, _P, _I, _I, _P, _P,
+        L.bmxo_moe_forward.argtypes = [_P, _I, ctypes.c_int64, _P, _P, _I, _I, _I, _I, ctypes.c_float, _P, _I, _I, _P, _P,
                                        _P, _I, _P]
         L.bmxo_exp.argtypes = [ctypes.c_float]; L.bmxo_exp.restype = ctypes.c_float
         L.bmxo_sigmoid.argtypes = [ctypes.c_float]; L.bmxo_sigmoid.restype = ctypes.c_float
+        L.bmxo_sqrtsp.argtypes = [ctypes.c_float]; L.bmxo_sqrtsp.restype = ctypes.c_float
+        L.bmxo_shared_gate.argtypes = [_P, _P, _I]; L.bmxo_shared_gate.restype = ctypes.c_float
         L.bmxo_act.argtypes = [_I, _I, ctypes.c_float, ctypes.c_float, ctypes.c_float]; L.bmxo_act.restype = ctypes.c_float
         L.bmxo_router.argtypes = [_P, _P, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, ctypes.c_int64, _P, _P]
         L.bmxo_dispatch.argtypes = [_P, _I, _I, _I, ctypes.c_int64, _I, _P, _P, _P, _P, _P, _P]
@@ -149,9 +151,10 @@ def expert_forward(ex, H, I, x, act=ACT_SILU, gated=True, limit=0.0):
     return y, g.view(np.float16), u.view(np.float16), a.view(np.float16)
 
 
-def moe_forward(experts, first, shared, H, I, x, sel, w, rows=None, act=ACT_SILU, gated=True, limit=0.0):
+def moe_forward(experts, first, shared, H, I, x, sel, w, rows=None, act=ACT_SILU, gated=True, limit=0.0, sh_gate=None):
     """Layer output fp32 [len(rows) or T, H]. experts: list of dicts with tr / suh / svh / fmt (3 each), None for
-    experts no selected pick uses."""
+    experts no selected pick uses. sh_gate: fp16 [H] gate vector of the shared expert (its output scaled by
+    sigmoid(x . sh_gate)), or None (weight 1)."""
     E = len(experts)
     arr = (_Expert * E)()
     keep = []
@@ -171,7 +174,9 @@ def moe_forward(experts, first, shared, H, I, x, sel, w, rows=None, act=ACT_SILU
     r = None if rows is None else _c(rows, np.int32)
     nr = T if rows is None else r.size
     out = np.zeros((nr, H), np.float32)
-    lib().bmxo_moe_forward(ctypes.cast(arr, _P), E, first, ctypes.byref(sh) if sh is not None else None, H, I, act,
+    g = None if sh_gate is None else _c(sh_gate, np.float16).view(np.uint16)
+    lib().bmxo_moe_forward(ctypes.cast(arr, _P), E, first, ctypes.byref(sh) if sh is not None else None,
+                           _p(g) if g is not None else None, H, I, act,
                            int(gated), limit, _p(x), T, topk, _p(sel), _p(w), _p(r) if r is not None else None, nr,
                            _p(out))
     return out
@@ -249,6 +254,24 @@ class SlotTable:
         nj = lib().bmxo_slot_prefetch(ctypes.byref(self._s), li, _p(sel), sel.size, first, min(limit, 1 << 30), maxj,
                                       _p(jobs), _p(ev), _p(self.stats))
         return jobs[:2 * nj].reshape(nj, 2), ev[:nj]
+
+
+def sqrtsp32(x):
+    """the fixed-sequence sqrt(softplus(x)) of the router's sqrt-softplus score"""
+    return np.float32(lib().bmxo_sqrtsp(float(x)))
+
+
+def shared_gate(x, g):
+    """sigmoid(x . g) of one token in the GPU combine's fixed order (x, g fp16 [H])"""
+    x = _c(x, np.float16).view(np.uint16)
+    g = _c(g, np.float16).view(np.uint16)
+    return np.float32(lib().bmxo_shared_gate(_p(x), _p(g), x.size))
+
+
+def router_logits(z, weight):
+    """The router projection's exact value in float64: z fp16 [T, H] times weight fp16 [E, H] transposed (the GPU's
+    fp16 logits are this value's RN16 within the fp32 accumulation's error)."""
+    return np.asarray(z, np.float16).astype(np.float64) @ np.asarray(weight, np.float16).astype(np.float64).T
 
 
 def exp32(x):

@@ -234,3 +234,128 @@ def test_slot_prefetch_properties_random(oracle):
             st.step(lj, np.array(got))
             assert st.stats[0] - stats0[0] == len(got) and np.flatnonzero(st.fresh).tolist() == sorted(got)
             assert st.stats[6] - stats0[6] == len(got)
+
+
+# ---- sqrt-softplus score, router projection, shared-expert gate ------------------------------------------------------
+
+def _sqrtsp64(x):
+    x = np.asarray(x, np.float64)
+    return np.sqrt(np.logaddexp(0.0, x))      # sqrt(log(1 + e^x)) without overflow
+
+
+def test_sqrtsp_fixed_accuracy(oracle):
+    """The fixed-sequence sqrt(softplus(x)) against the float64 closed form: within 2 fp32 ulps over a sweep that covers
+    the series' range (|x| small: s near 1/3), the tails (e^-|x| tiny) and the limits; a plausible mistake in the
+    restatement (the max(x, 0) term dropped, or log1p replaced by the raw series variable) fails the same bound."""
+    xs = np.concatenate([np.linspace(-30, 30, 24001), np.linspace(-80, 104, 2001),
+                         np.array([0.0, -0.0, 1e-8, -1e-8, 1e-30, 88.0, -80.0])]).astype(np.float32)
+    got = np.array([oracle.sqrtsp32(v) for v in xs], np.float64)
+    want = _sqrtsp64(xs)
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert np.max(np.abs(got - want) / ulp) <= 2.0
+    # below x = -87 softplus(x) = e^x is subnormal in fp32 and keeps fewer bits: an absolute error of two subnormal
+    # spacings (2^-148) in softplus is at most 2^-74 after the square root
+    tail = np.linspace(-103, -81, 221).astype(np.float32)
+    gt = np.array([oracle.sqrtsp32(v) for v in tail], np.float64)
+    wt = _sqrtsp64(tail)
+    assert np.all(np.abs(gt - wt) <= 2.0 ** -74 + 4 * np.spacing(wt.astype(np.float32)))
+    assert oracle.sqrtsp32(float("inf")) == float("inf") and oracle.sqrtsp32(float("-inf")) == 0.0
+    assert np.isnan(oracle.sqrtsp32(float("nan")))
+    # planted mistakes, evaluated on the same sweep, must fail the bound
+    e = np.exp(-np.abs(xs.astype(np.float64)))
+    no_max = np.sqrt(np.log1p(e))
+    raw_s = np.sqrt(np.maximum(xs, 0) + 2.0 * e / (2.0 + e))
+    for bad in (no_max, raw_s):
+        assert np.max(np.abs(bad - want) / ulp) > 100.0
+
+
+def test_router_sqrtsp_topk(oracle):
+    """sqrt-softplus scoring (DeepSeek-V4's router): selection by score + bias, weights = scores renormalised over the
+    picks times the scale, or the raw scores without renormalisation; against the float64 closed form."""
+    rng = np.random.default_rng(21)
+    T, E, k = 32, 256, 6
+    lg = (rng.standard_normal((T, E)) * 2.0).astype(np.float16)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    for renorm in (True, False):
+        sel, w = oracle.router(lg, k, bias=bias, score_fn=oracle.SCORE_SQRTSP, renorm=renorm, scale=1.5, first=5)
+        for t in range(T):
+            sc = _sqrtsp64(lg[t].astype(np.float64))
+            ch = sc + bias
+            order = sorted(range(E), key=lambda e: (-ch[e], e))
+            want = order[:k]
+            # a selection boundary closer than fp32 rounding could flip; the draws here have none
+            assert ch[order[k - 1]] - ch[order[k]] > 1e-5
+            assert (sel[t] - 5).tolist() == want
+            v = sc[want]
+            ref = v / v.sum() * 1.5 if renorm else v * 1.5
+            assert np.allclose(w[t].astype(np.float64), ref, rtol=2e-3, atol=0)
+    # grouped selection works on the same scores
+    sel, _ = oracle.router(lg, k, bias=bias, n_group=8, topk_group=4, score_fn=oracle.SCORE_SQRTSP)
+    gs = E // 8
+    for t in range(T):
+        ch = _sqrtsp64(lg[t].astype(np.float64)) + bias
+        gsc = [np.sort(ch[g * gs:(g + 1) * gs])[-2:].sum() for g in range(8)]
+        keep = set(sorted(range(8), key=lambda g: (-gsc[g], g))[:4])
+        assert all(int(e) // gs in keep for e in sel[t])
+
+
+def test_shared_gate_closed_form(oracle):
+    """sigmoid(x . g) in the GPU combine's order against float64 (scipy's expit of the exact dot), within 2e-7; the
+    order's one-lane-per-16 partial sums matter only at fp32 rounding; planted mistakes (the butterfly's last stage
+    dropped, the sigmoid left out) fail."""
+    from scipy.special import expit
+    rng = np.random.default_rng(5)
+    for H in (128, 2048, 4096):
+        for _ in range(5):
+            x = rng.standard_normal(H).astype(np.float16)
+            g = (rng.standard_normal(H) / np.sqrt(H)).astype(np.float16)
+            dot = float(x.astype(np.float64) @ g.astype(np.float64))
+            got = float(oracle.shared_gate(x, g))
+            assert abs(got - expit(dot)) < 2e-7
+            # planted: half the partial sums missing (no last butterfly stage), or the raw dot
+            parts = [sum(float(x[h]) * float(g[h]) for b in range(H // 128) for h in range(128 * b + 8 * j, 128 * b + 8 * j + 8))
+                     for j in range(16)]
+            assert abs(expit(sum(parts[:8])) - got) > 1e-6 or abs(sum(parts[8:])) < 1e-3
+            assert abs(dot - got) > 1e-3 or abs(expit(dot) - dot) < 1e-3
+    z = np.zeros(256, np.float16)
+    assert float(oracle.shared_gate(z, z)) == 0.5
+
+
+def test_moe_forward_shared_gate(oracle):
+    """The layer with a gated shared expert: a zero gate vector gives sigmoid(0) = 1/2 exactly, so the output is the
+    routed sum plus half the shared expert's output (the ungated layer minus the routed-only layer)."""
+    rng = np.random.default_rng(8)
+    E, H, I, T, k = 6, 256, 128, 3, 2
+    exps = [_rand_expert(rng, H, I) for _ in range(E)]
+    sh = _rand_expert(rng, H, I)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    sel = np.array([[0, 3], [5, 1], [2, 2]], np.int64)
+    w = np.array([[0.6, 0.4], [0.7, 0.3], [0.5, 0.5]], np.float16)
+    routed = oracle.moe_forward(exps, 0, None, H, I, x, sel, w)
+    full = oracle.moe_forward(exps, 0, sh, H, I, x, sel, w)
+    half = oracle.moe_forward(exps, 0, sh, H, I, x, sel, w, sh_gate=np.zeros(H, np.float16))
+    assert np.allclose(half, routed + 0.5 * (full - routed), rtol=1e-6, atol=1e-6)
+    g = (rng.standard_normal(H) * 0.05).astype(np.float16)
+    gated = oracle.moe_forward(exps, 0, sh, H, I, x, sel, w, sh_gate=g)
+    for t in range(T):
+        gv = float(oracle.shared_gate(x[t], g))
+        assert np.allclose(gated[t], routed[t] + gv * (full[t] - routed[t]), rtol=1e-5, atol=1e-6)
+
+
+def test_router_projection_closed_form(oracle):
+    """The oracle's projection (float64 product) against a brute-force sum on a small case."""
+    rng = np.random.default_rng(3)
+    z = rng.standard_normal((3, 64)).astype(np.float16)
+    W = rng.standard_normal((5, 64)).astype(np.float16)
+    got = oracle.router_logits(z, W)
+    for t in range(3):
+        for e in range(5):
+            assert got[t, e] == pytest.approx(sum(float(z[t, h]) * float(W[e, h]) for h in range(64)), rel=1e-12, abs=1e-12)
+
+
+def _rand_expert(rng, H, I, fmt=2):
+    tb = {0: 64, 1: 80, 2: 96, 3: 128}[fmt]
+    tr = [rng.integers(0, 256, (a // 16) * (b // 16) * tb, dtype=np.uint8) for a, b in ((H, I), (H, I), (I, H))]
+    suh = [(rng.random(n) + 0.5).astype(np.float16) for n in (H, H, I)]
+    svh = [((rng.random(n) + 0.5) / np.sqrt(kk)).astype(np.float16) for n, kk in ((I, H), (I, H), (H, I))]
+    return {"tr": tr, "suh": suh, "svh": svh, "fmt": [fmt] * 3}
