@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from test_store import E, exl3_checkpoint
+from test_store import E, exl3_checkpoint, tensor_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -22,13 +22,13 @@ def direct_table(tensors, l, H, I, cuda):
     mats = ("gate_proj", "up_proj", "down_proj")
     rows, suh, svh = [], [[], [], []], [[], [], []]
     for e in range(E):
-        parts = [tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.trellis"][2] for m in mats]
+        parts = [tensor_bytes(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.trellis"]) for m in mats]
         rows.append(np.frombuffer(b"".join(parts), np.uint8))
         for i, m in enumerate(mats):
-            suh[i].append(np.frombuffer(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.suh"][2], np.float16))
-            svh[i].append(np.frombuffer(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.svh"][2], np.float16))
-    n0 = len(tensors[f"model.layers.{l}.mlp.experts.0.gate_proj.trellis"][2])
-    n1 = len(tensors[f"model.layers.{l}.mlp.experts.0.up_proj.trellis"][2])
+            suh[i].append(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.suh"])
+            svh[i].append(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.svh"])
+    n0 = tensors[f"model.layers.{l}.mlp.experts.0.gate_proj.trellis"].nbytes
+    n1 = tensors[f"model.layers.{l}.mlp.experts.0.up_proj.trellis"].nbytes
     arena = torch.from_numpy(np.stack(rows)).to(cuda)
     tb = n0 // ((H // 16) * (I // 16))
     fmt = {64: 0, 80: 1, 96: 2, 128: 3}[tb]

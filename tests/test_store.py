@@ -3,80 +3,79 @@
 The v1 layout's known answers are the reference's own (tests/test_store.py:12-49 of the reference: two MoE layers of
 4 experts, 4096-byte trellis tensors, 64 / 32-value scales -> trellis part 12288, record 16384, slot offsets 4096 /
 8192, a corrupted byte found in record 5)."""
+import itertools
 import json
-import struct
 
 import numpy as np
 import pytest
 
 LAYERS, E = (3, 4), 4
+GLM = ("gate_proj", "up_proj", "down_proj")
 
 
-def write_safetensors(path, tensors):
-    """tensors: {name: (dtype, shape, bytes)}"""
-    hdr, off, blobs = {}, 0, []
-    for name, (dt, shape, data) in tensors.items():
-        hdr[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(data)]}
-        blobs.append(data)
-        off += len(data)
-    h = json.dumps(hdr).encode()
-    h += b" " * (-len(h) % 8)
-    with open(path, "wb") as f:
-        f.write(struct.pack("<Q", len(h)) + h + b"".join(blobs))
+def save_checkpoint(directory, tensors, shards=1):
+    """A sharded safetensors checkpoint written by the safetensors library: tensors {key: numpy array} dealt over the
+    shards in sorted key order, and the model.safetensors.index.json weight map."""
+    from safetensors.numpy import save_file
+    directory.mkdir()
+    keys = sorted(tensors)
+    weight_map = {}
+    for i in range(shards):
+        fn = f"model-{i + 1:05d}-of-{shards:05d}.safetensors"
+        part = {k: np.ascontiguousarray(tensors[k]) for k in keys[i::shards]}
+        save_file(part, str(directory / fn))
+        weight_map.update(dict.fromkeys(part, fn))
+    (directory / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
 
 
-def write_checkpoint(d, tensors, shards=1):
-    d.mkdir()
-    names = sorted(tensors)
-    wm = {}
-    for s in range(shards):
-        fn = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
-        part = {k: tensors[k] for k in names[s::shards]}
-        write_safetensors(d / fn, part)
-        wm.update({k: fn for k in part})
-    (d / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
-
-
-def small_checkpoint(d):
-    """The reference test's checkpoint: layers 3 and 4, 4 experts, byte patterns per tensor, .mul1 markers."""
-    t, seed = {}, 0
-    for l in LAYERS:
-        t[f"model.layers.{l}.self_attn.q_proj.weight"] = ("F16", (64,), bytes([l]) * 128)
+def pattern_checkpoint(directory):
+    """Two MoE layers (model layers 3 and 4) of 4 experts, the sizes of the reference's store test: int16 trellis
+    tensors of 4096 bytes, fp16 suh of 64 and svh of 32 values, an int32 .mul1 marker (7) per matrix, and one
+    attention tensor per layer that the store must skip. Every tensor holds its own ramp of values, so a record can be
+    checked byte by byte."""
+    t = {}
+    tag = itertools.count(1)
+    for layer in LAYERS:
+        t[f"model.layers.{layer}.self_attn.q_proj.weight"] = np.full(64, layer, np.float16)
         for e in range(E):
-            for m in ("gate_proj", "up_proj", "down_proj"):
-                seed += 1
-                k = f"model.layers.{l}.mlp.experts.{e}.{m}"
-                t[k + ".trellis"] = ("I16", (2048,), bytes([seed % 251]) * 4096)
-                t[k + ".suh"] = ("F16", (64,), bytes([(seed + 1) % 251]) * 128)
-                t[k + ".svh"] = ("F16", (32,), bytes([(seed + 2) % 251]) * 64)
-                t[k + ".mul1"] = ("I32", (), struct.pack("<i", 7))
-    write_checkpoint(d, t, shards=2)
+            for m in GLM:
+                k = f"model.layers.{layer}.mlp.experts.{e}.{m}"
+                n = next(tag)
+                t[k + ".trellis"] = (np.arange(2048, dtype=np.int32) * 7 + n * 1000).astype(np.int16)
+                t[k + ".suh"] = (np.arange(64) / 64 + n).astype(np.float16)
+                t[k + ".svh"] = (np.arange(32) / 32 - n).astype(np.float16)
+                t[k + ".mul1"] = np.array(7, np.int32)
+    save_checkpoint(directory, t, shards=2)
     return t
 
 
-def exl3_checkpoint(d, layers, H, I, tile_bytes, seed=0, naming=("gate_proj", "up_proj", "down_proj"), mul1=True):
+def exl3_checkpoint(d, layers, H, I, tile_bytes, seed=0, naming=GLM, mul1=True):
     """Random EXL3-shaped experts: trellis int16 [k/16, n/16, 8 * TB / 16], suh fp16 [k], svh fp16 [n]; tile_bytes
-    per layer (64 / 80 / 96 / 128 for K 2 / 2.5 / 3 / 4)."""
+    per layer (64 / 80 / 96 / 128 for K 2 / 2.5 / 3 / 4). Returns {key: numpy array}."""
     rng = np.random.default_rng(seed)
     t = {}
-    for li, (l, tb) in enumerate(zip(layers, tile_bytes)):
+    for l, tb in zip(layers, tile_bytes):
         for e in range(E):
             for m, (k, n) in zip(naming, ((H, I), (H, I), (I, H))):
                 key = f"model.layers.{l}.mlp.experts.{e}.{m}"
                 tr = rng.integers(0, 256, (k // 16) * (n // 16) * tb, dtype=np.uint8)
-                t[key + ".trellis"] = ("I16", (k // 16, n // 16, tb // 2), tr.tobytes())
-                t[key + ".suh"] = ("F16", (k,), (rng.random(k) + 0.5).astype(np.float16).tobytes())
-                t[key + ".svh"] = ("F16", (n,), ((rng.random(n) + 0.5) / np.sqrt(k)).astype(np.float16).tobytes())
+                t[key + ".trellis"] = tr.view(np.int16).reshape(k // 16, n // 16, tb // 2)
+                t[key + ".suh"] = (rng.random(k) + 0.5).astype(np.float16)
+                t[key + ".svh"] = ((rng.random(n) + 0.5) / np.sqrt(k)).astype(np.float16)
                 if mul1:
-                    t[key + ".mul1"] = ("I32", (), struct.pack("<I", 0x83DCD12D))
-    write_checkpoint(d, t)
+                    t[key + ".mul1"] = np.array(0x83DCD12D, np.uint32).view(np.int32)
+    save_checkpoint(d, t)
     return t
+
+
+def tensor_bytes(a):
+    return np.ascontiguousarray(a).tobytes()
 
 
 def test_v1_layout_known_answers(tmp_path):
     from bmx import store
     ck = tmp_path / "ckpt"
-    tensors = small_checkpoint(ck)
+    tensors = pattern_checkpoint(ck)
     out = tmp_path / "out"
     out.mkdir()
     store.pack(ck, out, "x", version=1, threads=2)
@@ -85,17 +84,15 @@ def test_v1_layout_known_answers(tmp_path):
     assert raw["n_layers"] == 2 and raw["experts_per_layer"] == E and raw["trellis_bytes"] == 3 * 4096
     assert raw["record_bytes"] == 4096 * 4 and raw["vram_slot"] == {"off_u": 4096, "off_d": 8192, "slot_bytes": 12288}
     assert [L["model_layer"] for L in raw["layers"]] == list(LAYERS)
-    assert raw["mul1_markers_hex"] == [struct.pack("<i", 7).hex()]
+    assert raw["mul1_markers_hex"] == [np.array(7, "<i4").tobytes().hex()]
     assert store.verify(out, "x", threads=2) == []
     # every record is its tensors in field order, then zeros
     blob = open(out / "x.bin", "rb").read()
     for li, l in enumerate(LAYERS):
         for e in range(E):
             rec = blob[(li * E + e) * 16384:(li * E + e + 1) * 16384]
-            want = b"".join(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.trellis"][2]
-                            for m in ("gate_proj", "up_proj", "down_proj"))
-            want += b"".join(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.{s}"][2]
-                             for m in ("gate_proj", "up_proj", "down_proj") for s in ("suh", "svh"))
+            want = b"".join(tensor_bytes(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.trellis"]) for m in GLM)
+            want += b"".join(tensor_bytes(tensors[f"model.layers.{l}.mlp.experts.{e}.{m}.{s}"]) for m in GLM for s in ("suh", "svh"))
             assert rec == want + bytes(16384 - len(want))
     with open(out / "x.bin", "r+b") as f:              # corrupt one byte of record 5 (layer 1, expert 1)
         f.seek(5 * 16384 + 100)
@@ -127,12 +124,12 @@ def test_v2_per_layer_records_and_classes(tmp_path):
         assert (H, I) == (256, 128) and fmts == ((2, 2, 2) if li != 1 else (0, 0, 0))
         for e in range(E):
             for m_ in ("gate_proj", "up_proj", "down_proj"):
-                tr = tensors[f"model.layers.{li}.mlp.experts.{e}.{m_}.trellis"][2]
+                tr = tensor_bytes(tensors[f"model.layers.{li}.mlp.experts.{e}.{m_}.trellis"])
                 assert bytes(st.field(li, f"{m_}.trellis")[e]) == tr
-                suh = np.frombuffer(tensors[f"model.layers.{li}.mlp.experts.{e}.{m_}.suh"][2], np.float16)
+                suh = tensors[f"model.layers.{li}.mlp.experts.{e}.{m_}.suh"]
                 assert np.array_equal(st.field(li, f"{m_}.suh")[e], suh)
             img = bytes(st.records(li)[e, :tb])
-            assert img[off_u:off_u + 10] == tensors[f"model.layers.{li}.mlp.experts.{e}.up_proj.trellis"][2][:10]
+            assert img[off_u:off_u + 10] == tensor_bytes(tensors[f"model.layers.{li}.mlp.experts.{e}.up_proj.trellis"])[:10]
     assert st.verify() == []
 
 
@@ -153,7 +150,7 @@ def test_v1_refuses_mixed_layers_and_reads_deepseek_names(tmp_path):
 def test_geometry_rejects_non_exl3_shapes(tmp_path):
     from bmx import store
     ck = tmp_path / "ckpt"
-    small_checkpoint(ck)
+    pattern_checkpoint(ck)
     (tmp_path / "o").mkdir()
     store.pack(ck, tmp_path / "o", "x", version=1)
     with pytest.raises(ValueError, match="trellis"):
