@@ -264,13 +264,17 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(DpArgs a)
     a.r.row_expert[row] = e;
 }
 
+// Most work groups a dispatch can produce: an expert with c rows gives ceil(c / rpg) <= 1 + (c - 1) / rpg groups, so u
+// experts with rows in total give at most u + (rows - u) / rpg, largest for the most experts a batch can touch.
 int groups_max(int T, int topk, int E, int shared, int rpg)
 {
     const long n = (long)T * topk;
     const long ne = E + (shared ? 1 : 0);
-    const long uniq = n + (shared ? 1 : 0) < ne ? n + (shared ? 1 : 0) : ne;
     const long rows = n + (shared ? T : 0);
-    return (int)(uniq + rows / rpg + 1);
+    long u = n + (shared ? 1 : 0);
+    if (u > ne) u = ne;
+    if (u > rows) u = rows;
+    return (int)(u + (rows - u) / rpg);
 }
 
 size_t dispatch_ws_bytes(int T, int topk, int E)
