@@ -13,6 +13,8 @@ ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
 PATH_AUTO, PATH_DECODE, PATH_PREFILL, PATH_MID = 0, 1, 2, 3
 STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT, STAGE_PREP = 0, 1, 2, 3, 4, 5
 STAGE_GATE_UP_RESIDENT, STAGE_GATE_UP_STAGED = 6, 7
+LANE_VRAM, LANE_ADMIT, LANE_HOME, LANE_CPU = 0, 1, 2, 3
+PLAN_MAXP, PLAN_MAXT = 64, 8
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -41,6 +43,13 @@ class SlotTable(ctypes.Structure):
 
 class CpuExpert(ctypes.Structure):
     _fields_ = [("tr", _P * 3), ("suh", _P * 3), ("svh", _P * 3), ("fmt", ctypes.c_int32 * 3), ("reserved", ctypes.c_int32)]
+
+
+class PlanPolicy(ctypes.Structure):
+    _fields_ = [("cpu_on", ctypes.c_int32), ("max_cpu", ctypes.c_int32), ("home_single", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)] + \
+               [(n, ctypes.c_double) for n in ("gpu_base_us", "gpu_hit_us", "gpu_home_us", "gpu_admit_us", "cpu_base_us",
+                                               "cpu_expert_us", "cpu_token_us")]
 
 
 class RouterDesc(ctypes.Structure):
@@ -95,6 +104,11 @@ SIGNATURES = {
     "bmx_decode_splits": (_I, [ctypes.POINTER(MoeDesc), _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "bmx_cpu_dot2": (_I, [_P, _P, _P, _P, _I]),
     "bmx_dot2_f32_f16": (_I, [_P, _P, _P, _P, _I, _P]),
+    "bmx_copy_agent_plan": (_I, [_P, ctypes.POINTER(PlanPolicy)]),
+    "bmx_copy_agent_cpu_lane": (_I, [_P, ctypes.POINTER(MoeDesc), _P, _I]),
+    "bmx_slot_step_planned": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _P, _I, _I, _I64, _I, _P, _P, _P, _P,
+                                   ctypes.POINTER(_I64), _P]),
+    "bmx_cpu_lane_add": (_I, [_P, _I64, _P, _I, _P]),
     "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
     "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }

@@ -72,8 +72,18 @@ class MoELayer:
 
     # ---- engine hook: residency before the experts run ----
     def layer(self, li, sel, w, z, bsz):
-        if self.slots is not None:
-            self.slots.step(li, sel, True, first=self.routing_first)
+        """The slot-table step of this call. With a planned table (ExpertSlots.plan) the agent's planner answers the
+        step: returns the selection the GPU computes (CPU-lane picks masked) and whether a CPU job may add to this call
+        (combine() adds it), as the reference's Nv2.layer (engine/nv2.py:374-437)."""
+        self._cpu_seq = None
+        if self.slots is None:
+            return sel, w, False
+        if getattr(self.slots, "planned", False):
+            sel_gpu, w_gpu, _, seq = self.slots.step_planned(li, sel, w, z, True, first=self.routing_first)
+            if z is not None and bsz <= L.PLAN_MAXT and sel.numel() <= L.PLAN_MAXP:
+                self._cpu_seq = seq
+            return sel_gpu.view(sel.shape), w_gpu.view(w.shape), self._cpu_seq is not None
+        self.slots.step(li, sel, True, first=self.routing_first)
         return sel, w, False
 
     # ---- experts + combine ----
@@ -162,7 +172,12 @@ class MoELayer:
         return fhs.view(shape) if shape is not None else fhs
 
     def combine(self, fhs):
-        return fhs if fhs.is_contiguous() else fhs.contiguous()
+        """Nv2.combine (engine/nv2.py:489-493): adds the CPU lane's partial of this call's planned step, if any."""
+        fhs = fhs if fhs.is_contiguous() else fhs.contiguous()
+        seq, self._cpu_seq = getattr(self, "_cpu_seq", None), None
+        if seq is not None:
+            self.slots.cpu_add(seq, fhs.view(-1, self.hidden_size))
+        return fhs
 
     def forward(self, z, logits=None, path=L.PATH_AUTO):
         if (logits is not None or self.router_weight is not None) and self.slots is None:

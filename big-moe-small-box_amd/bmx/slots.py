@@ -64,6 +64,7 @@ class ExpertSlots:
         self.copies = copies
         self.agent = None
         self.seq = [0] * self.L               # dma: sequence number of each layer's last step
+        self.planned = False                  # dma: layer calls use planned steps (plan())
         if copies == "dma":
             homes = (ctypes.c_uint64 * (self.L * self.E))(*[t.addr[e][0] for t in layers for e in range(t.E)])
             nb = (ctypes.c_int64 * (self.L * self.E * 3))(*[t.mat_bytes(e, m) for t in layers for e in range(t.E)
@@ -183,6 +184,78 @@ class ExpertSlots:
         if self.copied[li] is not None:
             ev = self.copied[li][0 if part == "gate_up" else 1]
             (stream or torch.cuda.current_stream()).wait_event(ev)
+
+    # ---- residency plan (dma) ----
+    def plan(self, policy=None):
+        """Set the copy agent's planner (a dict of bmx_plan_policy fields; None: every miss admitted). From then on
+        layer calls through MoELayer use planned steps."""
+        if self.agent is None:
+            raise ValueError("ExpertSlots.plan: the residency plan runs on the copy agent (copies='dma')")
+        if policy is None:
+            L.check(L.lib().bmx_copy_agent_plan(self.agent, None), "bmx_copy_agent_plan")
+        else:
+            pol = L.PlanPolicy(**policy)
+            L.check(L.lib().bmx_copy_agent_plan(self.agent, ctypes.byref(pol)), "bmx_copy_agent_plan")
+        self.planned = True
+
+    def cpu_lane(self, topk, act=L.ACT_SILU, gated=True, act_limit=0.0, threads=16):
+        """Give the copy agent its CPU lane: host copies of every layer's experts (kept here) for the agent's worker."""
+        if self.agent is None:
+            raise ValueError("ExpertSlots.cpu_lane: needs the copy agent (copies='dma')")
+        import numpy as np
+        keep, exps = [], (L.CpuExpert * (self.L * self.E))()
+        for li, t in enumerate(self.layers):
+            for e in range(t.E):
+                h = t.host_expert(e)
+                arrs = [np.ascontiguousarray(a) for a in h["tr"]] + \
+                       [np.ascontiguousarray(v, dtype=np.float16) for v in h["suh"] + h["svh"]]
+                keep.append(arrs)
+                ce = exps[li * self.E + e]
+                for m in range(3):
+                    ce.tr[m] = arrs[m].ctypes.data
+                    ce.suh[m] = arrs[3 + m].ctypes.data
+                    ce.svh[m] = arrs[6 + m].ctypes.data
+                    ce.fmt[m] = int(h["fmt"][m])
+        self._cpu_keep = (keep, exps)
+        d = self.layers[0].desc(topk, self.first, act, gated, act_limit)
+        L.check(L.lib().bmx_copy_agent_cpu_lane(self.agent, ctypes.byref(d), exps, int(threads)),
+                "bmx_copy_agent_cpu_lane")
+
+    def step_planned(self, li, sel, w, x=None, admit=True, *, first=None):
+        """A planned step of layer li (bmx_slot_step_planned): publishes the call to the agent's planner, waits for its
+        reply and applies it. sel int64 [n], w fp16 [n] (device; n = T * topk), x fp16 [T, H] (the call's rows, for the
+        CPU lane) or None. Returns (sel_gpu, w_gpu, lanes, seq): the selection the GPU computes, each pick's lane, and
+        the step's sequence number (for cpu_add)."""
+        T = sel.shape[0] if sel.dim() == 2 else 1
+        topk = sel.numel() // max(T, 1)
+        sel = sel.reshape(-1)
+        if sel.dtype != torch.int64 or not sel.is_contiguous():
+            sel = sel.long().contiguous()
+        w = w.reshape(-1)
+        if w.dtype != torch.float16 or not w.is_contiguous():
+            w = w.half().contiguous()
+        if x is not None:
+            x = x.reshape(T, -1)
+            if x.dtype != torch.float16 or not x.is_contiguous():
+                x = x.half().contiguous()
+            self._x_keep = x
+        first = self.first if first is None else int(first)
+        sel_gpu, w_gpu = torch.empty_like(sel), torch.empty_like(w)
+        lanes = torch.empty(sel.numel(), dtype=torch.int32, device=sel.device)
+        q = ctypes.c_int64()
+        P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+        L.check(L.lib().bmx_slot_step_planned(ctypes.byref(self.struct), self.agent, li, P(sel), P(w), T, topk,
+                                              int(first), int(admit), P(x), P(sel_gpu), P(w_gpu), P(lanes),
+                                              ctypes.byref(q), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                "bmx_slot_step_planned")
+        self.seq[li] = q.value
+        return sel_gpu, w_gpu, lanes, q.value
+
+    def cpu_add(self, seq, out):
+        """out [T, H] fp32 += the CPU lane's partial of planned step seq (bounded wait for its job; nothing without one)."""
+        L.check(L.lib().bmx_cpu_lane_add(self.agent, int(seq), ctypes.c_void_p(out.data_ptr()), out.shape[0],
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "bmx_cpu_lane_add")
+        return out
 
     def desc(self, li, topk, first=0, act=L.ACT_SILU, gated=True, act_limit=0.0, shared_gate=None):
         return self.layers[li].desc(topk, first, act, gated, act_limit, fresh=self.fresh, shared_gate=shared_gate)

@@ -19,10 +19,13 @@
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <condition_variable>
 #include <cstring>
 #include <deque>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -32,6 +35,15 @@ namespace bmx {
 
 constexpr int AG_PENDING = 256;  // parts in flight
 constexpr int AG_SIGNALS = 2 * AG_PENDING;   // a signal is reused only after every part issued after it has retired
+
+// A CPU-lane job: the picks of one planned step that its plan put on the CPU, with the call's input rows
+struct CpuJob {
+    int64_t seq;
+    int li, ntok, topk;
+    std::vector<int> pick_e, pick_t;    // in pick order
+    std::vector<float> pick_w;
+    std::vector<uint16_t> x;            // [ntok][H]
+};
 
 }  // namespace bmx
 
@@ -56,6 +68,25 @@ struct bmx_copy_agent {
     std::atomic<int> error{0};
     std::atomic<int64_t> records{0}, copies{0};
     std::atomic<int64_t> copied_bytes{0};
+    // residency plan
+    std::mutex plan_mu;
+    bmx_plan_policy policy{};            // cpu_on 0: every miss admitted
+    std::atomic<int64_t> plans{0}, plan_cpu{0};
+    // CPU lane
+    bool cpu_ready = false;
+    bmx_moe_desc cpu_desc{};
+    std::vector<bmx_cpu_expert> cpu_experts;   // [L * E]
+    int cpu_threads = 1;
+    uint16_t* xring = nullptr;           // [AG_RING][BMX_PLAN_MAXT][H] fp16, pinned host
+    uint16_t* xring_dev = nullptr;
+    float* cpu_part = nullptr;           // [AG_RING][BMX_PLAN_MAXT][H] fp32, pinned host
+    float* cpu_part_dev = nullptr;
+    std::vector<int64_t> job_of;         // [AG_RING]: the planned step whose request carried rows (a job follows)
+    std::thread cpu_th;
+    std::mutex cpu_mu;
+    std::condition_variable cpu_cv;
+    std::deque<bmx::CpuJob> cpu_q;
+    std::atomic<int64_t> cpu_jobs{0};
 };
 
 namespace bmx {
@@ -84,11 +115,208 @@ __global__ __launch_bounds__(64) void k_copy_wait(AgentShared* sh, int part, int
     }
 }
 
+// out[T][H] += the CPU lane's partial of step seq (ring slot seq % AG_RING), once the job is done (bounded wait by
+// thread 0 of each workgroup; nothing is added when the job had no picks or the wait ran out). Four values a thread.
+__global__ __launch_bounds__(256) void k_cpu_add(AgentShared* sh, const float* part, int64_t seq, float* out, int T,
+                                                 int H, int64_t limit)
+{
+    __shared__ int go;
+    if (threadIdx.x == 0)
+    {
+        go = 0;
+        const int64_t t0 = wall_clock64();
+        for (;;)
+        {
+            if (__hip_atomic_load(&sh->cpu_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= seq)
+            {
+                go = __hip_atomic_load(&sh->cpu_n[(int)((uint64_t)seq % AG_RING)], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM) > 0;
+                break;
+            }
+            if (__hip_atomic_load(&sh->flags[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
+                __hip_atomic_load(&sh->flags[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM))
+                break;
+            if (wall_clock64() - t0 > limit)
+            {
+                __hip_atomic_store(&sh->flags[3], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+    if (!go) return;
+    const float* p = part + (size_t)((uint64_t)seq % AG_RING) * BMX_PLAN_MAXT * H;
+    const int i = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (i >= T * H) return;
+    const float4 v = *reinterpret_cast<const float4*>(p + i);
+    float4 o = *reinterpret_cast<const float4*>(out + i);
+    o.x = o.x + v.x;
+    o.y = o.y + v.y;
+    o.z = o.z + v.z;
+    o.w = o.w + v.w;
+    *reinterpret_cast<float4*>(out + i) = o;
+}
+
 static void agent_fail(bmx_copy_agent* a, int code)
 {
     int z = 0;
     a->error.compare_exchange_strong(z, code);
     __atomic_store_n(&a->sh->flags[2], 1, __ATOMIC_RELEASE);
+}
+
+static float h2f_host(uint16_t h)
+{
+    const uint32_t sg = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t f;
+    if (e == 0 && m == 0) f = sg;
+    else if (e == 0)
+    {
+        int k = 0;                      // subnormal: m 2^-24, normalised
+        uint32_t mm = m;
+        while (!(mm & 0x400u)) { mm <<= 1; ++k; }
+        f = sg | ((uint32_t)(113 - k) << 23) | ((mm & 0x3ffu) << 13);
+    }
+    else if (e == 31) f = sg | 0x7f800000u | (m << 13);
+    else f = sg | ((e + 112) << 23) | (m << 13);
+    float r;
+    memcpy(&r, &f, 4);
+    return r;
+}
+
+// The planner (bmx_plan_policy): lanes of request r into p; the CPU picks of the call into job (when it carries rows).
+static void plan_reply(bmx_copy_agent* a, const PlanReq& r, PlanRep& p, CpuJob* job)
+{
+    bmx_plan_policy pol;
+    {
+        std::lock_guard<std::mutex> lk(a->plan_mu);
+        pol = a->policy;
+    }
+    const int nu = r.nu;
+    const bool cpu_ok = pol.cpu_on && a->cpu_ready && r.has_x && r.np <= BMX_PLAN_MAXP && r.ntok <= BMX_PLAN_MAXT;
+    int nres = 0;
+    std::vector<int> miss;
+    for (int u = 0; u < nu; ++u)
+    {
+        if (r.res[u]) { p.lane[u] = BMX_LANE_VRAM; ++nres; }
+        else miss.push_back(u);
+    }
+    std::stable_sort(miss.begin(), miss.end(), [&](int x, int y) {
+        return r.cnt[x] != r.cnt[y] ? r.cnt[x] > r.cnt[y] : r.ex[x] < r.ex[y];
+    });
+    double g = pol.gpu_base_us + pol.gpu_hit_us * nres, c = 0.0;
+    int ncpu = 0;
+    for (int u : miss)
+    {
+        const bool home = pol.home_single && r.ntok > 1 && r.cnt[u] == 1;
+        const double gc = home ? pol.gpu_home_us : pol.gpu_admit_us;
+        const double cc = (ncpu == 0 ? pol.cpu_base_us : 0.0) + pol.cpu_expert_us + pol.cpu_token_us * (r.cnt[u] - 1);
+        if (cpu_ok && ncpu < pol.max_cpu && std::max(c + cc, g) <= std::max(c, g + gc))
+        {
+            p.lane[u] = BMX_LANE_CPU;
+            c += cc;
+            ++ncpu;
+        }
+        else
+        {
+            p.lane[u] = home ? BMX_LANE_HOME : BMX_LANE_ADMIT;
+            g += gc;
+        }
+    }
+    p.ncpu = ncpu;
+    a->plans.fetch_add(1, std::memory_order_relaxed);
+    a->plan_cpu.fetch_add(ncpu, std::memory_order_relaxed);
+    if (!job) return;
+    job->li = r.li;
+    job->ntok = r.ntok;
+    job->topk = r.topk;
+    if (!ncpu) return;
+    for (int i = 0; i < r.np; ++i)
+    {
+        const int e = r.pe[i];
+        if (e < 0) continue;
+        const int32_t* f = std::lower_bound(r.ex, r.ex + nu, e);
+        if (f == r.ex + nu || *f != e || p.lane[f - r.ex] != BMX_LANE_CPU) continue;
+        job->pick_e.push_back(e);
+        job->pick_t.push_back(i / std::max(1, r.topk));
+        job->pick_w.push_back(h2f_host(r.pw[i]));
+    }
+}
+
+// The CPU-lane worker: jobs in sequence order; each CPU pick's y row (bit for bit the decode path's), summed w * y in
+// pick order into its token's partial, which goes to the ring slot of the job's step, then cpu_done = seq.
+static void cpu_loop(bmx_copy_agent* a)
+{
+    const int H = a->cpu_desc.H, I = a->cpu_desc.I, E = a->t.E;
+    std::vector<float> part, y;
+    for (;;)
+    {
+        CpuJob job;
+        {
+            std::unique_lock<std::mutex> lk(a->cpu_mu);
+            a->cpu_cv.wait(lk, [&] { return !a->cpu_q.empty() || a->stop.load(std::memory_order_acquire); });
+            if (a->cpu_q.empty()) return;
+            job = std::move(a->cpu_q.front());
+            a->cpu_q.pop_front();
+        }
+        const int slot = ring_index(job.seq), n = (int)job.pick_e.size();
+        bool ok = true;
+        if (n > 0)
+        {
+            int ks_gu = 0, ks_dn = 0, grouped = 0;
+            bmx_moe_desc d = a->cpu_desc;
+            ok = bmx_decode_splits(&d, job.ntok, &ks_gu, &ks_dn, &grouped) == BMX_OK;
+            part.assign((size_t)job.ntok * H, 0.0f);
+            y.resize(H);
+            for (int i = 0; ok && i < n; ++i)
+            {
+                const int e = job.pick_e[i], tt = job.pick_t[i];
+                if (job.li < 0 || job.li >= a->t.L || e < 0 || e >= E || tt < 0 || tt >= job.ntok) { ok = false; break; }
+                ok = bmx_cpu_expert_rows(&a->cpu_experts[(size_t)job.li * E + e], H, I, job.x.data() + (size_t)tt * H, 1,
+                                         ks_gu, ks_dn, grouped, d.act, d.gated, d.act_limit, y.data(),
+                                         a->cpu_threads) == BMX_OK;
+                for (int h = 0; ok && h < H; ++h)
+                {
+                    const float pr = job.pick_w[i] * y[h];
+                    part[(size_t)tt * H + h] = part[(size_t)tt * H + h] + pr;
+                }
+            }
+            if (ok) memcpy(a->cpu_part + (size_t)slot * BMX_PLAN_MAXT * H, part.data(), part.size() * 4);
+        }
+        if (!ok) agent_fail(a, BMX_ERR_ARG);
+        __atomic_store_n(&a->sh->cpu_n[slot], ok ? n : 0, __ATOMIC_RELAXED);
+        a->cpu_jobs.fetch_add(1, std::memory_order_relaxed);
+        __atomic_store_n(&a->sh->cpu_done, job.seq, __ATOMIC_RELEASE);
+    }
+}
+
+// Serve request seq: plan, queue its CPU job (every request that carried rows has one, in order), reply.
+static void serve_plan(bmx_copy_agent* a, int64_t seq)
+{
+    const PlanReq& r = a->sh->req[ring_index(seq)];
+    PlanRep& p = a->sh->rep[ring_index(seq)];
+    if (r.nu < 0 || r.nu > PL_MAXU || r.nu > a->t.E || r.np < 0 || r.ntok < 0 || r.topk <= 0 ||
+        (r.has_x && (r.ntok > BMX_PLAN_MAXT || r.np > BMX_PLAN_MAXP)))
+    {
+        agent_fail(a, BMX_ERR_ARG);
+        return;
+    }
+    const bool job = r.has_x && a->cpu_ready;
+    CpuJob cj;
+    cj.seq = seq;
+    plan_reply(a, r, p, job ? &cj : nullptr);
+    if (job)
+    {
+        const int H = a->cpu_desc.H;
+        const uint16_t* src = a->xring + (size_t)ring_index(seq) * BMX_PLAN_MAXT * H;
+        cj.x.assign(src, src + (size_t)r.ntok * H);      // the step's rows leave the ring before the reply
+        {
+            std::lock_guard<std::mutex> lk(a->cpu_mu);
+            a->cpu_q.push_back(std::move(cj));
+        }
+        a->cpu_cv.notify_one();
+    }
+    __atomic_store_n(&p.seq, seq, __ATOMIC_RELEASE);
 }
 
 // The agent thread: records in sequence order; per step record the gate / up copies under one signal, the down copies
@@ -126,9 +354,19 @@ static void agent_loop(bmx_copy_agent* a)
         a->copied_bytes.fetch_add(n, std::memory_order_relaxed);
     };
     auto last_work = std::chrono::steady_clock::now();
+    int64_t served = 0;                   // the last planned step's request answered
     for (;;)
     {
         bool idle = true;
+        // a planned step publishes its request under the sequence number of its record and waits for the reply before
+        // it publishes the record
+        if (served < next && !a->hold.load(std::memory_order_acquire) &&
+            __atomic_load_n(&a->sh->req[ring_index(next)].seq, __ATOMIC_ACQUIRE) == next)
+        {
+            serve_plan(a, next);
+            served = next;
+            idle = false;
+        }
         // retire completed parts in order
         while (!pending.empty())
         {
@@ -339,7 +577,15 @@ int bmx_copy_agent_destroy(bmx_copy_agent* a)
     if (!a) return BMX_OK;
     a->stop.store(true, std::memory_order_release);
     if (a->th.joinable()) a->th.join();
+    {
+        std::lock_guard<std::mutex> lk(a->cpu_mu);
+        a->cpu_q.clear();
+    }
+    a->cpu_cv.notify_all();
+    if (a->cpu_th.joinable()) a->cpu_th.join();
     const int err = a->error.load();
+    if (a->xring) (void)hipHostFree(a->xring);
+    if (a->cpu_part) (void)hipHostFree(a->cpu_part);
     if (a->sh) (void)hipHostFree(a->sh);
     if (a->need) (void)hipFree(a->need);
     if (a->hsa_up) hsa_shut_down();
@@ -410,6 +656,99 @@ int bmx_slot_prefetch_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, 
     a->next_seq = q;
     *seq = q;
     return BMX_OK;
+}
+
+int bmx_copy_agent_plan(bmx_copy_agent* a, const bmx_plan_policy* p)
+{
+    if (!a) return set_error(BMX_ERR_ARG, "bmx_copy_agent_plan: null agent");
+    bmx_plan_policy q{};
+    if (p)
+    {
+        q = *p;
+        if (q.max_cpu < 0 || q.gpu_base_us < 0 || q.gpu_hit_us < 0 || q.gpu_home_us < 0 || q.gpu_admit_us < 0 ||
+            q.cpu_base_us < 0 || q.cpu_expert_us < 0 || q.cpu_token_us < 0)
+            return set_error(BMX_ERR_ARG, "bmx_copy_agent_plan: negative count or cost");
+    }
+    std::lock_guard<std::mutex> lk(a->plan_mu);
+    a->policy = q;
+    return BMX_OK;
+}
+
+int bmx_copy_agent_cpu_lane(bmx_copy_agent* a, const bmx_moe_desc* desc, const bmx_cpu_expert* experts, int threads)
+{
+    if (!a || !desc || !experts) return set_error(BMX_ERR_ARG, "bmx_copy_agent_cpu_lane: null argument");
+    if (a->cpu_ready) return set_error(BMX_ERR_ARG, "bmx_copy_agent_cpu_lane: already set up");
+    if (desc->E != a->t.E || desc->H != a->t.H || desc->I != a->t.I || desc->H % 128 || desc->I % 128)
+        return set_error(BMX_ERR_ARG, "bmx_copy_agent_cpu_lane: the descriptor's shape is not the slot table's");
+    const size_t K = (size_t)a->t.L * a->t.E, n = (size_t)AG_RING * BMX_PLAN_MAXT * desc->H;
+    void *x = nullptr, *xd = nullptr, *pp = nullptr, *pd = nullptr;
+    if (hipHostMalloc(&x, n * 2, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess ||
+        hipHostGetDevicePointer(&xd, x, 0) != hipSuccess ||
+        hipHostMalloc(&pp, n * 4, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess ||
+        hipHostGetDevicePointer(&pd, pp, 0) != hipSuccess)
+    {
+        if (x) (void)hipHostFree(x);
+        if (pp) (void)hipHostFree(pp);
+        return set_error(BMX_ERR_HIP, "bmx_copy_agent_cpu_lane: pinned rings");
+    }
+    a->cpu_desc = *desc;
+    a->cpu_experts.assign(experts, experts + K);
+    a->cpu_threads = threads < 1 ? 1 : threads;
+    a->xring = static_cast<uint16_t*>(x);
+    a->xring_dev = static_cast<uint16_t*>(xd);
+    a->cpu_part = static_cast<float*>(pp);
+    a->cpu_part_dev = static_cast<float*>(pd);
+    a->job_of.assign(AG_RING, 0);
+    a->cpu_ready = true;
+    a->cpu_th = std::thread(cpu_loop, a);
+    return BMX_OK;
+}
+
+int bmx_slot_step_planned(const bmx_slot_table* t, bmx_copy_agent* a, int li, const int64_t* sel, const void* w_fp16,
+                          int T, int topk, int64_t first, int admit, const void* x_fp16, int64_t* sel_gpu, void* w_gpu,
+                          int32_t* lanes, int64_t* seq, bmx_stream_t stream)
+{
+    if (!a || !seq) return set_error(BMX_ERR_ARG, "bmx_slot_step_planned: null agent or seq");
+    if (li < 0 || li >= a->t.L) return set_error(BMX_ERR_ARG, "bmx_slot_step_planned: bad layer %d", li);
+    if (T < 0 || topk <= 0) return set_error(BMX_ERR_ARG, "bmx_slot_step_planned: bad T %d or topk %d", T, topk);
+    if (x_fp16 && (reinterpret_cast<uintptr_t>(x_fp16) & 15))
+        return set_error(BMX_ERR_ARG, "bmx_slot_step_planned: x must be 16-byte aligned");
+    int rc = agent_failure(a, "bmx_slot_step_planned");
+    if (rc) return rc;
+    const int n = T * topk;
+    const int64_t q = a->next_seq + 1;
+    PlanArgs pl;
+    pl.w = static_cast<const uint16_t*>(w_fp16);
+    pl.T = T;
+    pl.topk = topk;
+    pl.H = a->t.H;
+    const bool rows = a->cpu_ready && x_fp16 && T <= BMX_PLAN_MAXT && n <= BMX_PLAN_MAXP;
+    pl.x = rows ? static_cast<const uint16_t*>(x_fp16) : nullptr;
+    pl.xring = rows ? a->xring_dev : nullptr;
+    pl.sel_gpu = sel_gpu;
+    pl.w_gpu = static_cast<uint16_t*>(w_gpu);
+    pl.lanes = lanes;
+    rc = launch_slot_step(t, li, sel, n, first, admit, static_cast<hipStream_t>(stream), a->sh_dev, q, a->need,
+                          a->wait_ticks, &pl);
+    if (rc) return rc;
+    if (a->cpu_ready) a->job_of[ring_index(q)] = rows ? q : 0;
+    a->next_seq = q;
+    *seq = q;
+    return BMX_OK;
+}
+
+int bmx_cpu_lane_add(bmx_copy_agent* a, int64_t seq, float* out, int T, bmx_stream_t stream)
+{
+    if (!a || !out) return set_error(BMX_ERR_ARG, "bmx_cpu_lane_add: null agent or output");
+    if (seq <= 0 || seq > a->next_seq || seq <= a->next_seq - AG_RING || T < 0 || T > BMX_PLAN_MAXT)
+        return set_error(BMX_ERR_ARG, "bmx_cpu_lane_add: sequence number %lld is not one of the last %d steps, or T %d "
+                         "> %d", (long long)seq, AG_RING, T, BMX_PLAN_MAXT);
+    if (!a->cpu_ready || a->job_of[ring_index(seq)] != seq || T == 0) return BMX_OK;   // no CPU job for that step
+    if (reinterpret_cast<uintptr_t>(out) & 15) return set_error(BMX_ERR_ARG, "bmx_cpu_lane_add: out must be 16-byte aligned");
+    const unsigned wgs = (unsigned)(((size_t)T * a->t.H / 4 + 255) / 256);
+    hipLaunchKernelGGL(k_cpu_add, dim3(wgs), dim3(256), 0, static_cast<hipStream_t>(stream), a->sh_dev, a->cpu_part_dev,
+                       seq, out, T, a->t.H, a->wait_ticks);
+    return check_launch("bmx_cpu_lane_add");
 }
 
 int bmx_copy_wait(bmx_copy_agent* a, int64_t seq, int part, bmx_stream_t stream)

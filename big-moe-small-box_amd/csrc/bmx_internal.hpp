@@ -77,18 +77,50 @@ __host__ __device__ inline int ring_index(int64_t seq) { return (int)((uint64_t)
 // agent has read out of the ring (its slot may be written again by record consumed + AG_RING). Once flags[2] or
 // flags[3] is set, steps admit nothing (every expert they see runs from its home) and publish nothing, and the host
 // entry points of the agent report the failure.
+// A planned step's request (device -> host) and the planner's reply (host -> device), ring slot seq % AG_RING
+constexpr int PL_MAXU = 512;
+struct PlanReq {
+    int64_t seq;                    // written last (system-scope release)
+    int32_t li, nu, np, ntok, topk, has_x;
+    int32_t ex[PL_MAXU];            // unique local experts, ascending
+    int32_t res[PL_MAXU];           // 1: resident in a VRAM slot at publication
+    int32_t cnt[PL_MAXU];           // picks of each
+    int32_t pe[BMX_PLAN_MAXP];      // np <= BMX_PLAN_MAXP: local expert of each pick, -1 out of range
+    uint16_t pw[BMX_PLAN_MAXP];     // its fp16 weight
+};
+struct PlanRep {
+    int64_t seq;                    // written last
+    int32_t ncpu, pad;
+    int32_t lane[PL_MAXU];          // BMX_LANE_* of each unique expert
+};
 struct AgentShared {
     int64_t flags[4];
     int64_t consumed;
-    int64_t pad[3];
+    int64_t cpu_done;               // the last planned step whose CPU job has finished (jobs finish in sequence order)
+    int64_t pad[2];
     SlotPub ring[AG_RING];
+    PlanReq req[AG_RING];
+    PlanRep rep[AG_RING];
+    int32_t cpu_n[AG_RING];         // CPU picks of the job in that slot (0: nothing to add)
+};
+// A planned step (slots.hip): the request's extra inputs and the step's masked outputs. xring: device address of the
+// agent's input-row ring [AG_RING][BMX_PLAN_MAXT][H] fp16 in host memory.
+struct PlanArgs {
+    const uint16_t* w;
+    int T, topk, H;
+    const uint16_t* x;
+    uint16_t* xring;
+    int64_t* sel_gpu;
+    uint16_t* w_gpu;
+    int32_t* lanes;
 };
 // Publishing (sh != null): the step writes ring[seq % AG_RING] once the agent has consumed record seq - AG_RING, waiting
 // at most wait_limit wall-clock ticks (then it sets flags[3]). need (steps only): need[li] = the last record layer li's
 // next products depend on (seq when the step admitted experts, seq - 1 when it did not: its prefetched hits came with
 // earlier records)
 int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
-                     AgentShared* sh = nullptr, int64_t seq = 0, int64_t* need = nullptr, int64_t wait_limit = 0);
+                     AgentShared* sh = nullptr, int64_t seq = 0, int64_t* need = nullptr, int64_t wait_limit = 0,
+                     const PlanArgs* plan = nullptr);
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
                          hipStream_t s, AgentShared* sh = nullptr, int64_t seq = 0, int64_t wait_limit = 0);
 int launch_slot_copy(const bmx_slot_table* t, int li, int mats, int buf, hipStream_t s);

@@ -22,7 +22,9 @@ struct SlotArgs {
     AgentShared* sh;  // or null: the admissions are also published to the copy agent's ring under sequence number seq
     int64_t seq;
     int64_t* need;    // steps that publish: need[li] = the last record the layer's products depend on
-    int64_t wait_limit;   // wall-clock ticks a publish waits for its ring slot
+    int64_t wait_limit;   // wall-clock ticks a publish waits for its ring slot (and a planned step for its reply)
+    int plan;             // 1: a planned step (sh set): request, reply, lanes (PlanArgs)
+    PlanArgs pl;
 };
 
 __device__ __forceinline__ bool agent_failed(AgentShared* sh)
@@ -78,6 +80,105 @@ __device__ __forceinline__ int compact_flags(bool flag, int value, int32_t* out,
     return total;
 }
 
+// A planned step's request and reply, by the whole workgroup: the picked experts (mark) in ascending order into uq
+// with their residency and pick counts (ecnt), the picks and input rows when the call is small enough, published under
+// a.seq; then the bounded wait for the planner's reply and each expert's lane into elane (a resident expert is always a
+// hit; a lane value the step does not know runs the expert from its home). Returns 0 when the agent had failed or the
+// ring slot or the reply did not come in time (then every lane is VRAM or HOME and the step admits nothing).
+__device__ int plan_step(const SlotArgs& a, const uint32_t* mark, const int32_t* ecnt, int32_t* elane, int32_t* uq,
+                         int* wave_cnt, int* s_ok)
+{
+    const int tid = threadIdx.x, E = a.t.E;
+    const int32_t* slotof = a.t.slotof + (size_t)a.li * E;
+    const bool marked = tid < E && ((mark[tid >> 5] >> (tid & 31)) & 1u);
+    const int nu = compact_flags(marked, tid, uq, wave_cnt);
+    if (tid == 0) *s_ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
+    __syncthreads();
+    PlanReq* rq = &a.sh->req[ring_index(a.seq)];
+    const PlanArgs& pl = a.pl;
+    const bool picks = a.n <= BMX_PLAN_MAXP;
+    const bool has_x = picks && pl.x && pl.xring && pl.T <= BMX_PLAN_MAXT;
+    if (*s_ok)
+    {
+        for (int u = tid; u < nu; u += SL_THREADS)
+        {
+            const int e = uq[u];
+            rq->ex[u] = e;
+            rq->res[u] = slotof[e] >= 0 ? 1 : 0;
+            rq->cnt[u] = ecnt[e];
+        }
+        if (picks)
+            for (int i = tid; i < a.n; i += SL_THREADS)
+            {
+                const int64_t e = a.sel[i] - a.first;
+                rq->pe[i] = (e >= 0 && e < E) ? (int32_t)e : -1;
+                rq->pw[i] = pl.w[i];
+            }
+        if (has_x)
+        {
+            const size_t n16 = (size_t)pl.T * pl.H / 8;
+            const u32x4* src = reinterpret_cast<const u32x4*>(pl.x);
+            u32x4* dst = reinterpret_cast<u32x4*>(pl.xring + (size_t)ring_index(a.seq) * BMX_PLAN_MAXT * pl.H);
+            for (size_t i = tid; i < n16; i += SL_THREADS) dst[i] = src[i];
+        }
+        if (tid == 0)
+        {
+            rq->li = a.li;
+            rq->nu = nu;
+            rq->np = a.n;
+            rq->ntok = pl.T;
+            rq->topk = pl.topk;
+            rq->has_x = has_x ? 1 : 0;
+        }
+        __threadfence_system();          // this thread's writes to host memory, before the barrier and the publish
+    }
+    __syncthreads();
+    if (tid == 0 && *s_ok)
+    {
+        __hip_atomic_store(&rq->seq, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        const PlanRep* rp = &a.sh->rep[ring_index(a.seq)];
+        const int64_t t0 = wall_clock64();
+        for (;;)
+        {
+            if (__hip_atomic_load(&rp->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) == a.seq) break;
+            if (agent_failed(a.sh))
+            {
+                *s_ok = 0;
+                break;
+            }
+            if (wall_clock64() - t0 > a.wait_limit)
+            {
+                __hip_atomic_store(&a.sh->flags[3], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                *s_ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+    const int ok = *s_ok;
+    const PlanRep* rp = &a.sh->rep[ring_index(a.seq)];
+    for (int u = tid; u < nu; u += SL_THREADS)
+    {
+        const int e = uq[u];
+        int ln = ok ? __hip_atomic_load(&rp->lane[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : BMX_LANE_HOME;
+        if (slotof[e] >= 0) ln = BMX_LANE_VRAM;
+        else if (ln != BMX_LANE_ADMIT && ln != BMX_LANE_CPU) ln = BMX_LANE_HOME;
+        elane[e] = ln;
+    }
+    __syncthreads();
+    for (int i = tid; i < a.n; i += SL_THREADS)
+    {
+        const int64_t e = a.sel[i] - a.first;
+        const int ln = (e >= 0 && e < E) ? elane[e] : -1;
+        const bool cpu = ln == BMX_LANE_CPU;
+        pl.sel_gpu[i] = cpu ? -1 : a.sel[i];
+        pl.w_gpu[i] = cpu ? (uint16_t)0 : pl.w[i];
+        if (pl.lanes) pl.lanes[i] = ln;
+    }
+    return ok;
+}
+
 __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
 {
     __shared__ int32_t pin[SL_MAXS];
@@ -86,7 +187,10 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     __shared__ int32_t miss[512];
     __shared__ int32_t first_at[512];
     __shared__ int wave_cnt[SL_THREADS / 64];
-    __shared__ int n_hit, n_pfused;
+    __shared__ int n_hit, n_pfused, n_missall, s_ok;
+    __shared__ int32_t ecnt[512];        // planned step: picks per expert
+    __shared__ int32_t elane[512];       // planned step: lane per expert
+    __shared__ int32_t uq[512];          // planned step: the picked experts, ascending
     const bmx_slot_table& t = a.t;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int S = t.S, E = t.E;
@@ -97,8 +201,13 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
         refb[s] = t.refb[s];
     }
     if (tid < 16) mark[tid] = 0;
-    if (tid < E) first_at[tid] = INT32_MAX;
-    if (tid == 0) n_hit = n_pfused = 0;
+    if (tid < E)
+    {
+        first_at[tid] = INT32_MAX;
+        ecnt[tid] = 0;
+        elane[tid] = BMX_LANE_VRAM;
+    }
+    if (tid == 0) n_hit = n_pfused = n_missall = 0;
     __syncthreads();
     int32_t* slotof = t.slotof + (size_t)a.li * E;
     int nmiss;
@@ -107,9 +216,15 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
         for (int i = tid; i < a.n; i += SL_THREADS)
         {
             const int64_t e = a.sel[i] - a.first;
-            if (e >= 0 && e < E) atomicOr(&mark[e >> 5], 1u << (e & 31));
+            if (e >= 0 && e < E)
+            {
+                atomicOr(&mark[e >> 5], 1u << (e & 31));
+                if (a.plan) atomicAdd(&ecnt[e], 1);
+            }
         }
         __syncthreads();
+        // a planned step: the planner's lanes (a miss is admitted only in BMX_LANE_ADMIT)
+        if (a.plan) plan_step(a, mark, ecnt, elane, uq, wave_cnt, &s_ok);
         // hits: reference bit, pinned for this step (the first use of a prefetched slot counts and marks the expert
         // fresh: its copy may still be in flight); misses: compacted in ascending expert order
         const int e = tid;
@@ -132,7 +247,11 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                         atomicAdd(&n_pfused, 1);
                     }
                 }
-                else is_miss = true;
+                else
+                {
+                    is_miss = !a.plan || elane[e] == BMX_LANE_ADMIT;
+                    atomicAdd(&n_missall, 1);
+                }
             }
             t.fresh[e] = fr;
         }
@@ -166,7 +285,8 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
             // a failed agent (aborted, or a wait ran out of time) copies nothing more: admit nothing, so every expert
             // this step sees runs from its home, and publish nothing
             int ok = 0;
-            if (lane == 0) ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
+            if (a.plan) ok = s_ok;           // the planned step has waited for its ring slot and its reply
+            else if (lane == 0) ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
             if (__shfl(ok, 0)) pub = &a.sh->ring[ring_index(a.seq)];
             else admit = 0;
         }
@@ -262,7 +382,7 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
                 t.ctl[1] = epoch;
                 t.ctl[2] = nj;
                 t.stats[0] += n_hit;
-                t.stats[1] += nmiss;
+                t.stats[1] += n_missall;
                 t.stats[2] += nj;
                 t.stats[3] += novictim;
                 t.stats[6] += n_pfused;
@@ -328,7 +448,7 @@ static int check_table(const bmx_slot_table* t, const char* who)
 }
 
 int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int admit, hipStream_t s,
-                     AgentShared* sh, int64_t seq, int64_t* need, int64_t wait_limit)
+                     AgentShared* sh, int64_t seq, int64_t* need, int64_t wait_limit, const PlanArgs* plan)
 {
     int rc = check_table(t, "bmx_slot_step");
     if (rc) return rc;
@@ -347,8 +467,18 @@ int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n,
     a.seq = seq;
     a.need = need;
     a.wait_limit = wait_limit;
+    a.plan = 0;
+    a.pl = PlanArgs{};
+    if (plan)
+    {
+        if (!sh) return set_error(BMX_ERR_ARG, "planned step without an agent");
+        if (!plan->w || !plan->sel_gpu || !plan->w_gpu || plan->T < 0 || plan->topk <= 0)
+            return set_error(BMX_ERR_ARG, "bmx_slot_step_planned: null weights or outputs, or bad T / topk");
+        a.plan = 1;
+        a.pl = *plan;
+    }
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
-    return check_launch("bmx_slot_step");
+    return check_launch(plan ? "bmx_slot_step_planned" : "bmx_slot_step");
 }
 
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,
@@ -373,6 +503,8 @@ int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, in
     a.seq = seq;
     a.need = nullptr;
     a.wait_limit = wait_limit;
+    a.plan = 0;
+    a.pl = PlanArgs{};
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
     return check_launch("bmx_slot_prefetch");
 }

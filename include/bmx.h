@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define BMX_ABI_VERSION 3
+#define BMX_ABI_VERSION 4
 
 typedef void* bmx_stream_t; /* hipStream_t */
 
@@ -332,6 +332,54 @@ int bmx_decode_splits(const bmx_moe_desc* desc, int T, int* ks_gu, int* ks_dn, i
  * v_dot2_f32_f16 on the host; bmx_dot2_f32_f16 runs the instruction (device arrays), to check the emulation. */
 int bmx_cpu_dot2(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n);
 int bmx_dot2_f32_f16(const uint32_t* a, const uint32_t* b, const float* c, float* out, int n, bmx_stream_t stream);
+
+/* ---- residency plan: request, reply, CPU lane ----
+ * The reference's controller protocol (engine/kernels/nv2/nv2_shared.h:36-59 Req / Rep, nv2_dev.cu:23-95 publish and
+ * :221-367 nv_step_k reading the reply, nv2_host.cpp:947-1133 plan_and_reply / serve, :1306-1445 the CPU job). A planned
+ * step publishes its layer call to the copy agent as a request: the unique experts it picks (ascending), whether each is
+ * resident in a VRAM slot, how many picks each has, and for calls of at most BMX_PLAN_MAXP picks the picks themselves
+ * (expert, fp16 weight) and, given x, the input rows of up to BMX_PLAN_MAXT tokens. The agent's thread answers each
+ * request in sequence order with a lane per unique expert (bmx_plan_policy); the step waits for the reply (bounded by
+ * the agent's wait limit; running out of it is the agent failure bmx_copy_agent_status reports, after which the step
+ * admits nothing) and applies it:
+ *   BMX_LANE_VRAM   resident: a hit (the planner never moves a resident expert)
+ *   BMX_LANE_ADMIT  admitted to a slot by the CLOCK step and copied by the agent (at most maxj per step, as
+ *                   bmx_slot_step; one that finds no slot runs from its home)
+ *   BMX_LANE_HOME   computed by the GPU from its home (the expert kernels read pinned host memory), not admitted
+ *   BMX_LANE_CPU    masked out of the GPU's selection (sel_gpu -1, w_gpu 0) and computed by the agent's CPU lane
+ * sel_gpu / w_gpu [n]: the selection the GPU computes (the others' picks as given); lanes [n] (or NULL): each pick's
+ * lane, -1 for ids outside [first, first + E). */
+#define BMX_PLAN_MAXP 64
+#define BMX_PLAN_MAXT 8
+enum { BMX_LANE_VRAM = 0, BMX_LANE_ADMIT = 1, BMX_LANE_HOME = 2, BMX_LANE_CPU = 3 };
+/* The planner: list scheduling of a call's non-resident experts onto two lanes by estimated finish time (the
+ * reference's rule, nv2_host.cpp:1030-1041). The GPU's time starts at gpu_base_us + gpu_hit_us per resident expert, the
+ * CPU lane's at 0. The experts not resident are taken by picks descending, then expert ascending; each costs the GPU
+ * gpu_admit_us (gpu_home_us when home_single is set, the call has several tokens and only one picked the expert: run
+ * from the home rather than take a slot for one read) and the CPU lane cpu_expert_us + cpu_token_us per pick beyond the
+ * first, plus cpu_base_us for the lane's first expert of the call; it goes to the CPU lane when cpu_on, fewer than
+ * max_cpu are there already, the call's picks and rows travel with the request and the later of the two finish times
+ * is then no later than with the GPU taking it; else to the GPU (BMX_LANE_HOME or BMX_LANE_ADMIT). Default (no policy
+ * set): cpu_on 0, home_single 0, every miss BMX_LANE_ADMIT. */
+typedef struct bmx_plan_policy {
+    int32_t cpu_on, max_cpu, home_single, reserved;
+    double gpu_base_us, gpu_hit_us, gpu_home_us, gpu_admit_us;
+    double cpu_base_us, cpu_expert_us, cpu_token_us;
+} bmx_plan_policy;
+int bmx_copy_agent_plan(bmx_copy_agent* agent, const bmx_plan_policy* policy);
+/* The CPU lane of an agent: experts[L * E] host copies of every layer's experts (trellis, scales, formats; the shared
+ * expert never goes to the CPU), desc: the layers' shape and activation (experts, shared and fresh ignored), threads:
+ * worker threads per job. Without it the planner puts nothing on the CPU lane. A job computes each CPU pick's y row of
+ * its token with bmx_cpu_expert_rows (bit for bit the GPU decode path's row for the call's T) and sums w * y in pick
+ * order into the token's partial (fp32 [T][H]). */
+int bmx_copy_agent_cpu_lane(bmx_copy_agent* agent, const bmx_moe_desc* desc, const bmx_cpu_expert* experts, int threads);
+int bmx_slot_step_planned(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const int64_t* sel,
+                          const void* w_fp16, int T, int topk, int64_t first, int admit, const void* x_fp16,
+                          int64_t* sel_gpu, void* w_gpu, int32_t* lanes, int64_t* seq, bmx_stream_t stream);
+/* out[T][H] += the CPU lane's partial of planned step seq (after its combine, the reference's nv_combine_k add,
+ * nv2_dev.cu:513-551): waits (bounded, as the copy waits) for the agent's CPU job of seq; adds nothing when the plan put
+ * no pick on the CPU. Enqueue it before the 64th step after seq. */
+int bmx_cpu_lane_add(bmx_copy_agent* agent, int64_t seq, float* out, int T, bmx_stream_t stream);
 
 /* Host-planned staging: n copies src[i] -> dst[i] of bytes[i] (hipMemcpyAsync, e.g. pinned host -> slot), in order on
  * stream (the reference's stage_layer, engine/kernels/nv2/nv2_host.cpp:1558-1593). */

@@ -676,6 +676,14 @@ static int clock_admit(bmxo_slots* t, int li, const int* miss, int nmiss, int ma
 int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int admit, int maxj, int32_t* jobs,
                    int32_t* evicted, int32_t* fresh, int64_t* stats)
 {
+    return bmxo_slot_step_lanes(t, li, sel, n, first, admit, maxj, NULL, jobs, evicted, fresh, stats);
+}
+
+/* A planned step (include/bmx.h bmx_slot_step_planned): elane[E] (or NULL: every miss admitted) is each expert's lane;
+ * a miss joins the admissions only in lane 1 (admit); every miss counts in stats[1]. */
+int bmxo_slot_step_lanes(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int admit, int maxj,
+                         const int32_t* elane, int32_t* jobs, int32_t* evicted, int32_t* fresh, int64_t* stats)
+{
     const int E = t->E, S = t->S;
     unsigned char* mark = (unsigned char*)calloc((size_t)E, 1);
     int* miss = (int*)malloc((size_t)E * sizeof(int));
@@ -686,7 +694,7 @@ int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t fir
         const int64_t e = sel[i] - first;
         if (e >= 0 && e < E) mark[e] = 1;
     }
-    int nhit = 0, nmiss = 0, nj = 0;
+    int nhit = 0, nmiss = 0, nmiss_all = 0, nj = 0;
     int32_t* slotof = t->slotof + (size_t)li * E;
     for (int e = 0; e < E; ++e)
     {
@@ -704,10 +712,14 @@ int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t fir
                 if (fresh) fresh[e] = 1;
             }
         }
-        else miss[nmiss++] = e;
+        else
+        {
+            ++nmiss_all;
+            if (!elane || elane[e] == 1) miss[nmiss++] = e;
+        }
     }
     stats[0] += nhit;
-    stats[1] += nmiss;
+    stats[1] += nmiss_all;
     if (admit && S > 0) nj = clock_admit(t, li, miss, nmiss, maxj, epoch, 0, jobs, evicted, fresh, stats);
     free(mark);
     free(miss);

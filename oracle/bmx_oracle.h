@@ -100,6 +100,8 @@ typedef struct {
  * stats[0..7] += hits, misses, admitted, no_victim, evictions, (prefetch:) admitted, used, evicted unused */
 int bmxo_slot_step(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int admit, int maxj, int32_t* jobs,
                    int32_t* evicted, int32_t* fresh, int64_t* stats);
+int bmxo_slot_step_lanes(bmxo_slots* t, int li, const int64_t* sel, int n, int64_t first, int admit, int maxj,
+                         const int32_t* elane, int32_t* jobs, int32_t* evicted, int32_t* fresh, int64_t* stats);
 /* layer-ahead prefetch into layer li's slots: the first `limit` distinct in-range picks of sel[n] (rank order) that are
  * not resident are admitted in that order, at most maxj, within the current epoch (slots pinned by the last step stay
  * pinned; the epoch does not advance) by a gentle CLOCK sweep: the first enabled, unpinned slot from the hand whose

@@ -70,6 +70,8 @@ def lib():
         L.bmxo_dispatch.restype = _I
         L.bmxo_slot_step.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _I, _I, _P, _P, _P, _P]
         L.bmxo_slot_step.restype = _I
+        L.bmxo_slot_step_lanes.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _I, _I, _P, _P, _P, _P, _P]
+        L.bmxo_slot_step_lanes.restype = _I
         L.bmxo_slot_prefetch.argtypes = [_P, _I, _P, _I, ctypes.c_int64, _I, _I, _P, _P, _P]
         L.bmxo_slot_prefetch.restype = _I
         _lib = L
@@ -238,14 +240,29 @@ class SlotTable:
     def epoch(self):
         return self._s.epoch
 
-    def step(self, li, sel, first=0, admit=True, maxj=1024):
-        """Returns (jobs [nj, 2] = (expert, slot), evicted owners [nj]); self.fresh is the step's fresh flags."""
+    def step(self, li, sel, first=0, admit=True, maxj=1024, elane=None):
+        """Returns (jobs [nj, 2] = (expert, slot), evicted owners [nj]); self.fresh is the step's fresh flags.
+        elane: int32 [E] lane of each expert (a planned step: only LANE_ADMIT misses are admitted) or None."""
         sel = _c(sel, np.int64).ravel()
         jobs = np.zeros(2 * maxj, np.int32)
         ev = np.zeros(maxj, np.int32)
-        nj = lib().bmxo_slot_step(ctypes.byref(self._s), li, _p(sel), sel.size, first, int(admit), maxj, _p(jobs),
-                                  _p(ev), _p(self.fresh), _p(self.stats))
+        if elane is None:
+            nj = lib().bmxo_slot_step(ctypes.byref(self._s), li, _p(sel), sel.size, first, int(admit), maxj, _p(jobs),
+                                      _p(ev), _p(self.fresh), _p(self.stats))
+        else:
+            el = _c(elane, np.int32)
+            nj = lib().bmxo_slot_step_lanes(ctypes.byref(self._s), li, _p(sel), sel.size, first, int(admit), maxj,
+                                            _p(el), _p(jobs), _p(ev), _p(self.fresh), _p(self.stats))
         return jobs[:2 * nj].reshape(nj, 2), ev[:nj]
+
+    def request(self, li, sel, first=0):
+        """What a planned step of these picks publishes: (unique local experts ascending, resident flags, pick
+        counts)."""
+        sel = _c(sel, np.int64).ravel() - first
+        sel = sel[(sel >= 0) & (sel < self.E)]
+        ex, cnt = np.unique(sel, return_counts=True)
+        res = (self.slotof[li * self.E + ex] >= 0).astype(np.int32)
+        return ex.astype(np.int32), res, cnt.astype(np.int32)
 
     def prefetch(self, li, sel, first=0, limit=1 << 30, maxj=1024):
         sel = _c(sel, np.int64).ravel()
@@ -254,6 +271,58 @@ class SlotTable:
         nj = lib().bmxo_slot_prefetch(ctypes.byref(self._s), li, _p(sel), sel.size, first, min(limit, 1 << 30), maxj,
                                       _p(jobs), _p(ev), _p(self.stats))
         return jobs[:2 * nj].reshape(nj, 2), ev[:nj]
+
+
+# ---- residency plan (a planned step's reply) ------------------------------------------------------------------------
+LANE_VRAM, LANE_ADMIT, LANE_HOME, LANE_CPU = 0, 1, 2, 3
+PLAN_MAXP, PLAN_MAXT = 64, 8
+PLAN_DEFAULT = dict(cpu_on=0, max_cpu=0, home_single=0, gpu_base_us=0.0, gpu_hit_us=0.0, gpu_home_us=0.0,
+                    gpu_admit_us=0.0, cpu_base_us=0.0, cpu_expert_us=0.0, cpu_token_us=0.0)
+
+
+def plan_lanes(ex, res, cnt, ntok, npicks, rows, policy=None, cpu_ready=True):
+    """The planner's lanes for a request (include/bmx.h bmx_plan_policy; the reference's two-lane rule,
+    engine/kernels/nv2/nv2_host.cpp:1030-1041): residents LANE_VRAM; the rest by picks descending then expert
+    ascending, each to the CPU lane when that keeps the later of the two estimated finish times no later than the GPU
+    taking it (and the lane is on, not full, and the call's picks and rows came with the request), else to the GPU
+    (LANE_HOME for a single-pick expert of a multi-token call under home_single, else LANE_ADMIT). rows: the request
+    carried the call's input rows."""
+    p = dict(PLAN_DEFAULT, **(policy or {}))
+    lanes = np.full(len(ex), LANE_VRAM, np.int32)
+    cpu_ok = bool(p["cpu_on"]) and cpu_ready and rows and npicks <= PLAN_MAXP and ntok <= PLAN_MAXT
+    g = p["gpu_base_us"] + p["gpu_hit_us"] * int(np.sum(res != 0))
+    c, ncpu = 0.0, 0
+    for u in sorted((u for u in range(len(ex)) if not res[u]), key=lambda u: (-int(cnt[u]), int(ex[u]))):
+        home = bool(p["home_single"]) and ntok > 1 and cnt[u] == 1
+        gc = p["gpu_home_us"] if home else p["gpu_admit_us"]
+        cc = (p["cpu_base_us"] if ncpu == 0 else 0.0) + p["cpu_expert_us"] + p["cpu_token_us"] * (int(cnt[u]) - 1)
+        if cpu_ok and ncpu < p["max_cpu"] and max(c + cc, g) <= max(c, g + gc):
+            lanes[u] = LANE_CPU
+            c += cc
+            ncpu += 1
+        else:
+            lanes[u] = LANE_HOME if home else LANE_ADMIT
+            g += gc
+    return lanes
+
+
+def expert_lanes(E, ex, lanes):
+    """[E] lane per local expert (LANE_VRAM for the ones not picked)"""
+    el = np.full(E, LANE_VRAM, np.int32)
+    el[np.asarray(ex, np.int64)] = lanes
+    return el
+
+
+def planned_selection(sel, w, first, elane):
+    """(sel_gpu, w_gpu, lanes) of a planned step: CPU-lane picks masked (-1, weight 0); lanes -1 out of range."""
+    sel = np.asarray(sel, np.int64).ravel()
+    w = np.asarray(w, np.float16).ravel()
+    E = len(elane)
+    e = sel - first
+    inr = (e >= 0) & (e < E)
+    ln = np.where(inr, elane[np.clip(e, 0, E - 1)], -1).astype(np.int32)
+    cpu = ln == LANE_CPU
+    return np.where(cpu, -1, sel), np.where(cpu, np.float16(0), w), ln
 
 
 def sqrtsp32(x):
