@@ -521,11 +521,12 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         n_cpu = T if T <= 64 else 64
         cpu = cpu_baseline(tabs[0], sels[0][:n_cpu], ws_[0][:n_cpu])
     kind = "prefill" if prefill else "mid" if mid else "decode"
-    traffic = traffic_src = None
+    traffic = traffic_src = prof_us = None
     tpath = os.path.join(REPO, "profiles", f"{kind}_{cfg}_t{T}.json")
     if os.path.exists(tpath):
         tr = json.load(open(tpath))
         traffic = tr["read_bytes"] + tr["write_bytes"]
+        prof_us = tr.get("kernel_us_avg")
         traffic_src = (f"loaded from the committed profiles/{kind}_{cfg}_t{T}.json ({tr.get('measured', 'date not recorded')}"
                        f"; command in profiles/{kind}_{cfg}_t{T}.md): rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the "
                        f"same workload, scaled by a plain copy's counters; not measured in this run")
@@ -536,15 +537,23 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         roofline = {"kernel": kern, "bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(ach / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": traffic,
                     "algorithmic_flops": gu_flops, "kernel_us": round(gu_ms * 1e3, 3), "traffic_source": traffic_src,
-                    "timing": "mean event-timed duration of the gate/up stage (one kernel launch) over the timed steps"}
+                    "timing": "achieved uses the mean event-timed duration of the gate/up stage (one kernel launch) over "
+                              "the timed steps; kernel_us_rocprof is the committed trace's average for the same leg"}
+        if prof_us:
+            roofline.update(kernel_us_rocprof=prof_us,
+                            frac_rocprof=round(gu_flops / (prof_us * 1e-6) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4))
     else:
         gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
         roofline = {"kernel": "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)",
                     "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "algorithmic_bytes": round(gu_bytes),
                     "kernel_us": round(gu_ms * 1e3, 3), "traffic_source": traffic_src,
-                    "timing": "mean event-timed duration of the gate/up stage (one kernel launch) over the timed steps, "
-                              "each step on other experts"}
+                    "timing": "achieved uses the mean event-timed duration of the gate/up stage (one kernel launch) over "
+                              "the timed steps, each step on other experts; kernel_us_rocprof is the committed trace's "
+                              "average for the same leg (no event records around the kernel)"}
+        if prof_us:
+            roofline.update(kernel_us_rocprof=prof_us,
+                            frac_rocprof=round(gu_bytes / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4))
     scores = {0: "softmax", 1: "sigmoid"}[c["score"]] + ("+bias" if c["bias"] else "")
     if c["n_group"] > 1:
         scores = f"group-limited ({c['n_group']} groups, top-{c['topk_group']}) {scores}"
