@@ -80,7 +80,7 @@ class MoELayer:
             return sel, w, False
         if getattr(self.slots, "planned", False):
             sel_gpu, w_gpu, _, seq = self.slots.step_planned(li, sel, w, z, True, first=self.routing_first)
-            if z is not None and bsz <= L.PLAN_MAXT and sel.numel() <= L.PLAN_MAXP:
+            if self.slots.cpu_ready and z is not None and bsz <= L.PLAN_MAXT and sel.numel() <= L.PLAN_MAXP:
                 self._cpu_seq = seq
             return sel_gpu.view(sel.shape), w_gpu.view(w.shape), self._cpu_seq is not None
         self.slots.step(li, sel, True, first=self.routing_first)

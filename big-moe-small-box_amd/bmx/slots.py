@@ -65,6 +65,7 @@ class ExpertSlots:
         self.agent = None
         self.seq = [0] * self.L               # dma: sequence number of each layer's last step
         self.planned = False                  # dma: layer calls use planned steps (plan())
+        self.cpu_ready = False                # dma: the agent has a CPU lane (cpu_lane())
         if copies == "dma":
             homes = (ctypes.c_uint64 * (self.L * self.E))(*[t.addr[e][0] for t in layers for e in range(t.E)])
             nb = (ctypes.c_int64 * (self.L * self.E * 3))(*[t.mat_bytes(e, m) for t in layers for e in range(t.E)
@@ -220,6 +221,7 @@ class ExpertSlots:
         d = self.layers[0].desc(topk, self.first, act, gated, act_limit)
         L.check(L.lib().bmx_copy_agent_cpu_lane(self.agent, ctypes.byref(d), exps, int(threads)),
                 "bmx_copy_agent_cpu_lane")
+        self.cpu_ready = True
 
     def step_planned(self, li, sel, w, x=None, admit=True, *, first=None):
         """A planned step of layer li (bmx_slot_step_planned): publishes the call to the agent's planner, waits for its

@@ -7,7 +7,10 @@ pinned homes) stand in for the 43: every layer of the stack runs the same code o
 Checks, for every token: each layer's output is bit-identical to the same layer with every expert resident in device
 memory, and the slot table's state (slot of every expert, owners, reference bits, pins, CLOCK hand, step counter,
 counters, fresh flags, every expert-table pointer) is bit-exact against the oracle's CLOCK table replaying the same picks
-(the reference's Pool.step / ec_step_k semantics, engine/tiers.py:360-373 and engine/ec.py:16-105)."""
+(the reference's Pool.step / ec_step_k semantics, engine/tiers.py:360-373 and engine/ec.py:16-105). The planned variant
+runs every step as a request answered by the copy agent's planner (its default policy: every miss admitted), the
+reference's publish / reply protocol (engine/kernels/nv2/nv2_dev.cu:221-367, nv2_host.cpp:947-1133), with the same
+checks."""
 import numpy as np
 import pytest
 import torch
@@ -21,7 +24,8 @@ def say(*a):
     print(*a, flush=True)
 
 
-def test_c4_stack_staged_matches_resident(cuda, oracle):
+@pytest.mark.parametrize("planned", [False, True])
+def test_c4_stack_staged_matches_resident(cuda, oracle, planned):
     import bmx
     from bmx import synth
     c = synth.CONFIGS["c4"]
@@ -54,7 +58,9 @@ def test_c4_stack_staged_matches_resident(cuda, oracle):
         for i in range(0, len(top), maxj):
             ref.step(li, np.array(top[i:i + maxj], np.int64), 0, True, maxj)
     check_state(slots, ref, ref.fresh.copy(), "warm")
-    say("c4 stack: warmed, stats", slots.stats())
+    say("c4 stack: warmed, stats", slots.stats(), "planned" if planned else "")
+    if planned:
+        slots.plan(None)
     lgs = [synth.zipf_logits(NTOK, E, 1.1, seed=li, perm_seed=7919 * (li + 1)) for li in range(NL)]
     for tok in range(NTOK):
         for li in range(NL):
@@ -63,11 +69,12 @@ def test_c4_stack_staged_matches_resident(cuda, oracle):
             sel, w = rf[li].routing_fn(1, None, x, {"logits": lg})
             want = rf[li].run_bszN(x, sel, w)
             sel2, w2 = st[li].routing_fn(1, None, x, {"logits": lg})
-            st[li].layer(li, sel2, w2, x, 1)
-            got = st[li].run_bszN(x, sel2, w2)
+            sel3, w3, _ = st[li].layer(li, sel2, w2, x, 1)
+            got = st[li].combine(st[li].run_bszN(x, sel3, w3))
             ref.step(li, sel2.cpu().numpy(), 0, True, maxj)
             torch.cuda.synchronize()
             assert torch.equal(sel, sel2) and torch.equal(w, w2), (tok, li)
+            assert torch.equal(sel3, sel2) and torch.equal(w3, w2), (tok, li)
             assert torch.equal(got, want), (tok, li)
         check_state(slots, ref, ref.fresh.copy(), f"token {tok}")
         if tok % 12 == 11:
