@@ -7,6 +7,7 @@ Names and argument meaning follow the reference:
   run_bszN(z, sel, rw) -> out [bsz, H] fp32                                     exllamav3 bc.run_bszN, engine/nv2.py:634
   cpu_split_combine(fhs, cpu_partial, cpu_pending, shape) -> fhs                engine/tiers.py:730-739
   combine(fhs) -> fhs                                                           engine/nv2.py:489-493 (Nv2.combine)
+  run_single_expert(y, e, x), run_single_expert_dq                             engine/tiers.py:597-605
 Every call enqueues on torch's current stream; nothing synchronises the host (verify_on_cpu, a host-side check with
 the exact CPU lane, excepted).
 """
@@ -134,6 +135,36 @@ class MoELayer:
         stage(L.STAGE_COMBINE)
         self._routes = routes
         return out
+
+    # ---- single-expert paths ----
+    def run_single_expert(self, y, e, x, path=L.PATH_AUTO):
+        """Expert e (local id) on the rows x (fp16 [n, H]): its down output after svh (what the combine weights) into
+        y (fp32 [n, H]), through the routed layer's kernels with every row routed to e alone (top-1, weight 1, no
+        shared expert). exllamav3's BlockSparseMLP run_single_expert, which the reference wraps
+        (engine/tiers.py:602-605) to copy the expert's bytes into its bounce slot first; here the expert table already
+        points at the expert's slot or home. Returns y."""
+        x = x.view(-1, self.hidden_size)
+        if x.dtype != torch.float16 or not x.is_contiguous():
+            x = x.half().contiguous()
+        n, E = x.shape[0], self.num_local_experts
+        if not 0 <= int(e) < E:
+            raise ValueError(f"run_single_expert: expert {e} outside [0, {E})")
+        if tuple(y.shape) != (n, self.hidden_size) or y.dtype != torch.float32:
+            raise ValueError("run_single_expert: y must be fp32 [n, H]")
+        if n == 0:
+            return y
+        sel = torch.full((n, 1), int(e) + self.routing_first, dtype=torch.int64, device=x.device)
+        desc = self.table.desc(1, self.routing_first, self.act, self.gated, self.act_limit)
+        desc.shared = None
+        routes = ops.dispatch(sel, E, self.routing_first, False, L.lib().bmx_rows_per_group(n, 1, path))
+        rows, _ = ops.moe_experts(desc, x, routes, path)
+        y.copy_(rows[:n])            # one expert: its rows are the tokens in order
+        return y
+
+    def run_single_expert_dq(self, y, e, x, path=L.PATH_AUTO):
+        """The reference's other per-expert entry (engine/tiers.py:597-600: exllamav3 reconstructs the expert's fp16
+        weights first). The trellis kernels compute the same products without a reconstructed copy: run_single_expert."""
+        return self.run_single_expert(y, e, x, path)
 
     def verify_on_cpu(self, z, sel, rw, threads=16, y_rows=None):
         """Recompute every expert row of a decode-path call on the host with the exact CPU lane and compare it with the

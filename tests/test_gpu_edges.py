@@ -95,3 +95,22 @@ def test_one_pick_per_token_odd_expert_count(cuda, oracle, path):
     got = out.cpu().numpy()
     say("top-1 path", path, "max_abs", float(np.abs(got - want).max()), "rel", rel_rms(got, want))
     assert float(np.abs(got - want).max()) < MAX_ABS and rel_rms(got, want) < REL_RMS
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_run_single_expert(cuda, oracle, path):
+    """MoELayer.run_single_expert (the reference's per-expert hook, engine/tiers.py:597-605): expert e's output rows for
+    given inputs against the oracle's expert forward, on every path; a layer with a shared expert (left out here)."""
+    import bmx
+    E, H, I, n = 6, 256, 128, 7
+    tab = small_table(E, H, I, True, 31, cuda)
+    layer = bmx.MoELayer(tab, 2, first=3)
+    x = torch.from_numpy(np.random.default_rng(8).standard_normal((n, H)).astype(np.float16)).to(cuda)
+    for e in (0, 4):
+        y = torch.full((n, H), float("nan"), dtype=torch.float32, device=cuda)
+        got = layer.run_single_expert(y, e, x, path).cpu().numpy()
+        want = np.stack([oracle.expert_forward(tab.host_expert(e), H, I, x[i].cpu().numpy())[0] for i in range(n)])
+        assert float(np.abs(got - want).max()) < MAX_ABS and rel_rms(got, want) < REL_RMS, (e, path)
+        assert torch.equal(layer.run_single_expert_dq(torch.empty_like(y), e, x, path), y)
+    with pytest.raises(ValueError):
+        layer.run_single_expert(torch.empty((n, H), dtype=torch.float32, device=cuda), E, x)
