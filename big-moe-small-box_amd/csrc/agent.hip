@@ -116,21 +116,24 @@ __global__ __launch_bounds__(64) void k_copy_wait(AgentShared* sh, int part, int
 }
 
 // out[T][H] += the CPU lane's partial of step seq (ring slot seq % AG_RING), once the job is done (bounded wait by
-// thread 0 of each workgroup; nothing is added when the job had no picks or the wait ran out). Four values a thread.
+// thread 0 of each workgroup; nothing is added when the job had no picks or the wait ran out; rows past the job's own
+// tokens are left alone). Four values a thread.
 __global__ __launch_bounds__(256) void k_cpu_add(AgentShared* sh, const float* part, int64_t seq, float* out, int T,
                                                  int H, int64_t limit)
 {
-    __shared__ int go;
+    __shared__ int go, rows;
     if (threadIdx.x == 0)
     {
         go = 0;
+        rows = 0;
         const int64_t t0 = wall_clock64();
         for (;;)
         {
             if (__hip_atomic_load(&sh->cpu_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= seq)
             {
-                go = __hip_atomic_load(&sh->cpu_n[(int)((uint64_t)seq % AG_RING)], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_SYSTEM) > 0;
+                const int slot = (int)((uint64_t)seq % AG_RING);
+                go = __hip_atomic_load(&sh->cpu_n[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) > 0;
+                rows = __hip_atomic_load(&sh->cpu_t[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 break;
             }
             if (__hip_atomic_load(&sh->flags[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
@@ -148,7 +151,7 @@ __global__ __launch_bounds__(256) void k_cpu_add(AgentShared* sh, const float* p
     if (!go) return;
     const float* p = part + (size_t)((uint64_t)seq % AG_RING) * BMX_PLAN_MAXT * H;
     const int i = 4 * (blockIdx.x * 256 + threadIdx.x);
-    if (i >= T * H) return;
+    if (i >= min(T, rows) * H) return;
     const float4 v = *reinterpret_cast<const float4*>(p + i);
     float4 o = *reinterpret_cast<const float4*>(out + i);
     o.x = o.x + v.x;
@@ -284,6 +287,7 @@ static void cpu_loop(bmx_copy_agent* a)
             if (ok) memcpy(a->cpu_part + (size_t)slot * BMX_PLAN_MAXT * H, part.data(), part.size() * 4);
         }
         if (!ok) agent_fail(a, BMX_ERR_ARG);
+        __atomic_store_n(&a->sh->cpu_t[slot], job.ntok, __ATOMIC_RELAXED);
         __atomic_store_n(&a->sh->cpu_n[slot], ok ? n : 0, __ATOMIC_RELAXED);
         a->cpu_jobs.fetch_add(1, std::memory_order_relaxed);
         __atomic_store_n(&a->sh->cpu_done, job.seq, __ATOMIC_RELEASE);

@@ -102,6 +102,7 @@ struct AgentShared {
     PlanReq req[AG_RING];
     PlanRep rep[AG_RING];
     int32_t cpu_n[AG_RING];         // CPU picks of the job in that slot (0: nothing to add)
+    int32_t cpu_t[AG_RING];         // its tokens: the partial rows the job wrote
 };
 // A planned step (slots.hip): the request's extra inputs and the step's masked outputs. xring: device address of the
 // agent's input-row ring [AG_RING][BMX_PLAN_MAXT][H] fp16 in host memory.
