@@ -233,6 +233,7 @@ __device__ __forceinline__ void had128_x8(float (&v)[8])
 
 // 16-byte global loads / stores and 8 fp16 <-> 16 bytes
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(1))) u32x4* gptr_u32x4;
 __device__ __forceinline__ u32x4 ldg4(const void* p)
 {

@@ -35,6 +35,7 @@ struct GvArgs {
     int gu_half;               // part_gu holds one split as fp16 [row][128-column block][matrix][128], each value the
                                // epilogue's own rounding of that split's sum (RN of 0.0f + product): same bits downstream
     const uint16_t* sh_gate;   // fp16 [H] or null: the shared expert's output is scaled by sigmoid(x[t] . sh_gate)
+    int pf_pairs = 0;          // prefill: two consecutive 128-row groups of one expert run as one 256-row tile
 };
 
 // The shared expert's gate of token t, sigmoid(x[t] . sh_gate), by the calling 16-lane group (every lane of the group

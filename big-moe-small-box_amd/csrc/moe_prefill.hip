@@ -67,14 +67,14 @@ static dim3 prep_grid(int R_max, int H)
 }
 
 // ---- LDS stages ------------------------------------------------------------------------------------------------------
-// A stage: [row 128][8 chunks of 16 B] = the k-step's 64 inputs of every row; chunk c of row r sits at slot
-//          c ^ ((r >> 1) & 7) of the row, so that the 16 lanes an LDS cycle serves (16 rows, one chunk) hit 16 different
-//          16-byte bank groups. Copied by the decode waves (each lane 32 B of one row) from registers loaded two steps
-//          ahead.
-// B stage: fragment f = tile-row * 8 + 32-column block (of the 256), 64 lanes x 16 B; lane L's 16 B at slot
-//          f * 64 + bsw(f, L), bsw(f, L) = L ^ ((L >> 4) & 1) ^ ((f & 1) << 3): a bijection on each 16-lane block (the
-//          MFMA reads stay conflict-free) that spreads the 16 lanes of a decode store over 16 bank groups.
-constexpr int PF_A_U4 = 128 * 8;
+// A stage: [row 128 (256 for a pair of groups)][8 chunks of 16 B] = the k-step's 64 inputs of every row; chunk c of row
+//          r sits at slot c ^ ((r >> 1) & 7) of the row, so that the 16 lanes an LDS cycle serves (16 rows, one chunk)
+//          hit 16 different 16-byte bank groups. Copied by the decode waves (each lane 32 B of a row per 16 rows) from
+//          registers loaded two steps ahead.
+// B stage: fragment f = tile-row * 8 + 32-column block (of the 256; of the 128 for a pair), 64 lanes x 16 B; lane L's
+//          16 B at slot f * 64 + bsw(f, L), bsw(f, L) = L ^ ((L >> 4) & 1) ^ ((f & 1) << 3): a bijection on each 16-lane
+//          block (the MFMA reads stay conflict-free) that spreads the 16 lanes of a decode store over 16 bank groups.
+constexpr int PF_A_U4 = 2 * PF_M * 8;
 constexpr int PF_B_U4 = 4 * 8 * 64;
 __shared__ u32x4 pf_a0[PF_A_U4];
 __shared__ u32x4 pf_a1[PF_A_U4];
@@ -134,6 +134,45 @@ __device__ __forceinline__ void decode_half(const uint32_t (&own)[Fmt<F>::TB / 1
     }
 }
 
+// A quarter strip: stream positions 32 HALF + 16 SUB .. + 15, the same two columns as decode_half<F, HALF> but only
+// input rows 4 SUB .. + 3 and 8 + 4 SUB .. + 3 (dwords 2 SUB, 2 SUB + 1 of each of the column's two fragment slots).
+template <int F, int HALF, int SUB>
+__device__ __forceinline__ void decode_quarter(const uint32_t (&own)[Fmt<F>::TB / 16], u32x4* __restrict__ stage, int kt,
+                                               int col0)
+{
+    constexpr int NW = Fmt<F>::TB / 16;
+    constexpr RingTab<F> tab;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) asm volatile("" :: "v"(own[k]));
+    const uint32_t prev = __builtin_amdgcn_mov_dpp(own[NW - 1], 0x93, 0xf, 0xf, false);
+    uint32_t fr[2][4];      // [column][dword 2 SUB, 2 SUB + 1 of rows 0-7, then of rows 8-15]
+#pragma unroll
+    for (int j8 = 32 * HALF + 16 * SUB; j8 < 32 * HALF + 16 * SUB + 16; j8 += 8)
+    {
+        uint32_t st[8], w[4];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st[q] = win_state(prev, own, tab.q[j8 + q]);
+        cb_oct(st, w);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const int dw = strip_dw(j8 + 2 * q);
+            fr[strip_cidx(j8 + 2 * q) >> 1][((dw >> 2) << 1) + (dw & 1)] = w[q];
+        }
+    }
+#pragma unroll
+    for (int ci = 0; ci < 2; ++ci)
+    {
+        const int col = col0 + lane_col(lane, HALF + 2 * ci);
+        const int f = kt * 8 + (col >> 5);
+        u32x4* fp = stage + f * 64;
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint32_t*>(fp + bsw(f, col & 31)) + 2 * SUB) = u32x2{fr[ci][0], fr[ci][1]};
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint32_t*>(fp + bsw(f, (col & 31) + 32)) + 2 * SUB) =
+            u32x2{fr[ci][2], fr[ci][3]};
+    }
+}
+
 // ---- grouped GEMM ----------------------------------------------------------------------------------------------------
 // Work unit: (group of <= 128 rows, matrix, 256-column block); 12 waves, one barrier per k-step (64 k). While waves 0-3
 // run the MFMAs of step i from A / B stage i % 2, waves 4-11 stage step i + 1: they store the A rows loaded two steps
@@ -145,59 +184,75 @@ __device__ __forceinline__ void decode_half(const uint32_t (&own)[Fmt<F>::TB / 1
 // DOWN = false: gate (matrix 0) or up (1) of the rotated input rows; DOWN = true: down of the down-input rows.
 constexpr int PF_WAVES = 12;
 
+// cb: the 256-column block of one group's unit; the 128-column block of a pair's (pair = 1)
 struct PfJob {
-    int g, mat, cb, e, r0, nr, K, N, nb128;
+    int g, mat, cb, e, r0, nr, K, N, nb128, pair;
     const bmx_expert* ex;
 };
 
 // An MFMA wave multiplies the 32-row blocks that hold rows of the group (rows past the group's end inside such a block
 // hold copies of its last row) and all its columns (a missing second 128-column half holds stale LDS); neither padding
-// is stored.
+// is stored. A wave's tile: MBW 32-row blocks x NBW 32-column blocks (2 x 4 for one group's 128 x 256 tile, 4 x 2 for a
+// pair's 256 x 128), the waves 2 (rows, wave & 1) x 2 (columns, wave >> 1).
+template <int MBW, int NBW>
 struct PfFrag {
-    f16x8 a[2];      // [row block]
-    f16x8 b[4];      // [column block]
+    f16x8 a[MBW];    // [row block]
+    f16x8 b[NBW];    // [column block]
 };
 
-// NMB: row blocks of 32 this wave computes (2; 1 when the group's rows end in the wave's first block)
-template <int NMB>
-__device__ __forceinline__ void pf_frag_load(PfFrag& f, const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, int ks)
+// NMB: row blocks of 32 this wave computes (MBW; fewer when the group's rows end inside the wave's blocks)
+template <int MBW, int NBW, int NMB>
+__device__ __forceinline__ void pf_frag_load(PfFrag<MBW, NBW>& f, const u32x4* __restrict__ sa, const u32x4* __restrict__ sb,
+                                             int ks)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave & 1, wn = wave >> 1;
     const int slot = (2 * ks + (lane >> 5)) ^ ((lane >> 1) & 7);
 #pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) f.a[mb] = __builtin_bit_cast(f16x8, sa[(64 * wm + 32 * mb + (lane & 31)) * 8 + slot]);
+    for (int mb = 0; mb < NMB; ++mb)
+        f.a[mb] = __builtin_bit_cast(f16x8, sa[(32 * MBW * wm + 32 * mb + (lane & 31)) * 8 + slot]);
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < NBW; ++nb)
     {
-        const int fi = ks * 8 + 4 * wn + nb;
+        const int fi = ks * 8 + NBW * wn + nb;
         f.b[nb] = __builtin_bit_cast(f16x8, sb[fi * 64 + bsw(fi, lane)]);
     }
 }
 
-template <int NMB>
-__device__ __forceinline__ void pf_frag_mfma(const PfFrag& f, f32x16 (&acc)[2][4])
+template <int MBW, int NBW, int NMB>
+__device__ __forceinline__ void pf_frag_mfma(const PfFrag<MBW, NBW>& f, f32x16 (&acc)[MBW][NBW])
 {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb)
             acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[mb], f.b[nb], acc[mb][nb], 0, 0, 0);
 }
 
 // one k-step of an MFMA wave: 4 sub-steps of 16 k, the fragments of sub-step ks + 1 read while those of ks feed the MFMAs
-template <int NMB>
+template <int MBW, int NBW, int NMB>
 __device__ __forceinline__ void pf_mfma_step(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb,
-                                             f32x16 (&acc)[2][4])
+                                             f32x16 (&acc)[MBW][NBW])
 {
-    PfFrag f0, f1;
-    pf_frag_load<NMB>(f0, sa, sb, 0);
-    pf_frag_load<NMB>(f1, sa, sb, 1);
-    pf_frag_mfma<NMB>(f0, acc);
-    pf_frag_load<NMB>(f0, sa, sb, 2);
-    pf_frag_mfma<NMB>(f1, acc);
-    pf_frag_load<NMB>(f1, sa, sb, 3);
-    pf_frag_mfma<NMB>(f0, acc);
-    pf_frag_mfma<NMB>(f1, acc);
+    PfFrag<MBW, NBW> f0, f1;
+    pf_frag_load<MBW, NBW, NMB>(f0, sa, sb, 0);
+    pf_frag_load<MBW, NBW, NMB>(f1, sa, sb, 1);
+    pf_frag_mfma<MBW, NBW, NMB>(f0, acc);
+    pf_frag_load<MBW, NBW, NMB>(f0, sa, sb, 2);
+    pf_frag_mfma<MBW, NBW, NMB>(f1, acc);
+    pf_frag_load<MBW, NBW, NMB>(f1, sa, sb, 3);
+    pf_frag_mfma<MBW, NBW, NMB>(f0, acc);
+    pf_frag_mfma<MBW, NBW, NMB>(f1, acc);
+}
+
+// the MFMA loop over K (one barrier per step, as the decode waves)
+template <int MBW, int NBW, int NMB>
+__device__ __forceinline__ void pf_mfma_loop(int KT, f32x16 (&acc)[MBW][NBW])
+{
+    for (int i = 0; i < KT; ++i)
+    {
+        pf_mfma_step<MBW, NBW, NMB>(a_stage(i & 1), b_stage(i & 1), acc);
+        step_barrier();
+    }
 }
 
 // A rows of one k-step: lane's 32 bytes (chunks 2 (lane & 3), + 1) of row 16 d + (lane >> 2)
@@ -223,75 +278,173 @@ __device__ __forceinline__ void a_store(const PfArow& r, u32x4* __restrict__ sta
 // The loop is straight-line code (every step issues the same loads, past-the-end steps re-read the last one, a missing
 // second 128-column half decodes the first one's tiles again), so the compiler's wait counts for the prefetched
 // registers stay exact and the waits land only where the data is two steps old.
-template <int F, int HALF, bool ACOPY>
+// One group (PAIR false): decode wave 4 + d decodes strip half d & 1 of 128-column half (d >> 1) & 1 and copies A rows
+// 16 d .. + 15. A pair (PAIR true, one 128-column block): strip quarter 2 HALF + SUB = d & 3, A rows 32 d .. + 31.
+template <int F, int HALF, int SUB, bool PAIR, bool ACOPY>
 __device__ __forceinline__ void pf_decoder(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int d)
 {
-    constexpr int TB = Fmt<F>::TB, NW = TB / 16;
+    constexpr int TB = Fmt<F>::TB, NW = TB / 16, NA = PAIR ? 2 : 1;
     const int lane = threadIdx.x & 63;
     const int h = lane >> 5, t = (lane >> 2) & 7, s = lane & 3;
     const int kt = 2 * (d >> 2) + h, th = (d >> 1) & 1;
-    const int tcol = min(2 * jb.cb + th, jb.nb128 - 1);
+    const int tcol = PAIR ? jb.cb : min(2 * jb.cb + th, jb.nb128 - 1);
     const size_t row_bytes = (size_t)(jb.N / 16) * TB, step_bytes = 4 * row_bytes;
     const uint8_t* p = mat_base + (size_t)kt * row_bytes + (size_t)(tcol * 8 + t) * TB + s * (TB / 4);
     const int KT = jb.K / 64;
-    // this lane's A row (rows past the group's end read its last row; their products are not stored)
-    const int arow = 16 * d + (lane >> 2);
-    const uint16_t* rowp = asrc + (size_t)(jb.r0 + min(arow, jb.nr - 1)) * jb.K;
+    // this lane's A rows (rows past the group's end read its last row; their products are not stored)
+    int arow[NA];
+    const uint16_t* rowp[NA];
+#pragma unroll
+    for (int j = 0; j < NA; ++j)
+    {
+        arow[j] = 16 * NA * d + 16 * j + (lane >> 2);
+        rowp[j] = asrc + (size_t)(jb.r0 + min(arow[j], jb.nr - 1)) * jb.K;
+    }
     auto wp = [&](int step) { return p + (size_t)min(step, KT - 1) * step_bytes; };
     auto ak = [&](int step) { return 64 * min(step, KT - 1); };
+    auto dec = [&](const uint32_t (&w)[NW], u32x4* stage) {
+        if constexpr (PAIR) decode_quarter<F, HALF, SUB>(w, stage, kt, 0);
+        else decode_half<F, HALF>(w, stage, kt, 128 * th);
+    };
+    auto fetch = [&](PfArow (&a)[NA], int step) {
+#pragma unroll
+        for (int j = 0; j < NA; ++j) a_fetch(a[j], rowp[j], ak(step));
+    };
+    auto store = [&](const PfArow (&a)[NA], u32x4* stage) {
+#pragma unroll
+        for (int j = 0; j < NA; ++j) a_store(a[j], stage, arow[j]);
+    };
     uint32_t w0[NW], w1[NW], w2[NW];
-    PfArow a0, a1, a2;
+    PfArow a0[NA], a1[NA], a2[NA];
     if (ACOPY)
     {
-        a_fetch(a0, rowp, ak(0));
-        a_fetch(a1, rowp, ak(1));
-        a_fetch(a2, rowp, ak(2));
+        fetch(a0, 0);
+        fetch(a1, 1);
+        fetch(a2, 2);
     }
     load_words(w0, wp(0));
     load_words(w1, wp(1));
     load_words(w2, wp(2));
-    decode_half<F, HALF>(w0, pf_b0, kt, 128 * th);
-    if (ACOPY) a_store(a0, pf_a0, arow);
+    dec(w0, pf_b0);
+    if (ACOPY) store(a0, pf_a0);
     step_barrier();
     // step i: stage step i + 1 (A rows, B fragments) into stage (i + 1) % 2, fetch step i + 3 into the sets step i used
     for (int i = 0; i < KT; i += 3)
     {
-        if (ACOPY) a_fetch(a0, rowp, ak(i + 3));
+        if (ACOPY) fetch(a0, i + 3);
         load_words(w0, wp(i + 3));
-        decode_half<F, HALF>(w1, b_stage((i + 1) & 1), kt, 128 * th);
-        if (ACOPY) a_store(a1, a_stage((i + 1) & 1), arow);
+        dec(w1, b_stage((i + 1) & 1));
+        if (ACOPY) store(a1, a_stage((i + 1) & 1));
         step_barrier();
         if (i + 1 >= KT) break;
-        if (ACOPY) a_fetch(a1, rowp, ak(i + 4));
+        if (ACOPY) fetch(a1, i + 4);
         load_words(w1, wp(i + 4));
-        decode_half<F, HALF>(w2, b_stage(i & 1), kt, 128 * th);
-        if (ACOPY) a_store(a2, a_stage(i & 1), arow);
+        dec(w2, b_stage(i & 1));
+        if (ACOPY) store(a2, a_stage(i & 1));
         step_barrier();
         if (i + 2 >= KT) break;
-        if (ACOPY) a_fetch(a2, rowp, ak(i + 5));
+        if (ACOPY) fetch(a2, i + 5);
         load_words(w2, wp(i + 5));
-        decode_half<F, HALF>(w0, b_stage((i + 1) & 1), kt, 128 * th);
-        if (ACOPY) a_store(a0, a_stage((i + 1) & 1), arow);
+        dec(w0, b_stage((i + 1) & 1));
+        if (ACOPY) store(a0, a_stage((i + 1) & 1));
         step_barrier();
     }
 }
 
 // A rows are copied only where an MFMA wave reads them: the 32-row blocks that hold rows of the group
+template <int F, bool PAIR>
+__device__ __forceinline__ void pf_decoder_role(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int d)
+{
+    const bool acopy = (PAIR ? 32 : 16) * d < (jb.nr + 31) / 32 * 32;
+    if (PAIR)
+    {
+        // quarter d & 3 (a switch on a wave-uniform value: one path per wave)
+        switch ((d & 3) + (acopy ? 4 : 0))
+        {
+            case 0: pf_decoder<F, 0, 0, true, false>(jb, mat_base, asrc, d); break;
+            case 1: pf_decoder<F, 0, 1, true, false>(jb, mat_base, asrc, d); break;
+            case 2: pf_decoder<F, 1, 0, true, false>(jb, mat_base, asrc, d); break;
+            case 3: pf_decoder<F, 1, 1, true, false>(jb, mat_base, asrc, d); break;
+            case 4: pf_decoder<F, 0, 0, true, true>(jb, mat_base, asrc, d); break;
+            case 5: pf_decoder<F, 0, 1, true, true>(jb, mat_base, asrc, d); break;
+            case 6: pf_decoder<F, 1, 0, true, true>(jb, mat_base, asrc, d); break;
+            default: pf_decoder<F, 1, 1, true, true>(jb, mat_base, asrc, d); break;
+        }
+    }
+    else if (acopy)
+    {
+        if (d & 1) pf_decoder<F, 1, 0, false, true>(jb, mat_base, asrc, d);
+        else pf_decoder<F, 0, 0, false, true>(jb, mat_base, asrc, d);
+    }
+    else
+    {
+        if (d & 1) pf_decoder<F, 1, 0, false, false>(jb, mat_base, asrc, d);
+        else pf_decoder<F, 0, 0, false, false>(jb, mat_base, asrc, d);
+    }
+}
+
 template <int F>
 __device__ __forceinline__ void pf_decoder_any(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc)
 {
     const int d = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) - 4);
-    const bool acopy = 16 * d < (jb.nr + 31) / 32 * 32;
-    if (acopy)
+    if (jb.pair) pf_decoder_role<F, true>(jb, mat_base, asrc, d);
+    else pf_decoder_role<F, false>(jb, mat_base, asrc, d);
+}
+
+// Store of an MFMA wave's products: accumulator element v of lane L is row 8 (v / 4) + 4 (L / 32) + v % 4, column L % 32
+// of its 32 x 32 block; rows past the group's end are not stored.
+template <bool DOWN, int MBW, int NBW>
+__device__ __forceinline__ void pf_store(const GvArgs& a, const PfJob& jb, const f32x16 (&acc)[MBW][NBW])
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave & 1, wn = wave >> 1;
+    // the wave's 128-column output block and its first column in it
+    const int cbo = jb.pair ? jb.cb : 2 * jb.cb + wn, c0 = jb.pair ? 32 * NBW * wn : 0;
+    if (cbo >= jb.nb128) return;
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb)
     {
-        if (d & 1) pf_decoder<F, 1, true>(jb, mat_base, asrc, d);
-        else pf_decoder<F, 0, true>(jb, mat_base, asrc, d);
+        if (32 * MBW * wm + 32 * mb >= jb.nr) continue;
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb)
+        {
+            const int col = c0 + 32 * nb + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+            {
+                const int row = 32 * MBW * wm + 32 * mb + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (row >= jb.nr) continue;
+                const size_t r = (size_t)(jb.r0 + row);
+                if (DOWN) a.part_dn[(r * a.NBH + cbo) * 128 + col] = acc[mb][nb][v];
+                else
+                    reinterpret_cast<uint16_t*>(a.part_gu)[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] =
+                        f2h_r(0.0f + acc[mb][nb][v]);
+            }
+        }
     }
-    else
+}
+
+// The MFMA waves of one tile shape: row blocks past the group's end are neither read nor multiplied (a wave with none
+// only keeps the barriers).
+template <bool DOWN, int MBW, int NBW>
+__device__ __forceinline__ void pf_mfma_wave(const GvArgs& a, const PfJob& jb, int KT)
+{
+    const int wm = (threadIdx.x >> 6) & 1;
+    f32x16 acc[MBW][NBW];
+#pragma unroll
+    for (int i = 0; i < MBW; ++i)
+#pragma unroll
+        for (int j = 0; j < NBW; ++j) acc[i][j] = f32x16{};
+    const int nmb = min(MBW, max(0, (jb.nr - 32 * MBW * wm + 31) / 32));
+    step_barrier();
+    switch (nmb)
     {
-        if (d & 1) pf_decoder<F, 1, false>(jb, mat_base, asrc, d);
-        else pf_decoder<F, 0, false>(jb, mat_base, asrc, d);
+        case 0: for (int i = 0; i < KT; ++i) step_barrier(); break;
+        case 1: pf_mfma_loop<MBW, NBW, 1>(KT, acc); break;
+        case 2: pf_mfma_loop<MBW, NBW, 2>(KT, acc); break;
+        case 3: if constexpr (MBW >= 3) pf_mfma_loop<MBW, NBW, 3>(KT, acc); break;
+        default: if constexpr (MBW >= 4) pf_mfma_loop<MBW, NBW, 4>(KT, acc); break;
     }
+    pf_store<DOWN, MBW, NBW>(a, jb, acc);
 }
 
 template <bool DOWN>
@@ -309,10 +462,27 @@ __global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
     if (!DOWN && group_skipped(a, jb.e)) return;
     jb.r0 = a.groups[3 * jb.g + 1];
     jb.nr = a.groups[3 * jb.g + 2];
+    jb.pair = 0;
+    if (a.pf_pairs)
+    {
+        // groups 2 j and 2 j + 1 of an expert (consecutive rows) form a pair; its units are both groups' units, unit
+        // (group 2 j + q, 256-column block c) taking 128-column block 2 c + q of all the pair's rows
+        const int base = a.offsets[jb.e], cnt = a.offsets[jb.e + 1] - base;
+        const int q = (jb.r0 - base) / PF_M, ng = (cnt + PF_M - 1) / PF_M;
+        if ((q & 1) || q + 1 < ng)
+        {
+            const int q0 = q & ~1;
+            jb.pair = 1;
+            jb.r0 = base + q0 * PF_M;
+            jb.nr = min(2 * PF_M, cnt - q0 * PF_M);
+            jb.cb = 2 * jb.cb + (q & 1);
+            if (jb.cb >= nb128) return;        // an odd block count: the last 256-column block has one half
+        }
+    }
     jb.ex = jb.e == a.E ? a.shared : a.experts + jb.e;
     jb.K = DOWN ? a.I : a.H;
     jb.N = DOWN ? a.H : a.I;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int KT = jb.K / 64;
 
     const uint16_t* asrc = DOWN ? a.act_rows : a.xt + (size_t)jb.mat * a.R_max * a.H;
@@ -328,57 +498,8 @@ __global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
         }
         return;
     }
-
-    // MFMA waves
-    f32x16 acc[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-    // row blocks past the group's end are neither read nor multiplied (a wave with none only keeps the barriers)
-    const int wm = wave & 1, wn = wave >> 1;
-    const int nmb = min(2, max(0, (jb.nr - 64 * wm + 31) / 32));
-    step_barrier();
-    if (nmb == 2)
-        for (int i = 0; i < KT; ++i)
-        {
-            pf_mfma_step<2>(a_stage(i & 1), b_stage(i & 1), acc);
-            step_barrier();
-        }
-    else if (nmb == 1)
-        for (int i = 0; i < KT; ++i)
-        {
-            pf_mfma_step<1>(a_stage(i & 1), b_stage(i & 1), acc);
-            step_barrier();
-        }
-    else
-        for (int i = 0; i < KT; ++i) step_barrier();
-
-    // accumulator element v of lane L: row 8 (v / 4) + 4 (L / 32) + v % 4, column L % 32 of its 32 x 32 block
-    const int r0 = jb.r0, nr = jb.nr;
-    const int cbo = 2 * jb.cb + wn;                 // this wave's 128-column output block
-    if (cbo >= nb128) return;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-    {
-        if (64 * wm + 32 * mb >= nr) continue;
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-        {
-            const int col = 32 * nb + (lane & 31);
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-            {
-                const int row = 64 * wm + 32 * mb + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                if (row >= nr) continue;
-                const size_t r = (size_t)(r0 + row);
-                if (DOWN) a.part_dn[(r * a.NBH + cbo) * 128 + col] = acc[mb][nb][v];
-                else
-                    reinterpret_cast<uint16_t*>(a.part_gu)[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] =
-                        f2h_r(0.0f + acc[mb][nb][v]);
-            }
-        }
-    }
+    if (jb.pair) pf_mfma_wave<DOWN, 4, 2>(a, jb, KT);
+    else pf_mfma_wave<DOWN, 2, 4>(a, jb, KT);
 }
 
 // ---- mid-size grouped GEMM: groups of <= 32 rows, every wave decodes and multiplies ------------------------------------
@@ -563,6 +684,13 @@ static PrefillPlan prefill_plan(const MoeShape& m)
 
 int prefill_rows_per_group() { return PF_M; }
 
+// BMX_PF_PAIRS=0: every group its own 128-row tile (the products are the same bits either way)
+static bool prefill_pairs_allowed()
+{
+    const char* v = getenv("BMX_PF_PAIRS");
+    return !(v && *v == '0');
+}
+
 // ---- mid-size path ------------------------------------------------------------------------------------------------------
 struct MidPlan {
     int NB, NBH, G_max, R_max, KS_gu, KS_dn;
@@ -699,6 +827,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.filter = 0;
     a.act_in_down = 0;
     a.gu_half = 1;
+    a.pf_pairs = prefill_pairs_allowed() ? 1 : 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);

@@ -189,3 +189,54 @@ def test_mid_experts_rows_and_properties(cuda):
     a = bmx.ops.moe_forward(d, x, sel, w, path=MID)
     b = bmx.ops.moe_forward(d, x, sel, (w * 2).contiguous(), path=MID)
     assert torch.equal(b, a * 2)
+
+
+def forced_picks(T, topk, E, plan, seed):
+    """sel [T, topk]: slot k of token t picks plan[k](t); weights random positive"""
+    sel = np.array([[plan[k](t) for k in range(topk)] for t in range(T)], np.int64)
+    assert all(len(set(r)) == topk for r in sel.tolist())
+    w = (np.random.default_rng(seed).random((T, topk)) + 0.25).astype(np.float16)
+    return sel, w
+
+
+PAIR_CASES = [
+    # name, H, I, fmts, shared, T, topk, E, slot plans: expert 0 takes 330 rows (groups 128 128 74: a pair and a
+    # single), expert 1 260 (128, 128, 4: a pair and a single), expert 2 70; odd block counts (H 384, I 384)
+    ("odd blocks, pair + single, shared", 384, 384, (2, 1, 3), True, 330, 2, 6,
+     (lambda t: 0, lambda t: 1 if t < 260 else 2)),
+    # expert 0: 600 rows (five groups: two pairs and a single), expert 1: 300, the rest spread
+    ("two pairs, K4", 1024, 512, (3, 3, 3), False, 600, 3, 9,
+     (lambda t: 0, lambda t: 1 if t < 300 else 2 + t % 7, lambda t: 3 + t % 6 if t < 300 else 2 + (t + 3) % 7)),
+]
+
+
+@pytest.mark.parametrize("name,H,I,fmts,shared,T,topk,E,plan", PAIR_CASES, ids=[c[0] for c in PAIR_CASES])
+def test_prefill_pairs(cuda, oracle, name, H, I, fmts, shared, T, topk, E, plan):
+    """Consecutive 128-row groups of one expert run as one 256-row x 128-column tile (a pair): the same products as
+    one tile per group (BMX_PF_PAIRS=0) bit for bit, and rows of both halves of a pair and of the single group after it
+    within the oracle's tolerance."""
+    import os
+    import bmx
+    tab = bmx.ExpertTable.random(H, I, E, fmts, shared=shared, seed=31, device=cuda)
+    layer = bmx.MoELayer(tab, topk, score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(32)
+    x = torch.randn((T, H), generator=g, device=cuda).half()
+    sel_np, w_np = forced_picks(T, topk, E, plan, 33)
+    sel, w = torch.from_numpy(sel_np).to(cuda), torch.from_numpy(w_np).to(cuda)
+    say("pairs", name, "run")
+    out = layer.run_bszN(x, sel, w, path=PREFILL).clone()
+    os.environ["BMX_PF_PAIRS"] = "0"
+    try:
+        ref = layer.run_bszN(x, sel, w, path=PREFILL).clone()
+    finally:
+        os.environ.pop("BMX_PF_PAIRS", None)
+    torch.cuda.synchronize()
+    say("pairs", name, "max |pairs - singles|", float((out - ref).abs().max()))
+    assert torch.equal(out, ref) and float(out.abs().max()) > 0
+    rows = [0, 127, 128, 200, 255, 256, T - 1]
+    want = oracle_layer(oracle, tab, x.cpu().numpy(), sel_np, w_np, rows)
+    got = out.cpu().numpy()[rows]
+    err_abs, err_rel = float(np.abs(got - want).max()), rel_rms(got, want)
+    say("pairs", name, "oracle rows", rows, "max_abs", err_abs, "rel_rms", err_rel)
+    assert err_abs < MAX_ABS and err_rel < REL_RMS
