@@ -239,6 +239,14 @@ def bench_c4(args):
         pf_admitted = [torch.cuda.Event() for _ in range(NL)]
     slots = bmx.ExpertSlots(layers, S, maxj=16, copies=args.copies)
     DMA = args.copies == "dma"
+    CPUL = args.cpu_lane > 0 and DMA
+    if CPUL:
+        # planned steps: the agent's planner puts misses on the CPU lane (fast mode, args.cpu_lane worker threads) when
+        # its estimated finish is no later than the GPU's; the GPU costs are measured per-expert times of this stack,
+        # the CPU's starts at args.cpu_expert_us and follows the worker's measured time per pick (cpu_measured)
+        slots.cpu_lane(topk, threads=args.cpu_lane)
+        slots.plan(dict(cpu_on=1, max_cpu=args.cpu_max, cpu_fast=1, cpu_measured=1, gpu_base_us=50.0, gpu_hit_us=0.0,
+                        gpu_admit_us=140.0, cpu_base_us=10.0, cpu_expert_us=args.cpu_expert_us, cpu_token_us=60.0))
     # warm: each layer's most popular experts (Zipf rank order of its permutation), S // NL per layer
     per = S // NL
     for li in range(NL):
@@ -254,6 +262,7 @@ def bench_c4(args):
     descs = [slots.desc(li, topk) for li in range(NL)]
     sel = torch.empty((1, topk), dtype=torch.int64, device=dev)
     w = torch.empty((1, topk), dtype=torch.float16, device=dev)
+    sel_g, w_g = torch.empty_like(sel), torch.empty_like(w)          # planned steps: the picks the GPU computes
     out = torch.empty((NL, H), dtype=torch.float32, device=dev)
     rpg = L.bmx_rows_per_group(1, topk, 1)
     routes = bmx.ops.RoutesBuf(1, topk, E, True, rpg, dev)
@@ -275,7 +284,11 @@ def bench_c4(args):
             lgp = ctypes.c_void_p(lg_all.data_ptr() + (li * NTOK + tok) * E * 2)
             bmx._lib.check(L.bmx_router_topk(lgp, P(biases[li]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0, P(sel),
                                              P(w), sp), "router")
-            if DMA:
+            if CPUL:
+                bmx._lib.check(L.bmx_slot_step_planned(tstruct, slots.agent, li, P(sel), P(w), 1, topk, 0, 1, P(x),
+                                                       P(sel_g), P(w_g), None, ctypes.byref(seq), sp), "planned step")
+                seqs[li] = seq.value
+            elif DMA:
                 bmx._lib.check(L.bmx_slot_step_agent(tstruct, slots.agent, li, P(sel), topk, 0, 1, ctypes.byref(seq),
                                                      sp), "slot step")
                 seqs[li] = seq.value
@@ -308,7 +321,8 @@ def bench_c4(args):
                 ev = torch.cuda.Event()
                 ev.record(side)
                 pf_copied[b] = ev
-            bmx._lib.check(L.bmx_dispatch(P(sel), 1, topk, E, 0, 1, rpg, ctypes.byref(routes.struct), P(dws), dws_n, sp),
+            gs, gw_ = (sel_g, w_g) if CPUL else (sel, w)
+            bmx._lib.check(L.bmx_dispatch(P(gs), 1, topk, E, 0, 1, rpg, ctypes.byref(routes.struct), P(dws), dws_n, sp),
                            "dispatch")
             d = ctypes.byref(descs[li])
             o = ctypes.c_void_p(out.data_ptr() + li * H * 4)
@@ -320,19 +334,23 @@ def bench_c4(args):
                     else:
                         s.wait_event(copied_gu[li] if st == "gu" else copied_dn[li])
                     continue
-                bmx._lib.check(L.bmx_moe_stage(d, st, P(x), 1, ctypes.byref(routes.struct), None, None, P(w), o, P(ws),
-                                               ws_n, 1, sp), "stage")
+                bmx._lib.check(L.bmx_moe_stage(d, st, P(x), 1, ctypes.byref(routes.struct), None, None, P(gw_), o,
+                                               P(ws), ws_n, 1, sp), "stage")
+            if CPUL:
+                bmx._lib.check(L.bmx_cpu_lane_add(slots.agent, seqs[li], o, 1, sp), "cpu lane add")
 
     for i in range(args.warmup):
         token(i % NTOK)
     torch.cuda.synchronize()
     st0 = slots.stats()
+    ps0 = slots.plan_stats() if CPUL else None
     t0 = time.perf_counter()
     for i in range(args.steps):
         token((args.warmup + i) % NTOK)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     st1 = slots.stats()
+    ps1 = slots.plan_stats() if CPUL else None
     d = [b - a for a, b in zip(st0, st1)]
     exp_bytes = layers[0].expert_bytes(0)
     staged = (d[2] + d[5]) * exp_bytes
@@ -366,6 +384,11 @@ def bench_c4(args):
                                  "prefetched": d[5] / args.steps, "prefetch_used": d[6] / args.steps,
                                  "prefetch_wasted": d[7] / args.steps},
         "copies": args.copies,
+        "cpu_lane": {"threads": args.cpu_lane, "max_cpu": args.cpu_max, "cpu_expert_us": args.cpu_expert_us,
+                     "cpu_experts_per_token": (ps1[1] - ps0[1]) / args.steps,
+                     "cpu_jobs_per_token": (ps1[2] - ps0[2]) / args.steps,
+                     "cpu_job_us": round((ps1[3] - ps0[3]) / max(1, ps1[2] - ps0[2]), 1),
+                     "cpu_pick_us_measured": round(ps1[4] / 1e3, 1)} if CPUL else None,
         "prefetch": {"limit": PF, "guess_noise": args.guess_noise, "ahead": AH,
                      "precision": round(d[6] / max(1, d[5]), 4)} if PF else None,
         "hit_rate": round(d[0] / max(1, d[0] + d[1]), 4),
@@ -599,6 +622,11 @@ def main():
                     help="c4: slot copies by a kernel on a side stream or by the copy agent on the DMA engines")
     ap.add_argument("--guess-noise", type=float, default=1.0, metavar="SIGMA",
                     help="c4 prefetch: the next layer's guess routes its own logits plus N(0, SIGMA) noise")
+    ap.add_argument("--cpu-lane", type=int, default=0, metavar="THREADS",
+                    help="c4: planned steps with the CPU lane (fast mode) on THREADS worker threads (0: off)")
+    ap.add_argument("--cpu-max", type=int, default=2, help="c4 --cpu-lane: most misses a layer call puts on the CPU")
+    ap.add_argument("--cpu-expert-us", type=float, default=125.0,
+                    help="c4 --cpu-lane: the planner's CPU cost of one expert until the lane's first job is timed")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (scale reference for HBM byte counters)")
     args = ap.parse_args()

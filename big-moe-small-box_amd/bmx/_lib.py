@@ -47,7 +47,7 @@ class CpuExpert(ctypes.Structure):
 
 class PlanPolicy(ctypes.Structure):
     _fields_ = [("cpu_on", ctypes.c_int32), ("max_cpu", ctypes.c_int32), ("home_single", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)] + \
+                ("cpu_fast", ctypes.c_int32), ("cpu_measured", ctypes.c_int32)] + \
                [(n, ctypes.c_double) for n in ("gpu_base_us", "gpu_hit_us", "gpu_home_us", "gpu_admit_us", "cpu_base_us",
                                                "cpu_expert_us", "cpu_token_us")]
 
@@ -101,6 +101,7 @@ SIGNATURES = {
     "bmx_copy_wait": (_I, [_P, _I64, _I, _P]),
     "bmx_copy_wait_layer": (_I, [_P, _I, _I, _P]),
     "bmx_cpu_expert_rows": (_I, [ctypes.POINTER(CpuExpert), _I, _I, _P, _I, _I, _I, _I, _I, _I, ctypes.c_float, _P, _I]),
+    "bmx_cpu_expert_rows_fast": (_I, [ctypes.POINTER(CpuExpert), _I, _I, _P, _I, _I, _I, ctypes.c_float, _P, _I]),
     "bmx_decode_splits": (_I, [ctypes.POINTER(MoeDesc), _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "bmx_cpu_dot2": (_I, [_P, _P, _P, _P, _I]),
     "bmx_dot2_f32_f16": (_I, [_P, _P, _P, _P, _I, _P]),
@@ -109,6 +110,7 @@ SIGNATURES = {
     "bmx_slot_step_planned": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _P, _I, _I, _I64, _I, _P, _P, _P, _P,
                                    ctypes.POINTER(_I64), _P]),
     "bmx_cpu_lane_add": (_I, [_P, _I64, _P, _I, _P]),
+    "bmx_copy_agent_plan_stats": (_I, [_P, _P]),
     "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
     "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }

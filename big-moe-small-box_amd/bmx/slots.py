@@ -97,6 +97,13 @@ class ExpertSlots:
         L.check(L.lib().bmx_copy_agent_status(self.agent, st), "bmx_copy_agent_status")
         return tuple(st)
 
+    def plan_stats(self):
+        """(requests answered, experts put on the CPU lane summed over requests, CPU jobs done, microseconds the CPU
+        lane's worker spent on them, its running mean per CPU pick in nanoseconds) of the agent's planner."""
+        st = (ctypes.c_int64 * 5)()
+        L.check(L.lib().bmx_copy_agent_plan_stats(self.agent, st), "bmx_copy_agent_plan_stats")
+        return tuple(st)
+
     def check(self):
         """Raise if the copy agent has failed (dma; a host read of shared memory, no synchronisation)."""
         if self.agent is not None:

@@ -69,7 +69,7 @@ struct bmx_copy_agent {
     std::atomic<int64_t> records{0}, copies{0};
     std::atomic<int64_t> copied_bytes{0};
     // residency plan
-    std::mutex plan_mu;
+    mutable std::mutex plan_mu;
     bmx_plan_policy policy{};            // cpu_on 0: every miss admitted
     std::atomic<int64_t> plans{0}, plan_cpu{0};
     // CPU lane
@@ -81,12 +81,15 @@ struct bmx_copy_agent {
     uint16_t* xring_dev = nullptr;
     float* cpu_part = nullptr;           // [AG_RING][BMX_PLAN_MAXT][H] fp32, pinned host
     float* cpu_part_dev = nullptr;
-    std::vector<int64_t> job_of;         // [AG_RING]: the planned step whose request carried rows (a job follows)
+    std::vector<int64_t> job_of;         // [AG_RING]: the planned step whose request carried rows (its plan may
+                                         // put picks on the CPU lane)
     std::thread cpu_th;
     std::mutex cpu_mu;
     std::condition_variable cpu_cv;
     std::deque<bmx::CpuJob> cpu_q;
     std::atomic<int64_t> cpu_jobs{0};
+    std::atomic<int64_t> cpu_ns{0};          // host time the CPU worker spent computing jobs
+    double cpu_pick_us = 0.0;                // running mean of the worker's time per pick (under plan_mu)
 };
 
 namespace bmx {
@@ -127,7 +130,12 @@ __global__ __launch_bounds__(256) void k_cpu_add(AgentShared* sh, const float* p
         go = 0;
         rows = 0;
         const int64_t t0 = wall_clock64();
-        for (;;)
+        // the step's own reply (read by the step before this launch; its ring slot is reused 64 steps later): a plan
+        // with no CPU pick has nothing to add, so the worker's completion of the empty job is not waited for
+        const PlanRep& rp = sh->rep[(uint64_t)seq % AG_RING];
+        const bool none = __hip_atomic_load(&rp.seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) == seq &&
+                          __hip_atomic_load(&rp.ncpu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0;
+        for (; !none;)
         {
             if (__hip_atomic_load(&sh->cpu_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= seq)
             {
@@ -194,6 +202,7 @@ static void plan_reply(bmx_copy_agent* a, const PlanReq& r, PlanRep& p, CpuJob* 
     {
         std::lock_guard<std::mutex> lk(a->plan_mu);
         pol = a->policy;
+        if (pol.cpu_measured && a->cpu_pick_us > 0.0) pol.cpu_expert_us = a->cpu_pick_us;
     }
     const int nu = r.nu;
     const bool cpu_ok = pol.cpu_on && a->cpu_ready && r.has_x && r.np <= BMX_PLAN_MAXP && r.ntok <= BMX_PLAN_MAXT;
@@ -246,8 +255,9 @@ static void plan_reply(bmx_copy_agent* a, const PlanReq& r, PlanRep& p, CpuJob* 
     }
 }
 
-// The CPU-lane worker: jobs in sequence order; each CPU pick's y row (bit for bit the decode path's), summed w * y in
-// pick order into its token's partial, which goes to the ring slot of the job's step, then cpu_done = seq.
+// The CPU-lane worker: jobs (steps with CPU picks) in sequence order; each CPU pick's y row (bit for bit the decode path's, or the fast mode's
+// when the policy asks for it), summed w * y in pick order into its token's partial, which goes to the ring slot of the
+// job's step, then cpu_done = seq.
 static void cpu_loop(bmx_copy_agent* a)
 {
     const int H = a->cpu_desc.H, I = a->cpu_desc.I, E = a->t.E;
@@ -263,10 +273,15 @@ static void cpu_loop(bmx_copy_agent* a)
             a->cpu_q.pop_front();
         }
         const int slot = ring_index(job.seq), n = (int)job.pick_e.size();
+        const auto t_job = std::chrono::steady_clock::now();
         bool ok = true;
         if (n > 0)
         {
-            int ks_gu = 0, ks_dn = 0, grouped = 0;
+            int ks_gu = 0, ks_dn = 0, grouped = 0, fast = 0;
+            {
+                std::lock_guard<std::mutex> lk(a->plan_mu);
+                fast = a->policy.cpu_fast;
+            }
             bmx_moe_desc d = a->cpu_desc;
             ok = bmx_decode_splits(&d, job.ntok, &ks_gu, &ks_dn, &grouped) == BMX_OK;
             part.assign((size_t)job.ntok * H, 0.0f);
@@ -275,9 +290,11 @@ static void cpu_loop(bmx_copy_agent* a)
             {
                 const int e = job.pick_e[i], tt = job.pick_t[i];
                 if (job.li < 0 || job.li >= a->t.L || e < 0 || e >= E || tt < 0 || tt >= job.ntok) { ok = false; break; }
-                ok = bmx_cpu_expert_rows(&a->cpu_experts[(size_t)job.li * E + e], H, I, job.x.data() + (size_t)tt * H, 1,
-                                         ks_gu, ks_dn, grouped, d.act, d.gated, d.act_limit, y.data(),
-                                         a->cpu_threads) == BMX_OK;
+                const bmx_cpu_expert* ce = &a->cpu_experts[(size_t)job.li * E + e];
+                const uint16_t* xr = job.x.data() + (size_t)tt * H;
+                ok = (fast ? bmx_cpu_expert_rows_fast(ce, H, I, xr, 1, d.act, d.gated, d.act_limit, y.data(), a->cpu_threads)
+                           : bmx_cpu_expert_rows(ce, H, I, xr, 1, ks_gu, ks_dn, grouped, d.act, d.gated, d.act_limit,
+                                                 y.data(), a->cpu_threads)) == BMX_OK;
                 for (int h = 0; ok && h < H; ++h)
                 {
                     const float pr = job.pick_w[i] * y[h];
@@ -289,12 +306,21 @@ static void cpu_loop(bmx_copy_agent* a)
         if (!ok) agent_fail(a, BMX_ERR_ARG);
         __atomic_store_n(&a->sh->cpu_t[slot], job.ntok, __ATOMIC_RELAXED);
         __atomic_store_n(&a->sh->cpu_n[slot], ok ? n : 0, __ATOMIC_RELAXED);
+        const int64_t ns =
+            std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t_job).count();
         a->cpu_jobs.fetch_add(1, std::memory_order_relaxed);
+        a->cpu_ns.fetch_add(ns, std::memory_order_relaxed);
+        if (ok && n > 0)
+        {
+            const double per = 1e-3 * (double)ns / n;
+            std::lock_guard<std::mutex> lk(a->plan_mu);
+            a->cpu_pick_us = a->cpu_pick_us > 0.0 ? a->cpu_pick_us + (per - a->cpu_pick_us) / 8.0 : per;
+        }
         __atomic_store_n(&a->sh->cpu_done, job.seq, __ATOMIC_RELEASE);
     }
 }
 
-// Serve request seq: plan, queue its CPU job (every request that carried rows has one, in order), reply.
+// Serve request seq: plan, queue its CPU job (a request whose plan put picks on the CPU lane has one, in order), reply.
 static void serve_plan(bmx_copy_agent* a, int64_t seq)
 {
     const PlanReq& r = a->sh->req[ring_index(seq)];
@@ -305,22 +331,20 @@ static void serve_plan(bmx_copy_agent* a, int64_t seq)
         agent_fail(a, BMX_ERR_ARG);
         return;
     }
-    const bool job = r.has_x && a->cpu_ready;
     CpuJob cj;
     cj.seq = seq;
-    plan_reply(a, r, p, job ? &cj : nullptr);
+    plan_reply(a, r, p, r.has_x && a->cpu_ready ? &cj : nullptr);
+    const bool job = !cj.pick_e.empty();
     if (job)
     {
         const int H = a->cpu_desc.H;
         const uint16_t* src = a->xring + (size_t)ring_index(seq) * BMX_PLAN_MAXT * H;
         cj.x.assign(src, src + (size_t)r.ntok * H);      // the step's rows leave the ring before the reply
-        {
-            std::lock_guard<std::mutex> lk(a->cpu_mu);
-            a->cpu_q.push_back(std::move(cj));
-        }
-        a->cpu_cv.notify_one();
+        std::lock_guard<std::mutex> lk(a->cpu_mu);
+        a->cpu_q.push_back(std::move(cj));
     }
     __atomic_store_n(&p.seq, seq, __ATOMIC_RELEASE);
+    if (job) a->cpu_cv.notify_one();                     // the wake-up's system call after the reply, not before it
 }
 
 // The agent thread: records in sequence order; per step record the gate / up copies under one signal, the down copies
@@ -605,6 +629,20 @@ static int agent_failure(const bmx_copy_agent* a, const char* who)
         return set_error(BMX_ERR_HIP, "%s: copy agent aborted", who);
     if (__atomic_load_n(&a->sh->flags[3], __ATOMIC_ACQUIRE))
         return set_error(BMX_ERR_HIP, "%s: a copy wait ran out of time (slot contents since then are not trusted)", who);
+    return BMX_OK;
+}
+
+int bmx_copy_agent_plan_stats(const bmx_copy_agent* a, int64_t* stats)
+{
+    if (!a || !stats) return set_error(BMX_ERR_ARG, "bmx_copy_agent_plan_stats: null argument");
+    stats[0] = a->plans.load();
+    stats[1] = a->plan_cpu.load();
+    stats[2] = a->cpu_jobs.load();
+    stats[3] = a->cpu_ns.load() / 1000;
+    {
+        std::lock_guard<std::mutex> lk(a->plan_mu);
+        stats[4] = (int64_t)(a->cpu_pick_us * 1e3);
+    }
     return BMX_OK;
 }
 

@@ -17,10 +17,17 @@
 // butterflies).
 #include <immintrin.h>
 
+#include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cmath>
+#include <condition_variable>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
+#include <memory>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -574,6 +581,356 @@ void parallel_cols(int N, int threads, F fn)
     for (auto& t : th) t.join();
 }
 
+// ---- fast mode: the decode fused into an fp32 GEMV --------------------------------------------------------------------
+// The weights are the device's fp16 values exactly: the codebook value RN16((1024 + s) * KINV + KBIAS) of a byte sum s
+// (0 .. 1020) equals the fp32 FMA of those operands rounded once more to fp16, for every s (checked at start-up against
+// the exact table). Each tile row's 16 states come from one byte permute of the tile (three stream bytes per column), a
+// variable shift and a mask; the byte sum of state * MUL1 from one VNNI dot product with ones. The matrix is read in
+// memory order, in chunks of eight tile rows (the units the workers take; their count depends on K only): per chunk and
+// column, two fp32 FMA chains over the chunk's even and odd input rows, then the chunks' (even + odd) added in chunk
+// order. Not the device's order, and no dot2 rounding: the rows agree with the exact lane within the layer tolerance,
+// not bit for bit, and do not depend on the worker count.
+
+// per format: for tile row r and column c, the stream position, its first bit, and the byte-permute indices / shifts
+struct FastTables {
+    int TB = 0;
+    alignas(64) uint8_t idx[16][64];   // byte 4 c + q of row r: stream byte i + 2 - q (q < 3) of column c, as memory index
+    alignas(64) uint32_t sh[16][16];   // right shift that aligns the 16-bit state in the 24-bit window
+};
+
+const FastTables& fast_tables(int f)
+{
+    static FastTables tabs[4];
+    static std::once_flag once;
+    std::call_once(once, [] {
+        const TilePos& tp = tile_pos();
+        for (int fmt = 0; fmt < 4; ++fmt)
+        {
+            const Fmt F = fmt_of(fmt);
+            const int ring = 256 * F.KA + 16 * __builtin_popcount(F.MASK);
+            int start[256], acc = 0;
+            for (int i = 0; i < 256; ++i)
+            {
+                acc += F.KA + (int)((F.MASK >> (i & 15)) & 1u);
+                start[i] = ((acc - 16) % ring + ring) % ring;
+            }
+            FastTables& T = tabs[fmt];
+            T.TB = F.TB;
+            for (int p = 0; p < 256; ++p)
+            {
+                const int r = tp.row[p], c = tp.col[p], b = start[p], i = b >> 3;
+                // the tile's 32-bit words hold the stream MSB first: stream byte j is memory byte j ^ 3
+                for (int q = 0; q < 4; ++q) T.idx[r][4 * c + q] = (uint8_t)(((i + 2 - (q < 3 ? q : 2)) % F.TB) ^ 3);
+                T.sh[r][c] = (uint32_t)(8 - (b & 7));
+            }
+        }
+    });
+    return tabs[f];
+}
+
+// the codebook's fp32 evaluation against its exact value, for every byte sum
+bool fast_codebook_exact()
+{
+    const float kinv = h2f(0x1eee), kbias = h2f(0xc931);
+    for (int s = 0; s <= 1020; ++s)
+        if (f2h(std::fma((float)(1024 + s), kinv, kbias)) != d2h((1024.0 + s) * (double)kinv + (double)kbias)) return false;
+    return true;
+}
+
+bool fast_simd()
+{
+    static const bool have = [] {
+        __builtin_cpu_init();
+        return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+               __builtin_cpu_supports("avx512vbmi") && __builtin_cpu_supports("avx512vnni") && fast_codebook_exact();
+    }();
+    const char* v = getenv("BMX_CPU_LANE_SCALAR");
+    return have && !(v && *v == '1');
+}
+
+// The products of one chunk of tile rows: for tile rows [kt0, kt1) of the trellis matrix W [K/16][N/16] tiles and every
+// column n, pe[m][n] / po[m][n] = sums over the chunk's even / odd input rows k of W[k][n] x[m][k] (x fp32 [nr][K]), each
+// in k order (one fp32 FMA per product). The tiles are read in memory order (a tile row of N/16 tiles, then the next),
+// so the reads stream. pe, po: fp32 [nr][N], overwritten.
+constexpr int FAST_MAXR = 8;
+constexpr int FAST_CHUNK_TR = 8;      // tile rows per chunk (the chunk count depends on K only)
+
+template <int NR>
+__attribute__((target("avx512f,avx512bw,avx512vl,avx512vbmi,avx512vnni"))) void
+fast_chunk_simd(const uint8_t* tr, int fmt, int K, int N, const float* x, int kt0, int kt1, float* pe, float* po)
+{
+    const FastTables& T = fast_tables(fmt);
+    const int TB = T.TB, tn = N / 16;
+    const __mmask64 mlo = TB >= 64 ? ~0ull : ((1ull << TB) - 1),
+                    mhi = TB > 64 ? ((TB - 64 >= 64) ? ~0ull : ((1ull << (TB - 64)) - 1)) : 0;
+    const __m512i MUL1 = _mm512_set1_epi32((int)0x83DCD12Du), ONES = _mm512_set1_epi32(0x01010101),
+                  C1024 = _mm512_set1_epi32(1024), M16 = _mm512_set1_epi32(0xffff);
+    const __m512 KINV = _mm512_set1_ps(h2f(0x1eee)), KBIAS = _mm512_set1_ps(h2f(0xc931));
+    for (int m = 0; m < NR; ++m)
+        for (int n = 0; n < N; n += 16)
+        {
+            _mm512_storeu_ps(pe + (size_t)m * N + n, _mm512_setzero_ps());
+            _mm512_storeu_ps(po + (size_t)m * N + n, _mm512_setzero_ps());
+        }
+    for (int kt = kt0; kt < kt1; ++kt)
+    {
+        const uint8_t* row = tr + (size_t)kt * tn * TB;
+        const float* xk = x + kt * 16;
+        for (int nt = 0; nt < tn; ++nt)
+        {
+            const uint8_t* t = row + (size_t)nt * TB;
+            const __m512i lo = _mm512_maskz_loadu_epi8(mlo, t), hi = _mm512_maskz_loadu_epi8(mhi, t + 64);
+            __m512 ae[NR], ao[NR];
+            for (int m = 0; m < NR; ++m)
+            {
+                ae[m] = _mm512_loadu_ps(pe + (size_t)m * N + nt * 16);
+                ao[m] = _mm512_loadu_ps(po + (size_t)m * N + nt * 16);
+            }
+#pragma GCC unroll 16
+            for (int r = 0; r < 16; ++r)
+            {
+                __m512i v = _mm512_permutex2var_epi8(lo, _mm512_load_si512(T.idx[r]), hi);
+                v = _mm512_and_si512(_mm512_srlv_epi32(v, _mm512_load_si512(T.sh[r])), M16);
+                v = _mm512_mullo_epi32(v, MUL1);
+                const __m512 f = _mm512_fmadd_ps(_mm512_cvtepi32_ps(_mm512_dpbusd_epi32(C1024, v, ONES)), KINV, KBIAS);
+                const __m512 w = _mm512_cvtph_ps(_mm512_cvtps_ph(f, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+                for (int m = 0; m < NR; ++m)
+                {
+                    const __m512 xv = _mm512_set1_ps(xk[(size_t)m * K + r]);
+                    if (r & 1) ao[m] = _mm512_fmadd_ps(w, xv, ao[m]);
+                    else ae[m] = _mm512_fmadd_ps(w, xv, ae[m]);
+                }
+            }
+            for (int m = 0; m < NR; ++m)
+            {
+                _mm512_storeu_ps(pe + (size_t)m * N + nt * 16, ae[m]);
+                _mm512_storeu_ps(po + (size_t)m * N + nt * 16, ao[m]);
+            }
+        }
+    }
+}
+
+// the same sums without SIMD: the exact codebook table, then one FMA per product in the same order
+void fast_chunk_scalar(const uint8_t* tr, int fmt, int K, int N, const float* x, int nr, int kt0, int kt1, float* pe,
+                       float* po)
+{
+    const int tn = N / 16;
+    const Fmt F = fmt_of(fmt);
+    for (size_t i = 0; i < (size_t)nr * N; ++i) pe[i] = po[i] = 0.0f;
+    for (int kt = kt0; kt < kt1; ++kt)
+        for (int nt = 0; nt < tn; ++nt)
+        {
+            uint16_t blk[16 * 16];                              // column c, row r at c * 16 + r
+            dequant_rows(tr + ((size_t)kt * tn + nt) * F.TB, fmt, 16, 16, blk, 0, 1);
+            for (int m = 0; m < nr; ++m)
+                for (int c = 0; c < 16; ++c)
+                    for (int r = 0; r < 16; ++r)
+                    {
+                        float* a = ((r & 1) ? po : pe) + (size_t)m * N + nt * 16 + c;
+                        *a = std::fma(h2f(blk[c * 16 + r]), x[(size_t)m * K + kt * 16 + r], *a);
+                    }
+        }
+}
+
+void fast_chunk(const uint8_t* tr, int fmt, int K, int N, const float* x, int nr, int kt0, int kt1, float* pe, float* po)
+{
+    if (!fast_simd())
+    {
+        fast_chunk_scalar(tr, fmt, K, N, x, nr, kt0, kt1, pe, po);
+        return;
+    }
+    for (int m0 = 0; m0 < nr; m0 += FAST_MAXR)
+    {
+        const int k = nr - m0 < FAST_MAXR ? nr - m0 : FAST_MAXR;
+        const float* xm = x + (size_t)m0 * K;
+        float *em = pe + (size_t)m0 * N, *om = po + (size_t)m0 * N;
+        switch (k)
+        {
+            case 1: fast_chunk_simd<1>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+            case 2: fast_chunk_simd<2>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+            case 3: fast_chunk_simd<3>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+            case 4: fast_chunk_simd<4>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+            case 5: fast_chunk_simd<5>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+            case 6: fast_chunk_simd<6>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+            case 7: fast_chunk_simd<7>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+            default: fast_chunk_simd<8>(tr, fmt, K, N, xm, kt0, kt1, em, om); break;
+        }
+    }
+}
+
+// Chunk partials of a matrix: [chunk][2 (even, odd)][nr][N]. The product of column n is, chunk by chunk in order,
+// s = s + (pe + po) from s = 0.
+struct FastParts {
+    int nch = 0, nr = 0, N = 0;
+    std::vector<float> p;
+    void init(int K, int nr_, int N_)
+    {
+        nch = (K / 16 + FAST_CHUNK_TR - 1) / FAST_CHUNK_TR;
+        nr = nr_;
+        N = N_;
+        p.assign((size_t)nch * 2 * nr * N, 0.0f);
+    }
+    float* even(int c) { return p.data() + (size_t)c * 2 * nr * N; }
+    float* odd(int c) { return even(c) + (size_t)nr * N; }
+    // the products of row m, columns [n0, n0 + n)
+    void sum(int m, int n0, int n, float* out) const
+    {
+        for (int i = 0; i < n; ++i) out[i] = 0.0f;
+        for (int c = 0; c < nch; ++c)
+        {
+            const float* e = p.data() + (size_t)c * 2 * nr * N + (size_t)m * N + n0;
+            const float* o = e + (size_t)nr * N;
+            for (int i = 0; i < n; ++i) out[i] = out[i] + (e[i] + o[i]);
+        }
+    }
+    void run_chunk(const uint8_t* tr, int fmt, int K, const float* x, int c)
+    {
+        const int kt0 = c * FAST_CHUNK_TR, kt1 = std::min(K / 16, kt0 + FAST_CHUNK_TR);
+        fast_chunk(tr, fmt, K, N, x, nr, kt0, kt1, even(c), odd(c));
+    }
+};
+
+// H128 on 16-float vectors: the same additions and subtractions as had128, in the same stage order (same bits)
+__attribute__((target("avx512f,avx512bw,avx512vl,avx512vbmi,avx512vnni"))) void had128_simd(float* v)
+{
+    __m512 r[8];
+    for (int i = 0; i < 8; ++i) r[i] = _mm512_loadu_ps(v + 16 * i);
+    // spans 1, 2, 4, 8 inside a vector: new[e] = v[e] + v[e ^ s] where bit s of e is clear, v[e ^ s] - v[e] where set
+    const __m512i P1 = _mm512_set_epi32(14, 15, 12, 13, 10, 11, 8, 9, 6, 7, 4, 5, 2, 3, 0, 1);
+    const __m512i P2 = _mm512_set_epi32(13, 12, 15, 14, 9, 8, 11, 10, 5, 4, 7, 6, 1, 0, 3, 2);
+    const __m512i P4 = _mm512_set_epi32(11, 10, 9, 8, 15, 14, 13, 12, 3, 2, 1, 0, 7, 6, 5, 4);
+    const __m512i P8 = _mm512_set_epi32(7, 6, 5, 4, 3, 2, 1, 0, 15, 14, 13, 12, 11, 10, 9, 8);
+    const __m512i P[4] = { P1, P2, P4, P8 };
+    const __mmask16 HI[4] = { 0xAAAA, 0xCCCC, 0xF0F0, 0xFF00 };
+    for (int k = 0; k < 4; ++k)
+        for (int i = 0; i < 8; ++i)
+        {
+            const __m512 sw = _mm512_permutexvar_ps(P[k], r[i]);
+            r[i] = _mm512_mask_blend_ps(HI[k], _mm512_add_ps(r[i], sw), _mm512_sub_ps(sw, r[i]));
+        }
+    // spans 16, 32, 64: whole vectors
+    for (int s = 1; s < 8; s <<= 1)
+        for (int i = 0; i < 8; ++i)
+            if (!(i & s))
+            {
+                const __m512 a = r[i], b = r[i + s];
+                r[i] = _mm512_add_ps(a, b);
+                r[i + s] = _mm512_sub_ps(a, b);
+            }
+    for (int i = 0; i < 8; ++i) _mm512_storeu_ps(v + 16 * i, r[i]);
+}
+
+// 16 fp16 -> fp32, and fp32 -> the nearest fp16 (ties to even) back to fp32, in hardware
+__attribute__((target("avx512f,avx512bw,avx512vl,avx512vbmi,avx512vnni"))) void h2f16(const uint16_t* h, float* f, int n)
+{
+    for (int i = 0; i < n; i += 16)
+        _mm512_storeu_ps(f + i, _mm512_cvtph_ps(_mm256_loadu_si256(reinterpret_cast<const __m256i*>(h + i))));
+}
+__attribute__((target("avx512f,avx512bw,avx512vl,avx512vbmi,avx512vnni"))) void round16(float* f, int n)
+{
+    for (int i = 0; i < n; i += 16)
+        _mm512_storeu_ps(f + i, _mm512_cvtph_ps(_mm512_cvtps_ph(_mm512_loadu_ps(f + i), _MM_FROUND_TO_NEAREST_INT |
+                                                                                           _MM_FROUND_NO_EXC)));
+}
+
+// the helpers above where the host has them, else the exact lane's scalar steps (the same bits either way)
+void had128_any(float* v, bool simd)
+{
+    if (simd) had128_simd(v);
+    else had128(v);
+}
+void h2f_any(const uint16_t* h, float* f, int n, bool simd)
+{
+    if (simd) h2f16(h, f, n);
+    else
+        for (int i = 0; i < n; ++i) f[i] = h2f(h[i]);
+}
+void round16_any(float* f, int n, bool simd)
+{
+    if (simd) round16(f, n);
+    else
+        for (int i = 0; i < n; ++i) f[i] = h2f(f2h(f[i]));
+}
+
+// A pool of persistent workers for the fast mode: a call hands every worker one function (the caller runs share 0)
+// and returns when all have run it. Workers spin while calls keep coming and sleep after 2 ms without one.
+class LanePool {
+public:
+    explicit LanePool(int n) : n_(n)
+    {
+        for (int i = 1; i < n; ++i) th_.emplace_back([this, i] { worker(i); });
+    }
+    ~LanePool()
+    {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            quit_.store(true, std::memory_order_release);
+        }
+        cv_.notify_all();
+        for (auto& t : th_) t.join();
+    }
+    int size() const { return n_; }
+    void run(const std::function<void(int, int)>& fn)
+    {
+        job_ = &fn;
+        pending_.store(n_ - 1, std::memory_order_relaxed);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            gen_.fetch_add(1, std::memory_order_release);
+        }
+        cv_.notify_all();
+        fn(0, n_);
+        while (pending_.load(std::memory_order_acquire) > 0) _mm_pause();
+    }
+
+private:
+    void worker(int i)
+    {
+        uint64_t seen = 0;
+        auto last = std::chrono::steady_clock::now();
+        for (;;)
+        {
+            uint64_t g = gen_.load(std::memory_order_acquire);
+            while (g == seen && !quit_.load(std::memory_order_acquire))
+            {
+                if (std::chrono::steady_clock::now() - last > std::chrono::milliseconds(2))
+                {
+                    std::unique_lock<std::mutex> lk(mu_);
+                    cv_.wait(lk, [&] { return gen_.load(std::memory_order_acquire) != seen || quit_.load(); });
+                }
+                else _mm_pause();
+                g = gen_.load(std::memory_order_acquire);
+            }
+            if (quit_.load(std::memory_order_acquire)) return;
+            seen = g;
+            (*job_)(i, n_);
+            pending_.fetch_sub(1, std::memory_order_acq_rel);
+            last = std::chrono::steady_clock::now();
+        }
+    }
+    const int n_;
+    std::vector<std::thread> th_;
+    std::atomic<uint64_t> gen_{0};
+    std::atomic<int> pending_{0};
+    std::atomic<bool> quit_{false};
+    const std::function<void(int, int)>* job_ = nullptr;
+    std::mutex mu_;
+    std::condition_variable cv_;
+};
+
+std::mutex g_pool_mu;
+std::unique_ptr<LanePool> g_pool;
+
+// units [0, n) over the pool's workers, in contiguous shares
+void pool_units(LanePool& pool, int n, const std::function<void(int)>& unit)
+{
+    pool.run([&](int w, int nw) {
+        const int a = (int)((int64_t)n * w / nw), b = (int)((int64_t)n * (w + 1) / nw);
+        for (int u = a; u < b; ++u) unit(u);
+    });
+}
+
+
 }  // namespace
 
 extern "C" int bmx_cpu_expert_rows(const bmx_cpu_expert* ex, int H, int I, const uint16_t* x, int nr, int ks_gu,
@@ -665,6 +1022,76 @@ extern "C" int bmx_cpu_expert_rows(const bmx_cpu_expert* ex, int H, int I, const
             had128(yv);
             for (int i = 0; i < 128; ++i) y[(size_t)m * H + cb + i] = (yv[i] * R_SCALE) * h2f(ex->svh[2][cb + i]);
         }
+    return BMX_OK;
+}
+
+extern "C" int bmx_cpu_expert_rows_fast(const bmx_cpu_expert* ex, int H, int I, const uint16_t* x, int nr, int act,
+                                        int gated, float act_limit, float* y, int threads)
+{
+    if (!ex || !x || !y || nr < 0 || H <= 0 || I <= 0 || H % 128 || I % 128)
+        return bmx::set_error(BMX_ERR_ARG, "bmx_cpu_expert_rows_fast: bad arguments (H, I multiples of 128)");
+    for (int m = 0; m < 3; ++m)
+        if (!ex->tr[m] || !ex->suh[m] || !ex->svh[m] || ex->fmt[m] < BMX_TF_K2 || ex->fmt[m] > BMX_TF_K4)
+            return bmx::set_error(BMX_ERR_ARG, "bmx_cpu_expert_rows_fast: matrix %d has no data or an unknown format", m);
+    if (nr == 0) return BMX_OK;
+    const int hw = (int)std::thread::hardware_concurrency();
+    threads = threads < 1 ? 1 : (hw > 0 && threads > hw ? hw : threads);
+    std::lock_guard<std::mutex> lk(g_pool_mu);       // one call at a time on the pool
+    if (!g_pool || g_pool->size() != threads) g_pool = std::make_unique<LanePool>(threads);
+    // input rotation per matrix (the exact lane's steps), as fp32: units (row, matrix, 128-block) over the pool
+    const bool simd = fast_simd();
+    LanePool& pool = *g_pool;
+    std::vector<float> xg((size_t)nr * H), xu((size_t)nr * H);
+    pool_units(pool, nr * 2 * (H / 128), [&](int u) {
+        const int b = 128 * (u % (H / 128)), mat = (u / (H / 128)) & 1, m = u / (H / 128) / 2;
+        float v[128], su[128];
+        h2f_any(x + (size_t)m * H + b, v, 128, simd);
+        h2f_any(ex->suh[mat] + b, su, 128, simd);
+        for (int i = 0; i < 128; ++i) v[i] = v[i] * su[i];
+        had128_any(v, simd);
+        for (int i = 0; i < 128; ++i) v[i] = v[i] * R_SCALE;
+        round16_any(v, 128, simd);
+        std::memcpy((mat ? xu.data() : xg.data()) + (size_t)m * H + b, v, sizeof(v));
+    });
+    FastParts pg, pu;
+    pg.init(H, nr, I);
+    pu.init(H, nr, I);
+    pool_units(pool, 2 * pg.nch, [&](int u) {
+        if (u < pg.nch) pg.run_chunk(ex->tr[0], ex->fmt[0], H, xg.data(), u);
+        else pu.run_chunk(ex->tr[1], ex->fmt[1], H, xu.data(), u - pg.nch);
+    });
+    // gate / up epilogue (the exact lane's steps on these sums) -> down-input rows: units (row, 128-block)
+    std::vector<float> arow((size_t)nr * I);
+    pool_units(pool, nr * (I / 128), [&](int u) {
+        const int cb = 128 * (u % (I / 128)), m = u / (I / 128);
+        float g[128], v[128], a[128], s0[128], s1[128], s2[128];
+        pg.sum(m, cb, 128, g);
+        pu.sum(m, cb, 128, v);
+        round16_any(g, 128, simd);
+        round16_any(v, 128, simd);
+        had128_any(g, simd);
+        had128_any(v, simd);
+        h2f_any(ex->svh[0] + cb, s0, 128, simd);
+        h2f_any(ex->svh[1] + cb, s1, 128, simd);
+        h2f_any(ex->suh[2] + cb, s2, 128, simd);
+        for (int i = 0; i < 128; ++i)
+            a[i] = act_gate(act, gated, (g[i] * R_SCALE) * s0[i], (v[i] * R_SCALE) * s1[i], act_limit) * s2[i];
+        had128_any(a, simd);
+        for (int i = 0; i < 128; ++i) a[i] = a[i] * R_SCALE;
+        round16_any(a, 128, simd);
+        std::memcpy(arow.data() + (size_t)m * I + cb, a, sizeof(a));
+    });
+    FastParts pd;
+    pd.init(I, nr, H);
+    pool_units(pool, pd.nch, [&](int u) { pd.run_chunk(ex->tr[2], ex->fmt[2], I, arow.data(), u); });
+    pool_units(pool, nr * (H / 128), [&](int u) {
+        const int cb = 128 * (u % (H / 128)), m = u / (H / 128);
+        float yv[128], sv[128];
+        pd.sum(m, cb, 128, yv);
+        had128_any(yv, simd);
+        h2f_any(ex->svh[2] + cb, sv, 128, simd);
+        for (int i = 0; i < 128; ++i) y[(size_t)m * H + cb + i] = (yv[i] * R_SCALE) * sv[i];
+    });
     return BMX_OK;
 }
 

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define BMX_ABI_VERSION 4
+#define BMX_ABI_VERSION 5
 
 typedef void* bmx_stream_t; /* hipStream_t */
 
@@ -295,6 +295,10 @@ int bmx_copy_agent_destroy(bmx_copy_agent* agent);
  * error without launching, and the slot contents of admissions whose copies had not completed are not trusted (the
  * layer calls that read them are to be discarded). Sequence numbers are 64-bit and never wrap. */
 int bmx_copy_agent_status(const bmx_copy_agent* agent, int64_t* stats);
+/* The residency planner's counts: stats[5] = requests answered, experts put on the CPU lane (summed over requests),
+ * CPU jobs done (one per request with picks on the CPU lane), microseconds the CPU lane's worker spent on them, the worker's running mean per CPU pick in
+ * nanoseconds (0 before its first job with picks; what policy cpu_measured prices a CPU expert at). */
+int bmx_copy_agent_plan_stats(const bmx_copy_agent* agent, int64_t* stats);
 /* Failure-path control (the reference's controller has no counterpart; for tests that force a failure from the host):
  * hold >= 0 sets whether the agent's thread reads new records (1: it stops reading, so the waits run into their limit);
  * wait_limit_us > 0 sets the limit of the device-side waits launched after the call (default 5 s). */
@@ -325,6 +329,16 @@ typedef struct bmx_cpu_expert {
 } bmx_cpu_expert;
 int bmx_cpu_expert_rows(const bmx_cpu_expert* ex, int H, int I, const uint16_t* x_fp16, int nr, int ks_gu, int ks_dn,
                         int grouped_gu, int act, int gated, float act_limit, float* y_rows, int threads);
+/* The CPU lane's fast mode: the same y rows within the layer tolerance, not bit for bit (the reference's lane is not
+ * bit-exact either; its host decode, engine/kernels/nv2/ft_core.h, is what this replaces for throughput). The trellis
+ * decode gives the device's fp16 weights exactly (the codebook's fp32 FMA rounded once to fp16 equals its exact value for
+ * every byte sum, checked at start-up); the products accumulate in fp32 FMAs over chunks of eight tile rows read in
+ * memory order (the result does not depend on threads), without the device's k-splits or dot2 rounding; the rotations,
+ * activation and roundings between the GEMVs are the exact lane's. AVX-512
+ * (BW, VBMI, VNNI) when the host has it, else scalar. threads: a pool of that many persistent workers (the calling
+ * thread is one), kept for later calls with the same count; calls are serialised on it. */
+int bmx_cpu_expert_rows_fast(const bmx_cpu_expert* ex, int H, int I, const uint16_t* x_fp16, int nr, int act,
+                             int gated, float act_limit, float* y_rows, int threads);
 /* The device plan of a decode-path call of T tokens: k-splits of the gate / up and down GEMVs, and whether the gate / up
  * epilogue sums the splits in four interleaved groups (small launches) or in sequence. */
 int bmx_decode_splits(const bmx_moe_desc* desc, int T, int* ks_gu, int* ks_dn, int* grouped_gu);
@@ -362,7 +376,10 @@ enum { BMX_LANE_VRAM = 0, BMX_LANE_ADMIT = 1, BMX_LANE_HOME = 2, BMX_LANE_CPU = 
  * is then no later than with the GPU taking it; else to the GPU (BMX_LANE_HOME or BMX_LANE_ADMIT). Default (no policy
  * set): cpu_on 0, home_single 0, every miss BMX_LANE_ADMIT. */
 typedef struct bmx_plan_policy {
-    int32_t cpu_on, max_cpu, home_single, reserved;
+    int32_t cpu_on, max_cpu, home_single;
+    int32_t cpu_fast;          /* 1: the agent's CPU jobs use bmx_cpu_expert_rows_fast; 0: the exact lane */
+    int32_t cpu_measured;      /* 1: a CPU expert costs the worker's measured mean per pick (a running mean over its
+                                  jobs, 1/8 weight to the newest) in place of cpu_expert_us once a job has run */
     double gpu_base_us, gpu_hit_us, gpu_home_us, gpu_admit_us;
     double cpu_base_us, cpu_expert_us, cpu_token_us;
 } bmx_plan_policy;
@@ -370,8 +387,9 @@ int bmx_copy_agent_plan(bmx_copy_agent* agent, const bmx_plan_policy* policy);
 /* The CPU lane of an agent: experts[L * E] host copies of every layer's experts (trellis, scales, formats; the shared
  * expert never goes to the CPU), desc: the layers' shape and activation (experts, shared and fresh ignored), threads:
  * worker threads per job. Without it the planner puts nothing on the CPU lane. A job computes each CPU pick's y row of
- * its token with bmx_cpu_expert_rows (bit for bit the GPU decode path's row for the call's T) and sums w * y in pick
- * order into the token's partial (fp32 [T][H]). */
+ * its token with bmx_cpu_expert_rows (bit for bit the GPU decode path's row for the call's T), or with
+ * bmx_cpu_expert_rows_fast when the policy's cpu_fast is set, and sums w * y in pick order into the token's partial
+ * (fp32 [T][H]). */
 int bmx_copy_agent_cpu_lane(bmx_copy_agent* agent, const bmx_moe_desc* desc, const bmx_cpu_expert* experts, int threads);
 int bmx_slot_step_planned(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const int64_t* sel,
                           const void* w_fp16, int T, int topk, int64_t first, int admit, const void* x_fp16,

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_host_side_checks():
     import bmx
     L = bmx.lib()
-    assert L.bmx_abi_version() == 4
+    assert L.bmx_abi_version() == 5
     assert [L.bmx_tile_bytes(f) for f in range(4)] == [64, 80, 96, 128] and L.bmx_tile_bytes(9) == -1
     assert L.bmx_exl3_dequant(None, 7, 16, 16, None, None) == bmx._lib.BMX_ERR_ARG
     assert b"format" in L.bmx_last_error()

@@ -83,3 +83,59 @@ def test_cpu_lane_vector_equals_scalar(monkeypatch, fmts, ks):
     monkeypatch.setenv("BMX_CPU_LANE_SCALAR", "1")
     y_sca = cpu_lane.expert_rows(ex, H, I, x, ks[0], ks[1], 1, 2, True, 0.0, threads=3)
     assert np.array_equal(y_vec.view(np.uint32), y_sca.view(np.uint32))
+
+
+# ---- fast mode ----------------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmts,nr", [((2, 0, 3), 1), ((1, 1, 1), 3), ((3, 2, 0), 9), ((0, 3, 1), 8)])
+def test_fast_lane_vector_equals_scalar(monkeypatch, fmts, nr):
+    """The fast mode's AVX-512 decode (byte permute, shift, hash, VNNI byte sum, fp32 FMA, fp16 rounding) against its
+    scalar path, which decodes through the exact codebook table: the two sum each column in the same order, so equal
+    bits mean every decoded weight equals the exact codebook's (where the host has AVX-512 VBMI and VNNI)."""
+    from bmx import cpu_lane
+    H, I = 512, 384
+    ex = host_expert(H, I, fmts, seed=31 + nr)
+    x = np.random.default_rng(nr).standard_normal((nr, H)).astype(np.float16) * np.float16(3.0)
+    y_vec = cpu_lane.expert_rows_fast(ex, H, I, x, 0, True, 0.0, threads=3)
+    monkeypatch.setenv("BMX_CPU_LANE_SCALAR", "1")
+    y_sca = cpu_lane.expert_rows_fast(ex, H, I, x, 0, True, 0.0, threads=3)
+    assert np.array_equal(y_vec.view(np.uint32), y_sca.view(np.uint32))
+    assert np.abs(y_vec).max() > 0
+
+
+@pytest.mark.parametrize("act,gated,limit", [(0, True, 0.0), (1, True, 0.0), (2, True, 0.0), (3, True, 7.0), (0, False, 0.0)])
+def test_fast_lane_rows_match_oracle(oracle, act, gated, limit):
+    """Fast-mode expert rows vs the oracle's fp64-accumulating expert forward: within the layer tolerance."""
+    from bmx import cpu_lane
+    H, I = 512, 256
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, H)).astype(np.float16)
+    for e, fmts in enumerate([(2, 0, 3), (1, 1, 1), (3, 3, 3)]):
+        ex = host_expert(H, I, fmts, seed=40 + e)
+        y = cpu_lane.expert_rows_fast(ex, H, I, x, act, gated, limit, threads=4)
+        for m in range(3):
+            yo = oracle.expert_forward(ex, H, I, x[m], act, gated, limit)[0]
+            err = np.sqrt(np.mean((y[m] - yo) ** 2)) / max(1e-30, np.sqrt(np.mean(yo ** 2)))
+            assert err < 1e-3 and np.abs(y[m] - yo).max() < 1e-2, (e, m, err)
+
+
+def test_fast_lane_close_to_exact_lane():
+    """A C2-shaped expert (H 4096, I 1536, K 3): the fast mode's rows within the layer tolerance of the exact lane's,
+    and repeated calls (the worker pool kept between them, its size changed) give the same bits."""
+    from bmx import cpu_lane
+    H, I = 4096, 1536
+    ex = host_expert(H, I, (2, 2, 2), seed=77)
+    x = np.random.default_rng(78).standard_normal((2, H)).astype(np.float16)
+    ye = cpu_lane.expert_rows(ex, H, I, x, 16, 4, 1, threads=8)
+    yf = cpu_lane.expert_rows_fast(ex, H, I, x, threads=8)
+    err = np.sqrt(np.mean((yf - ye) ** 2)) / np.sqrt(np.mean(ye ** 2))
+    assert err < 1e-3 and np.abs(yf - ye).max() < 1e-2, err
+    assert np.array_equal(cpu_lane.expert_rows_fast(ex, H, I, x, threads=8).view(np.uint32), yf.view(np.uint32))
+    assert np.array_equal(cpu_lane.expert_rows_fast(ex, H, I, x, threads=3).view(np.uint32), yf.view(np.uint32))
+
+
+def test_fast_lane_rejects_bad_shapes():
+    import bmx
+    from bmx import cpu_lane
+    with pytest.raises(bmx.BmxError, match="multiples of 128"):
+        cpu_lane.expert_rows_fast(host_expert(256, 128, (2, 2, 2), 1), 200, 128, np.zeros((1, 200), np.float16))

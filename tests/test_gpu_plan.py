@@ -144,3 +144,87 @@ def test_plan_reply_timeout_is_reported(cuda):
         slots.check()
     bmx._lib.check(lib.bmx_copy_agent_control(slots.agent, 0, 0), "bmx_copy_agent_control")
     slots.close()
+
+
+def test_cpu_lane_fast_partial_added(cuda, oracle):
+    """The same layer calls with the CPU lane in its fast mode (policy cpu_fast): out = the GPU's combine of the masked
+    selection + the fast lane's partial, within the layer tolerance of the all-GPU rows' combine (the fast mode keeps the
+    exact weights but not the device's summation order)."""
+    import bmx
+    from bmx import synth
+    Lyr, E, H, I, topk, first = 2, 16, 256, 128, 4, 0
+    dev_layers = small_layers(Lyr, E, H, I, 150, "device")
+    host_layers = small_layers(Lyr, E, H, I, 150, "host")
+    slots = bmx.ExpertSlots(host_layers, 6, maxj=2, copies="dma")
+    slots.cpu_lane(topk, threads=4)
+    slots.plan(dict(cpu_on=1, max_cpu=2, cpu_fast=1, gpu_base_us=1.0, gpu_admit_us=1.0))
+    kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
+    ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
+    st_layers = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(Lyr)]
+    rng = np.random.default_rng(31)
+    ncpu = 0
+    for step in range(8):
+        li = step % Lyr
+        T = 1 + step % 3
+        x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float16)).cuda()
+        lg = torch.from_numpy(synth.zipf_logits(T, E, 1.1, seed=500 + step)).cuda()
+        m = st_layers[li]
+        sel, w = m.routing_fn(T, None, x, {"logits": lg})
+        sel_g, w_g, flag = m.layer(li, sel, w, x, T)
+        assert flag
+        out = m.cpu_split_combine(m.combine(m.run_bszN(x, sel_g, w_g, bmx.PATH_DECODE)), None, False, None)
+        want = ref_layers[li].run_bszN(x, sel, w, bmx.PATH_DECODE)
+        torch.cuda.synchronize()
+        got, want = out.cpu().numpy(), want.cpu().numpy()
+        s, sg = sel.cpu().numpy().ravel(), sel_g.cpu().numpy().ravel()
+        n = int(np.sum((sg == -1) & (s != -1)))
+        ncpu += len(set(s[(sg == -1) & (s != -1)].tolist()))       # the planner counts experts, not picks
+        err = float(np.sqrt(np.mean((got - want) ** 2)) / np.sqrt(np.mean(want ** 2)))
+        say("fast cpu lane step", step, "layer", li, "T", T, "cpu picks", n, "max diff", float(np.abs(got - want).max()),
+            "rel rms", err)
+        assert np.abs(got - want).max() < 1e-2 and err < 1e-3, step
+    assert ncpu > 0
+    st = slots.plan_stats()
+    say("plan stats", st)
+    assert st[1] == ncpu and st[2] >= 1
+    slots.close()
+
+
+def test_plan_measured_cpu_cost(cuda, oracle):
+    """Policy cpu_measured: with every cost 0 the first call's misses go to the CPU lane (its finish is then no later);
+    once its job has run the planner prices a CPU expert at the worker's measured time per pick, which no longer ties
+    with a GPU costing 0, so later calls put nothing there. The outputs stay the all-GPU rows' within the layer
+    tolerance throughout."""
+    import bmx
+    from bmx import synth
+    Lyr, E, H, I, topk = 2, 16, 256, 128, 4
+    dev_layers = small_layers(Lyr, E, H, I, 160, "device")
+    host_layers = small_layers(Lyr, E, H, I, 160, "host")
+    slots = bmx.ExpertSlots(host_layers, 6, maxj=2, copies="dma")
+    slots.cpu_lane(topk, threads=2)
+    slots.plan(dict(cpu_on=1, max_cpu=2, cpu_fast=1, cpu_measured=1))
+    kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
+    ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
+    st_layers = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(Lyr)]
+    rng = np.random.default_rng(37)
+    seen = []
+    for step in range(6):
+        li = step % Lyr
+        x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float16)).cuda()
+        lg = torch.from_numpy(synth.zipf_logits(1, E, 1.1, seed=700 + step)).cuda()
+        m = st_layers[li]
+        sel, w = m.routing_fn(1, None, x, {"logits": lg})
+        sel_g, w_g, flag = m.layer(li, sel, w, x, 1)
+        assert flag
+        out = m.cpu_split_combine(m.combine(m.run_bszN(x, sel_g, w_g, bmx.PATH_DECODE)), None, False, None)
+        want = ref_layers[li].run_bszN(x, sel, w, bmx.PATH_DECODE)
+        torch.cuda.synchronize()
+        got, want = out.cpu().numpy(), want.cpu().numpy()
+        err = float(np.sqrt(np.mean((got - want) ** 2)) / np.sqrt(np.mean(want ** 2)))
+        st = slots.plan_stats()
+        seen.append(st)
+        say("measured-cost step", step, "plan stats", st, "rel rms", err)
+        assert np.abs(got - want).max() < 1e-2 and err < 1e-3, step
+    assert seen[0][1] == 2 and seen[0][2] >= 1 and seen[0][4] > 0      # the first call's two misses ran on the CPU
+    assert all(s[1] == seen[0][1] for s in seen[1:])                   # and, priced as measured, nothing after it
+    slots.close()
