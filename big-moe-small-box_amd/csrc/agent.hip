@@ -89,7 +89,8 @@ struct bmx_copy_agent {
     std::deque<bmx::CpuJob> cpu_q;
     std::atomic<int64_t> cpu_jobs{0};
     std::atomic<int64_t> cpu_ns{0};          // host time the CPU worker spent computing jobs
-    double cpu_pick_us = 0.0;                // running mean of the worker's time per pick (under plan_mu)
+    double cpu_pick_us[2] = {0.0, 0.0};      // running mean of the worker's time per pick, exact / fast mode
+                                             // (under plan_mu; the fast one seeded at set-up)
 };
 
 namespace bmx {
@@ -202,7 +203,8 @@ static void plan_reply(bmx_copy_agent* a, const PlanReq& r, PlanRep& p, CpuJob* 
     {
         std::lock_guard<std::mutex> lk(a->plan_mu);
         pol = a->policy;
-        if (pol.cpu_measured && a->cpu_pick_us > 0.0) pol.cpu_expert_us = a->cpu_pick_us;
+        const double mean = a->cpu_pick_us[pol.cpu_fast ? 1 : 0];
+        if (pol.cpu_measured && mean > 0.0) pol.cpu_expert_us = mean;
     }
     const int nu = r.nu;
     const bool cpu_ok = pol.cpu_on && a->cpu_ready && r.has_x && r.np <= BMX_PLAN_MAXP && r.ntok <= BMX_PLAN_MAXT;
@@ -275,9 +277,10 @@ static void cpu_loop(bmx_copy_agent* a)
         const int slot = ring_index(job.seq), n = (int)job.pick_e.size();
         const auto t_job = std::chrono::steady_clock::now();
         bool ok = true;
+        int fast = 0;
         if (n > 0)
         {
-            int ks_gu = 0, ks_dn = 0, grouped = 0, fast = 0;
+            int ks_gu = 0, ks_dn = 0, grouped = 0;
             {
                 std::lock_guard<std::mutex> lk(a->plan_mu);
                 fast = a->policy.cpu_fast;
@@ -314,7 +317,8 @@ static void cpu_loop(bmx_copy_agent* a)
         {
             const double per = 1e-3 * (double)ns / n;
             std::lock_guard<std::mutex> lk(a->plan_mu);
-            a->cpu_pick_us = a->cpu_pick_us > 0.0 ? a->cpu_pick_us + (per - a->cpu_pick_us) / 8.0 : per;
+            double& mean = a->cpu_pick_us[fast ? 1 : 0];
+            mean = mean > 0.0 ? mean + (per - mean) / 8.0 : per;
         }
         __atomic_store_n(&a->sh->cpu_done, job.seq, __ATOMIC_RELEASE);
     }
@@ -641,7 +645,7 @@ int bmx_copy_agent_plan_stats(const bmx_copy_agent* a, int64_t* stats)
     stats[3] = a->cpu_ns.load() / 1000;
     {
         std::lock_guard<std::mutex> lk(a->plan_mu);
-        stats[4] = (int64_t)(a->cpu_pick_us * 1e3);
+        stats[4] = (int64_t)(a->cpu_pick_us[a->policy.cpu_fast ? 1 : 0] * 1e3);
     }
     return BMX_OK;
 }
@@ -722,6 +726,29 @@ int bmx_copy_agent_cpu_lane(bmx_copy_agent* a, const bmx_moe_desc* desc, const b
     if (a->cpu_ready) return set_error(BMX_ERR_ARG, "bmx_copy_agent_cpu_lane: already set up");
     if (desc->E != a->t.E || desc->H != a->t.H || desc->I != a->t.I || desc->H % 128 || desc->I % 128)
         return set_error(BMX_ERR_ARG, "bmx_copy_agent_cpu_lane: the descriptor's shape is not the slot table's");
+    // fast-mode rows through the first experts of layer 0: the worker pool, tables and buffers are set up here rather
+    // than in the first job, and the median time of the rows after the first seeds the fast mode's measured cost
+    // (policy cpu_measured), which a single slow first job would otherwise hold high with no job run to correct it
+    double seed_us = 0.0;
+    {
+        std::vector<uint16_t> z((size_t)desc->H, 0);
+        std::vector<float> yz((size_t)desc->H);
+        std::vector<double> ts;
+        const int ne = std::min(desc->E, 5);
+        for (int e = 0; e < ne; ++e)
+        {
+            const auto t0 = std::chrono::steady_clock::now();
+            const int rc = bmx_cpu_expert_rows_fast(&experts[e], desc->H, desc->I, z.data(), 1, desc->act, desc->gated,
+                                                    desc->act_limit, yz.data(), threads < 1 ? 1 : threads);
+            if (rc) return rc;
+            if (e > 0) ts.push_back(std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count());
+        }
+        if (!ts.empty())
+        {
+            std::sort(ts.begin(), ts.end());
+            seed_us = ts[ts.size() / 2];
+        }
+    }
     const size_t K = (size_t)a->t.L * a->t.E, n = (size_t)AG_RING * BMX_PLAN_MAXT * desc->H;
     void *x = nullptr, *xd = nullptr, *pp = nullptr, *pd = nullptr;
     if (hipHostMalloc(&x, n * 2, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess ||
@@ -741,6 +768,10 @@ int bmx_copy_agent_cpu_lane(bmx_copy_agent* a, const bmx_moe_desc* desc, const b
     a->cpu_part = static_cast<float*>(pp);
     a->cpu_part_dev = static_cast<float*>(pd);
     a->job_of.assign(AG_RING, 0);
+    {
+        std::lock_guard<std::mutex> lk(a->plan_mu);
+        a->cpu_pick_us[1] = seed_us;
+    }
     a->cpu_ready = true;
     a->cpu_th = std::thread(cpu_loop, a);
     return BMX_OK;

@@ -586,9 +586,9 @@ void parallel_cols(int N, int threads, F fn)
 // (0 .. 1020) equals the fp32 FMA of those operands rounded once more to fp16, for every s (checked at start-up against
 // the exact table). Each tile row's 16 states come from one byte permute of the tile (three stream bytes per column), a
 // variable shift and a mask; the byte sum of state * MUL1 from one VNNI dot product with ones. The matrix is read in
-// memory order, in chunks of eight tile rows (the units the workers take; their count depends on K only): per chunk and
-// column, two fp32 FMA chains over the chunk's even and odd input rows, then the chunks' (even + odd) added in chunk
-// order. Not the device's order, and no dot2 rounding: the rows agree with the exact lane within the layer tolerance,
+// memory order, in chunks of up to eight tile rows (the units the workers take; their size depends on K only): per
+// chunk and column, two fp32 FMA chains over the chunk's even and odd input rows, then the chunks' (even + odd) added in
+// chunk order. Not the device's order, and no dot2 rounding: the rows agree with the exact lane within the layer tolerance,
 // not bit for bit, and do not depend on the worker count.
 
 // per format: for tile row r and column c, the stream position, its first bit, and the byte-permute indices / shifts
@@ -653,7 +653,9 @@ bool fast_simd()
 // in k order (one fp32 FMA per product). The tiles are read in memory order (a tile row of N/16 tiles, then the next),
 // so the reads stream. pe, po: fp32 [nr][N], overwritten.
 constexpr int FAST_MAXR = 8;
-constexpr int FAST_CHUNK_TR = 8;      // tile rows per chunk (the chunk count depends on K only)
+// tile rows per chunk: at most 8, fewer when K is short, so that a matrix has 32 chunks or more to hand out (a function
+// of K only, so the sums do not depend on the worker count)
+inline int fast_chunk_rows(int K) { return std::max(1, std::min(8, K / 16 / 32)); }
 
 template <int NR>
 __attribute__((target("avx512f,avx512bw,avx512vl,avx512vbmi,avx512vnni"))) void
@@ -758,17 +760,20 @@ void fast_chunk(const uint8_t* tr, int fmt, int K, int N, const float* x, int nr
     }
 }
 
-// Chunk partials of a matrix: [chunk][2 (even, odd)][nr][N]. The product of column n is, chunk by chunk in order,
-// s = s + (pe + po) from s = 0.
+// Chunk partials of a matrix: [chunk][2 (even, odd)][nr][N], each chunk's written whole by its unit. The product of
+// column n is, chunk by chunk in order, s = s + (pe + po) from s = 0. The buffer persists between calls (it only grows):
+// a fresh zero-filled one per call cost more than the products on many threads.
 struct FastParts {
-    int nch = 0, nr = 0, N = 0;
+    int nch = 0, nr = 0, N = 0, tr = 8;
     std::vector<float> p;
     void init(int K, int nr_, int N_)
     {
-        nch = (K / 16 + FAST_CHUNK_TR - 1) / FAST_CHUNK_TR;
+        tr = fast_chunk_rows(K);
+        nch = (K / 16 + tr - 1) / tr;
         nr = nr_;
         N = N_;
-        p.assign((size_t)nch * 2 * nr * N, 0.0f);
+        const size_t need = (size_t)nch * 2 * nr * N;
+        if (p.size() < need) p.resize(need);
     }
     float* even(int c) { return p.data() + (size_t)c * 2 * nr * N; }
     float* odd(int c) { return even(c) + (size_t)nr * N; }
@@ -783,10 +788,10 @@ struct FastParts {
             for (int i = 0; i < n; ++i) out[i] = out[i] + (e[i] + o[i]);
         }
     }
-    void run_chunk(const uint8_t* tr, int fmt, int K, const float* x, int c)
+    void run_chunk(const uint8_t* w, int fmt, int K, const float* x, int c)
     {
-        const int kt0 = c * FAST_CHUNK_TR, kt1 = std::min(K / 16, kt0 + FAST_CHUNK_TR);
-        fast_chunk(tr, fmt, K, N, x, nr, kt0, kt1, even(c), odd(c));
+        const int kt0 = c * tr, kt1 = std::min(K / 16, kt0 + tr);
+        fast_chunk(w, fmt, K, N, x, nr, kt0, kt1, even(c), odd(c));
     }
 };
 
@@ -920,13 +925,21 @@ private:
 
 std::mutex g_pool_mu;
 std::unique_ptr<LanePool> g_pool;
+// the fast mode's buffers, reused by every call (under g_pool_mu)
+struct FastScratch {
+    FastParts pg, pu, pd;
+    std::vector<float> xg, xu, arow;
+};
+FastScratch g_fast;
 
-// units [0, n) over the pool's workers, in contiguous shares
+// units [0, n) over the pool's workers, each taking the next unit left (a worker slowed by other work takes fewer);
+// every unit writes its own outputs, so which worker ran it changes nothing
 void pool_units(LanePool& pool, int n, const std::function<void(int)>& unit)
 {
-    pool.run([&](int w, int nw) {
-        const int a = (int)((int64_t)n * w / nw), b = (int)((int64_t)n * (w + 1) / nw);
-        for (int u = a; u < b; ++u) unit(u);
+    std::atomic<int> next{0};
+    pool.run([&](int, int) {
+        for (int u = next.fetch_add(1, std::memory_order_relaxed); u < n; u = next.fetch_add(1, std::memory_order_relaxed))
+            unit(u);
     });
 }
 
@@ -1041,7 +1054,11 @@ extern "C" int bmx_cpu_expert_rows_fast(const bmx_cpu_expert* ex, int H, int I, 
     // input rotation per matrix (the exact lane's steps), as fp32: units (row, matrix, 128-block) over the pool
     const bool simd = fast_simd();
     LanePool& pool = *g_pool;
-    std::vector<float> xg((size_t)nr * H), xu((size_t)nr * H);
+    FastScratch& sc = g_fast;
+    if (sc.xg.size() < (size_t)nr * H) sc.xg.resize((size_t)nr * H);
+    if (sc.xu.size() < (size_t)nr * H) sc.xu.resize((size_t)nr * H);
+    if (sc.arow.size() < (size_t)nr * I) sc.arow.resize((size_t)nr * I);
+    float *xg = sc.xg.data(), *xu = sc.xu.data(), *arow = sc.arow.data();
     pool_units(pool, nr * 2 * (H / 128), [&](int u) {
         const int b = 128 * (u % (H / 128)), mat = (u / (H / 128)) & 1, m = u / (H / 128) / 2;
         float v[128], su[128];
@@ -1051,17 +1068,16 @@ extern "C" int bmx_cpu_expert_rows_fast(const bmx_cpu_expert* ex, int H, int I, 
         had128_any(v, simd);
         for (int i = 0; i < 128; ++i) v[i] = v[i] * R_SCALE;
         round16_any(v, 128, simd);
-        std::memcpy((mat ? xu.data() : xg.data()) + (size_t)m * H + b, v, sizeof(v));
+        std::memcpy((mat ? xu : xg) + (size_t)m * H + b, v, sizeof(v));
     });
-    FastParts pg, pu;
+    FastParts &pg = sc.pg, &pu = sc.pu;
     pg.init(H, nr, I);
     pu.init(H, nr, I);
     pool_units(pool, 2 * pg.nch, [&](int u) {
-        if (u < pg.nch) pg.run_chunk(ex->tr[0], ex->fmt[0], H, xg.data(), u);
-        else pu.run_chunk(ex->tr[1], ex->fmt[1], H, xu.data(), u - pg.nch);
+        if (u < pg.nch) pg.run_chunk(ex->tr[0], ex->fmt[0], H, xg, u);
+        else pu.run_chunk(ex->tr[1], ex->fmt[1], H, xu, u - pg.nch);
     });
     // gate / up epilogue (the exact lane's steps on these sums) -> down-input rows: units (row, 128-block)
-    std::vector<float> arow((size_t)nr * I);
     pool_units(pool, nr * (I / 128), [&](int u) {
         const int cb = 128 * (u % (I / 128)), m = u / (I / 128);
         float g[128], v[128], a[128], s0[128], s1[128], s2[128];
@@ -1079,11 +1095,11 @@ extern "C" int bmx_cpu_expert_rows_fast(const bmx_cpu_expert* ex, int H, int I, 
         had128_any(a, simd);
         for (int i = 0; i < 128; ++i) a[i] = a[i] * R_SCALE;
         round16_any(a, 128, simd);
-        std::memcpy(arow.data() + (size_t)m * I + cb, a, sizeof(a));
+        std::memcpy(arow + (size_t)m * I + cb, a, sizeof(a));
     });
-    FastParts pd;
+    FastParts& pd = sc.pd;
     pd.init(I, nr, H);
-    pool_units(pool, pd.nch, [&](int u) { pd.run_chunk(ex->tr[2], ex->fmt[2], I, arow.data(), u); });
+    pool_units(pool, pd.nch, [&](int u) { pd.run_chunk(ex->tr[2], ex->fmt[2], I, arow, u); });
     pool_units(pool, nr * (H / 128), [&](int u) {
         const int cb = 128 * (u % (H / 128)), m = u / (H / 128);
         float yv[128], sv[128];

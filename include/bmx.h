@@ -296,8 +296,9 @@ int bmx_copy_agent_destroy(bmx_copy_agent* agent);
  * layer calls that read them are to be discarded). Sequence numbers are 64-bit and never wrap. */
 int bmx_copy_agent_status(const bmx_copy_agent* agent, int64_t* stats);
 /* The residency planner's counts: stats[5] = requests answered, experts put on the CPU lane (summed over requests),
- * CPU jobs done (one per request with picks on the CPU lane), microseconds the CPU lane's worker spent on them, the worker's running mean per CPU pick in
- * nanoseconds (0 before its first job with picks; what policy cpu_measured prices a CPU expert at). */
+ * CPU jobs done (one per request with picks on the CPU lane), microseconds the CPU lane's worker spent on them, and the
+ * running mean per CPU pick of the policy's mode in nanoseconds (what policy cpu_measured prices a CPU expert at; 0
+ * while there is none). */
 int bmx_copy_agent_plan_stats(const bmx_copy_agent* agent, int64_t* stats);
 /* Failure-path control (the reference's controller has no counterpart; for tests that force a failure from the host):
  * hold >= 0 sets whether the agent's thread reads new records (1: it stops reading, so the waits run into their limit);
@@ -332,7 +333,7 @@ int bmx_cpu_expert_rows(const bmx_cpu_expert* ex, int H, int I, const uint16_t* 
 /* The CPU lane's fast mode: the same y rows within the layer tolerance, not bit for bit (the reference's lane is not
  * bit-exact either; its host decode, engine/kernels/nv2/ft_core.h, is what this replaces for throughput). The trellis
  * decode gives the device's fp16 weights exactly (the codebook's fp32 FMA rounded once to fp16 equals its exact value for
- * every byte sum, checked at start-up); the products accumulate in fp32 FMAs over chunks of eight tile rows read in
+ * every byte sum, checked at start-up); the products accumulate in fp32 FMAs over chunks of up to eight tile rows read in
  * memory order (the result does not depend on threads), without the device's k-splits or dot2 rounding; the rotations,
  * activation and roundings between the GEMVs are the exact lane's. AVX-512
  * (BW, VBMI, VNNI) when the host has it, else scalar. threads: a pool of that many persistent workers (the calling
@@ -378,8 +379,9 @@ enum { BMX_LANE_VRAM = 0, BMX_LANE_ADMIT = 1, BMX_LANE_HOME = 2, BMX_LANE_CPU = 
 typedef struct bmx_plan_policy {
     int32_t cpu_on, max_cpu, home_single;
     int32_t cpu_fast;          /* 1: the agent's CPU jobs use bmx_cpu_expert_rows_fast; 0: the exact lane */
-    int32_t cpu_measured;      /* 1: a CPU expert costs the worker's measured mean per pick (a running mean over its
-                                  jobs, 1/8 weight to the newest) in place of cpu_expert_us once a job has run */
+    int32_t cpu_measured;      /* 1: a CPU expert costs the worker's measured mean per pick in the policy's mode (a
+                                  running mean over its jobs, 1/8 weight to the newest; the fast mode's seeded by timed
+                                  rows at bmx_copy_agent_cpu_lane) in place of cpu_expert_us once there is one */
     double gpu_base_us, gpu_hit_us, gpu_home_us, gpu_admit_us;
     double cpu_base_us, cpu_expert_us, cpu_token_us;
 } bmx_plan_policy;

@@ -171,19 +171,32 @@ def test_cpu_lane_rows_bitexact_sequential_splits(cuda):
 
 
 def test_cpu_lane_time_c2_expert(cuda):
-    """Reported, not asserted: one C2-shaped expert (H 4096, I 1536, K 3) for one token on the host's cores."""
+    """Reported, not asserted: one C2-shaped expert (H 4096, I 1536, K 3) for one token on the host's cores, the exact
+    lane once, the fast mode warm (one expert again and again) and cold (32 experts in turn, 227 MB)."""
     import time
     import os
     import bmx
     from bmx import cpu_lane
     H, I = 4096, 1536
-    tab = bmx.ExpertTable.random(H, I, 1, (bmx.TF_K3,) * 3, seed=2, device=cuda)
-    ex = tab.host_expert(0)
+    tab = bmx.ExpertTable.random(H, I, 32, (bmx.TF_K3,) * 3, seed=2, device=cuda)
+    exs = [tab.host_expert(e) for e in range(32)]
     x = np.random.default_rng(2).standard_normal((1, H)).astype(np.float16)
     th = min(16, os.cpu_count() or 1)
     t0 = time.perf_counter()
-    cpu_lane.expert_rows(ex, H, I, x, 16, 4, 1, threads=th)
+    cpu_lane.expert_rows(exs[0], H, I, x, 16, 4, 1, threads=th)
     say(f"cpu lane: one C2 expert, one token, {th} threads: {(time.perf_counter() - t0) * 1e3:.1f} ms")
+    cpu_lane.expert_rows_fast(exs[0], H, I, x, threads=th)
+    warm, cold = [], []
+    for _ in range(10):
+        t0 = time.perf_counter()
+        cpu_lane.expert_rows_fast(exs[0], H, I, x, threads=th)
+        warm.append(time.perf_counter() - t0)
+    for e in range(1, 32):
+        t0 = time.perf_counter()
+        cpu_lane.expert_rows_fast(exs[e], H, I, x, threads=th)
+        cold.append(time.perf_counter() - t0)
+    say(f"cpu lane fast mode: one C2 expert, one token, {th} threads: warm {np.median(warm) * 1e6:.0f} us, "
+        f"cold {np.median(cold) * 1e6:.0f} us (medians)")
 
 
 def test_layer_verify_on_cpu_finds_a_flipped_bit(cuda):

@@ -191,10 +191,10 @@ def test_cpu_lane_fast_partial_added(cuda, oracle):
 
 
 def test_plan_measured_cpu_cost(cuda, oracle):
-    """Policy cpu_measured: with every cost 0 the first call's misses go to the CPU lane (its finish is then no later);
-    once its job has run the planner prices a CPU expert at the worker's measured time per pick, which no longer ties
-    with a GPU costing 0, so later calls put nothing there. The outputs stay the all-GPU rows' within the layer
-    tolerance throughout."""
+    """Policy cpu_measured: the fast mode's mean is seeded when the lane is set up; the exact mode's starts empty, so with
+    every cost 0 the first call's misses go to the CPU lane (its finish is then no later); once its job has run the
+    planner prices a CPU expert at the worker's measured time per pick, which no longer ties with a GPU costing 0, so
+    later calls put nothing there. The outputs stay the all-GPU rows' within the layer tolerance throughout."""
     import bmx
     from bmx import synth
     Lyr, E, H, I, topk = 2, 16, 256, 128, 4
@@ -203,6 +203,9 @@ def test_plan_measured_cpu_cost(cuda, oracle):
     slots = bmx.ExpertSlots(host_layers, 6, maxj=2, copies="dma")
     slots.cpu_lane(topk, threads=2)
     slots.plan(dict(cpu_on=1, max_cpu=2, cpu_fast=1, cpu_measured=1))
+    assert slots.plan_stats()[4] > 0                                   # the fast mode's seed
+    slots.plan(dict(cpu_on=1, max_cpu=2, cpu_fast=0, cpu_measured=1))
+    assert slots.plan_stats()[4] == 0                                  # no exact-mode job yet
     kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
     ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
     st_layers = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(Lyr)]
