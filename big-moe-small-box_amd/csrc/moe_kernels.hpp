@@ -90,11 +90,14 @@ __device__ __forceinline__ uint32_t win_state(uint32_t prev, const uint32_t (&ow
     return __builtin_amdgcn_alignbit(hi, own[d], 48 - o);
 }
 
-template <int NW>
+// NT: non-temporal loads. The prefill GEMM reads with the default policy instead, since a row group decoded again by
+// another workgroup then finds its words in the caches (C3's layer 2 % faster); the decode GEMV (5 % slower without)
+// and the mid-size GEMM (1 %) keep the non-temporal loads.
+template <bool NT = true, int NW>
 __device__ __forceinline__ void load_words(uint32_t (&w)[NW], const uint8_t* p)
 {
 #pragma unroll
-    for (int i = 0; i < NW; ++i) w[i] = ldg_nt(p, i);
+    for (int i = 0; i < NW; ++i) w[i] = NT ? ldg_nt(p, i) : ldg(p, i);
 }
 
 // The strip of lane s (= lane & 3) of a tile: stream positions 64 s .. 64 s + 63, i.e. output columns

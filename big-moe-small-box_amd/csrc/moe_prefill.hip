@@ -314,40 +314,35 @@ __device__ __forceinline__ void pf_decoder(const PfJob& jb, const uint8_t* mat_b
 #pragma unroll
         for (int j = 0; j < NA; ++j) a_store(a[j], stage, arow[j]);
     };
-    uint32_t w0[NW], w1[NW], w2[NW];
-    PfArow a0[NA], a1[NA], a2[NA];
-    if (ACOPY)
+    // DEPTH register sets (words and A rows) in rotation: step s is loaded into set s % DEPTH DEPTH - 1 steps before it
+    // is staged. The MFMA waves set the kernel's register count; a group's decoder has the room for a fourth set up to
+    // K 3 (six words a strip), a pair's (twice the A rows) or a K 4 one's (eight words) keeps three.
+    constexpr int DEPTH = (PAIR || NW > 6) ? 3 : 4;
+    uint32_t w[DEPTH][NW];
+    PfArow ar[DEPTH][NA];
+#pragma unroll
+    for (int q = 0; q < DEPTH; ++q)
     {
-        fetch(a0, 0);
-        fetch(a1, 1);
-        fetch(a2, 2);
+        if (ACOPY) fetch(ar[q], q);
+        load_words<false>(w[q], wp(q));
     }
-    load_words(w0, wp(0));
-    load_words(w1, wp(1));
-    load_words(w2, wp(2));
-    dec(w0, pf_b0);
-    if (ACOPY) store(a0, pf_a0);
+    dec(w[0], pf_b0);
+    if (ACOPY) store(ar[0], pf_a0);
     step_barrier();
-    // step i: stage step i + 1 (A rows, B fragments) into stage (i + 1) % 2, fetch step i + 3 into the sets step i used
-    for (int i = 0; i < KT; i += 3)
+    // sub-step q of the trip from step i: load step i + q + DEPTH into set q (staged in the sub-step before), stage step
+    // i + q + 1 from set (q + 1) % DEPTH into stage (i + q + 1) % 2
+    for (int i = 0; i < KT; i += DEPTH)
     {
-        if (ACOPY) fetch(a0, i + 3);
-        load_words(w0, wp(i + 3));
-        dec(w1, b_stage((i + 1) & 1));
-        if (ACOPY) store(a1, a_stage((i + 1) & 1));
-        step_barrier();
-        if (i + 1 >= KT) break;
-        if (ACOPY) fetch(a1, i + 4);
-        load_words(w1, wp(i + 4));
-        dec(w2, b_stage(i & 1));
-        if (ACOPY) store(a2, a_stage(i & 1));
-        step_barrier();
-        if (i + 2 >= KT) break;
-        if (ACOPY) fetch(a2, i + 5);
-        load_words(w2, wp(i + 5));
-        dec(w0, b_stage((i + 1) & 1));
-        if (ACOPY) store(a0, a_stage((i + 1) & 1));
-        step_barrier();
+#pragma unroll
+        for (int q = 0; q < DEPTH; ++q)
+        {
+            if (ACOPY) fetch(ar[q], i + q + DEPTH);
+            load_words<false>(w[q], wp(i + q + DEPTH));
+            dec(w[(q + 1) % DEPTH], b_stage((i + q + 1) & 1));
+            if (ACOPY) store(ar[(q + 1) % DEPTH], a_stage((i + q + 1) & 1));
+            step_barrier();
+            if (i + q + 1 >= KT) return;
+        }
     }
 }
 
