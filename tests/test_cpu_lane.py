@@ -119,6 +119,26 @@ def test_fast_lane_rows_match_oracle(oracle, act, gated, limit):
             assert err < 1e-3 and np.abs(y[m] - yo).max() < 1e-2, (e, m, err)
 
 
+@pytest.mark.parametrize("H,I,fmts", [(2048, 1536, (2, 1, 0)), (4096, 256, (3, 0, 2))])
+def test_fast_lane_long_chunks(monkeypatch, oracle, H, I, fmts):
+    """Shapes whose chunks hold several tile-rows (K / 512 of them, at most 8: 4 for gate / up and 3 for down at
+    (2048, 1536), 8 and 1 at (4096, 256), the last chunk of K 1536 short): the SIMD path equals the scalar one and a
+    different worker count gives the same bits, and the rows are within the layer tolerance of the oracle."""
+    from bmx import cpu_lane
+    ex = host_expert(H, I, fmts, seed=H + I)
+    x = np.random.default_rng(H).standard_normal((2, H)).astype(np.float16)
+    y = cpu_lane.expert_rows_fast(ex, H, I, x, 0, True, 0.0, threads=1)
+    y7 = cpu_lane.expert_rows_fast(ex, H, I, x, 0, True, 0.0, threads=7)
+    assert np.array_equal(y.view(np.uint32), y7.view(np.uint32))
+    for m in range(2):
+        yo = oracle.expert_forward(ex, H, I, x[m], 0, True, 0.0)[0]
+        err = np.sqrt(np.mean((y[m] - yo) ** 2)) / max(1e-30, np.sqrt(np.mean(yo ** 2)))
+        assert err < 1e-3 and np.abs(y[m] - yo).max() < 1e-2, (m, err)
+    monkeypatch.setenv("BMX_CPU_LANE_SCALAR", "1")
+    y_sca = cpu_lane.expert_rows_fast(ex, H, I, x, 0, True, 0.0, threads=3)
+    assert np.array_equal(y.view(np.uint32), y_sca.view(np.uint32))
+
+
 def test_fast_lane_close_to_exact_lane():
     """A C2-shaped expert (H 4096, I 1536, K 3): the fast mode's rows within the layer tolerance of the exact lane's,
     and repeated calls (the worker pool kept between them, its size changed) give the same bits."""
