@@ -241,10 +241,11 @@ def bench_c4(args):
     DMA = args.copies == "dma"
     CPUL = args.cpu_lane > 0 and DMA
     if CPUL:
-        # planned steps: the agent's planner puts misses on the CPU lane (fast mode, args.cpu_lane worker threads) when
-        # its estimated finish is no later than the GPU's; the GPU costs are measured per-expert times of this stack,
-        # the CPU's starts at args.cpu_expert_us and follows the worker's measured time per pick (cpu_measured)
-        slots.cpu_lane(topk, threads=args.cpu_lane)
+        # planned steps: the agent's planner puts misses on the CPU lane (fast mode, args.cpu_lane worker threads, reading
+        # its own huge-page copy of the homes) when its estimated finish is no later than the GPU's; the GPU costs are
+        # measured per-expert times of this stack, the CPU's is measured (seeded when the lane is set up, then the
+        # worker's running mean per pick)
+        slots.cpu_lane(topk, threads=args.cpu_lane, copy=True)
         slots.plan(dict(cpu_on=1, max_cpu=args.cpu_max, cpu_fast=1, cpu_measured=1, gpu_base_us=50.0, gpu_hit_us=0.0,
                         gpu_admit_us=140.0, cpu_base_us=10.0, cpu_expert_us=args.cpu_expert_us, cpu_token_us=60.0))
     # warm: each layer's most popular experts (Zipf rank order of its permutation), S // NL per layer

@@ -206,16 +206,37 @@ class ExpertSlots:
             L.check(L.lib().bmx_copy_agent_plan(self.agent, ctypes.byref(pol)), "bmx_copy_agent_plan")
         self.planned = True
 
-    def cpu_lane(self, topk, act=L.ACT_SILU, gated=True, act_limit=0.0, threads=16):
-        """Give the copy agent its CPU lane: host copies of every layer's experts (kept here) for the agent's worker."""
+    def cpu_lane(self, topk, act=L.ACT_SILU, gated=True, act_limit=0.0, threads=16, copy=False):
+        """Give the copy agent its CPU lane: the experts of every layer (kept here) for the agent's worker.
+
+        copy=False: the lane reads the trellis bytes where they are (the homes, pinned host memory, for a host-homed
+        table). copy=True: the lane reads its own copy of each distinct home arena in ordinary host memory, which the
+        kernel backs with 2 MB pages (numpy advises huge pages for large arrays). Pinned memory is mapped in 4 KB pages,
+        and a cold expert read from a few tens of GB of them waits on page-table walks: measured in a 43-layer stack,
+        a fast-mode expert call took 543 us from the pinned homes and 185 us from the copy. The copy costs the homes'
+        size again in host memory."""
         if self.agent is None:
             raise ValueError("ExpertSlots.cpu_lane: needs the copy agent (copies='dma')")
         import numpy as np
         keep, exps = [], (L.CpuExpert * (self.L * self.E))()
+        copies = {}
         for li, t in enumerate(self.layers):
+            src = None
+            if copy and t.arena.device.type == "cpu":
+                key = t.arena.data_ptr()
+                if key not in copies:
+                    a = t.arena.numpy()
+                    c = np.empty(a.shape, a.dtype)
+                    np.copyto(c, a)
+                    copies[key] = c
+                src = copies[key]
             for e in range(t.E):
                 h = t.host_expert(e)
-                arrs = [np.ascontiguousarray(a) for a in h["tr"]] + \
+                tr = h["tr"]
+                if src is not None:
+                    offs = (0, t.off_u, t.off_d)
+                    tr = [src[e, offs[m]:offs[m] + t.mat_bytes(e, m)] for m in range(3)]
+                arrs = [np.ascontiguousarray(a) for a in tr] + \
                        [np.ascontiguousarray(v, dtype=np.float16) for v in h["suh"] + h["svh"]]
                 keep.append(arrs)
                 ce = exps[li * self.E + e]
@@ -224,7 +245,7 @@ class ExpertSlots:
                     ce.suh[m] = arrs[3 + m].ctypes.data
                     ce.svh[m] = arrs[6 + m].ctypes.data
                     ce.fmt[m] = int(h["fmt"][m])
-        self._cpu_keep = (keep, exps)
+        self._cpu_keep = (keep, exps, copies)
         d = self.layers[0].desc(topk, self.first, act, gated, act_limit)
         L.check(L.lib().bmx_copy_agent_cpu_lane(self.agent, ctypes.byref(d), exps, int(threads)),
                 "bmx_copy_agent_cpu_lane")

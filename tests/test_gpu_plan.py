@@ -146,17 +146,18 @@ def test_plan_reply_timeout_is_reported(cuda):
     slots.close()
 
 
-def test_cpu_lane_fast_partial_added(cuda, oracle):
+@pytest.mark.parametrize("copy", [False, True])
+def test_cpu_lane_fast_partial_added(cuda, oracle, copy):
     """The same layer calls with the CPU lane in its fast mode (policy cpu_fast): out = the GPU's combine of the masked
     selection + the fast lane's partial, within the layer tolerance of the all-GPU rows' combine (the fast mode keeps the
-    exact weights but not the device's summation order)."""
+    exact weights but not the device's summation order). copy: the lane reads its own copy of the homes."""
     import bmx
     from bmx import synth
     Lyr, E, H, I, topk, first = 2, 16, 256, 128, 4, 0
     dev_layers = small_layers(Lyr, E, H, I, 150, "device")
     host_layers = small_layers(Lyr, E, H, I, 150, "host")
     slots = bmx.ExpertSlots(host_layers, 6, maxj=2, copies="dma")
-    slots.cpu_lane(topk, threads=4)
+    slots.cpu_lane(topk, threads=4, copy=copy)
     slots.plan(dict(cpu_on=1, max_cpu=2, cpu_fast=1, gpu_base_us=1.0, gpu_admit_us=1.0))
     kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
     ref_layers = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(Lyr)]
