@@ -83,7 +83,8 @@ __device__ __forceinline__ int compact_flags(bool flag, int value, int32_t* out,
 // A planned step's request and reply, by the whole workgroup: the picked experts (mark) in ascending order into uq
 // with their residency and pick counts (ecnt), the picks and input rows when the call is small enough, published under
 // a.seq; then the bounded wait for the planner's reply and each expert's lane into elane (a resident expert is always a
-// hit; a lane value the step does not know runs the expert from its home). Returns 0 when the agent had failed or the
+// hit; a lane value the step does not know runs the expert from its home). A call with every expert resident publishes
+// nothing and writes its own reply (no CPU pick). Returns 0 when the agent had failed or the
 // ring slot or the reply did not come in time (then every lane is VRAM or HOME and the step admits nothing).
 __device__ int plan_step(const SlotArgs& a, const uint32_t* mark, const int32_t* ecnt, int32_t* elane, int32_t* uq,
                          int* wave_cnt, int* s_ok)
@@ -92,13 +93,24 @@ __device__ int plan_step(const SlotArgs& a, const uint32_t* mark, const int32_t*
     const int32_t* slotof = a.t.slotof + (size_t)a.li * E;
     const bool marked = tid < E && ((mark[tid >> 5] >> (tid & 31)) & 1u);
     const int nu = compact_flags(marked, tid, uq, wave_cnt);
-    if (tid == 0) *s_ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
+    __shared__ int s_miss;
+    if (tid == 0)
+    {
+        *s_ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
+        s_miss = 0;
+    }
     __syncthreads();
+    for (int u = tid; u < nu; u += SL_THREADS)
+        if (slotof[uq[u]] < 0) atomicAdd(&s_miss, 1);
+    __syncthreads();
+    // a call whose experts are all resident has nothing to plan (the planner never moves a resident expert): no request,
+    // no wait; the step writes that call's reply itself (no CPU pick), which is what the CPU partial's add reads
+    const bool resident = s_miss == 0;
     PlanReq* rq = &a.sh->req[ring_index(a.seq)];
     const PlanArgs& pl = a.pl;
     const bool picks = a.n <= BMX_PLAN_MAXP;
     const bool has_x = picks && pl.x && pl.xring && pl.T <= BMX_PLAN_MAXT;
-    if (*s_ok)
+    if (*s_ok && !resident)
     {
         for (int u = tid; u < nu; u += SL_THREADS)
         {
@@ -133,7 +145,13 @@ __device__ int plan_step(const SlotArgs& a, const uint32_t* mark, const int32_t*
         __threadfence_system();          // this thread's writes to host memory, before the barrier and the publish
     }
     __syncthreads();
-    if (tid == 0 && *s_ok)
+    if (tid == 0 && *s_ok && resident)
+    {
+        PlanRep* wr = &a.sh->rep[ring_index(a.seq)];
+        __hip_atomic_store(&wr->ncpu, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(&wr->seq, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    else if (tid == 0 && *s_ok)
     {
         __hip_atomic_store(&rq->seq, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         const PlanRep* rp = &a.sh->rep[ring_index(a.seq)];

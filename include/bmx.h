@@ -354,7 +354,8 @@ int bmx_dot2_f32_f16(const uint32_t* a, const uint32_t* b, const float* c, float
  * step publishes its layer call to the copy agent as a request: the unique experts it picks (ascending), whether each is
  * resident in a VRAM slot, how many picks each has, and for calls of at most BMX_PLAN_MAXP picks the picks themselves
  * (expert, fp16 weight) and, given x, the input rows of up to BMX_PLAN_MAXT tokens. The agent's thread answers each
- * request in sequence order with a lane per unique expert (bmx_plan_policy); the step waits for the reply (bounded by
+ * request in sequence order with a lane per unique expert (bmx_plan_policy; a call whose experts are all resident
+ * publishes no request, its plan being fixed); the step waits for the reply (bounded by
  * the agent's wait limit; running out of it is the agent failure bmx_copy_agent_status reports, after which the step
  * admits nothing) and applies it:
  *   BMX_LANE_VRAM   resident: a hit (the planner never moves a resident expert)
