@@ -22,6 +22,10 @@ int launch_router(const void* logits, const float* bias, int T, int E, int topk,
 
 int launch_router_logits(const void* z, const void* W, int T, int H, int E, void* logits, hipStream_t s);
 bool route_dispatch_small_fits(int T, int E, int topk);
+struct RouteFuse;
+int route_fuse_args(const void* logits, const float* bias, int T, int E, int topk, int n_group, int topk_group,
+                    int score_fn, int renorm, float scale, int64_t first, int64_t* sel, void* w, int shared, int rpg,
+                    const bmx_routes* routes, RouteFuse* out);
 int launch_route_dispatch_small(const void* logits, const float* bias, int T, int E, int topk, int n_group,
                                 int topk_group, int score_fn, int renorm, float scale, int64_t first, int64_t* sel,
                                 void* w, int shared, int rpg, const bmx_routes* routes, hipStream_t s);
@@ -56,7 +60,8 @@ int decode_gu_grouped(const MoeShape& m);     // 1: the gate / up epilogue sums 
 size_t decode_ws_bytes(const MoeShape& m);
 // ws layout: [part_gu][part_dn][act rows (used when act_rows == NULL)]; stages: 1 = gate/up, 2 = down (+ combine)
 int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
-                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages);
+                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages,
+                          const RouteFuse* rf = nullptr);
 int decode_rows_per_group(int T);
 int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const int32_t* offsets, int T, int topk,
                    int H, int E, int has_shared, float* out, hipStream_t s);

@@ -1,6 +1,7 @@
 // C ABI of libbmx.so (include/bmx.h): argument checks, workspace layout, launch order.
 #include "bmx_common.hpp"
 #include "bmx_internal.hpp"
+#include "router_wave.hpp"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -102,6 +103,13 @@ static long env_rows(const char* name, long dflt)
 {
     const char* v = getenv(name);
     return (v && *v) ? atol(v) : dflt;
+}
+
+// BMX_ROUTE_IN_GEMV=0: a one-token layer call launches route + dispatch before its gate / up GEMV (same results)
+static bool route_in_gemv_allowed()
+{
+    const char* v = getenv("BMX_ROUTE_IN_GEMV");
+    return !(v && *v == '0');
 }
 
 static int resolve_path(int path, int T, int topk)
@@ -398,6 +406,17 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
     const size_t dws_bytes = align_up(dispatch_ws_bytes(T, desc->topk, desc->E), 256);
     char* ews = dws + dws_bytes;
     const size_t ews_bytes = align_up(experts_ws_bytes(p, m), 256);
+    if (T == 1 && p == BMX_PATH_DECODE && rpg == 1 && route_dispatch_small_fits(T, desc->E, desc->topk) &&
+        route_in_gemv_allowed())
+    {
+        // one token: the gate / up GEMV routes it and writes the dispatch itself (one launch fewer)
+        RouteFuse f;
+        rc = route_fuse_args(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group, router->topk_group,
+                             router->score_fn, router->renorm, router->scale, desc->first, sel, w_fp16, m.shared, rpg,
+                             &r, &f);
+        if (rc) return rc;
+        return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER, &f);
+    }
     if (route_dispatch_small_fits(T, desc->E, desc->topk))
         rc = launch_route_dispatch_small(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group,
                                          router->topk_group, router->score_fn, router->renorm, router->scale,

@@ -14,6 +14,7 @@
 //                        shared expert                                     (exllamav3 kernel B, x16_red_k order)
 // The kernels hand data over only at kernel boundaries (no inter-workgroup flags or fences inside a kernel).
 #include "moe_kernels.hpp"
+#include "router_wave.hpp"
 
 #include <stdlib.h>
 
@@ -134,18 +135,14 @@ __device__ __forceinline__ void gemv_rows(const GvArgs& a, const bmx_expert& ex,
             for (int m = 0; m < MR; ++m) red[(wave * MX + m) * 128 + lane_col(lane, c)] = acc[c][m];
 }
 
+// One work unit (k-split ks, column block cb of a group: expert e, rows r0 .. r0 + nr - 1) of the split-K GEMV. tok1 >= 0:
+// the rows' token (a one-token call whose dispatch is being written by another workgroup), else from row_token.
 template <int MX, int NM>
-__global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
+__device__ __forceinline__ void gemv_unit(const GvArgs& a, int ks, int cb, int e, int r0, int nr, int tok1)
 {
     extern __shared__ uint32_t smem[];
-    int bid = blockIdx.x;
-    const int KS = NM == 2 ? a.KS_gu : a.KS_dn, NB = NM == 2 ? a.NB : a.NBH;
-    const int ks = bid % KS;
-    bid /= KS;
-    const int cb = bid % NB, g = bid / NB;
-    if (g >= *a.ngroups) return;
-    const int e = a.groups[3 * g], r0 = a.groups[3 * g + 1], nr = a.groups[3 * g + 2];
-    if (NM == 2 && group_skipped(a, e)) return;
+    const int NB = NM == 2 ? a.NB : a.NBH;
+    const int KS = NM == 2 ? a.KS_gu : a.KS_dn;
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const int K = NM == 2 ? a.H : a.I, N = NM == 2 ? a.I : a.H;
     const int KR = K / KS, k0 = ks * KR, XW = KR / 2;
@@ -164,7 +161,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
                 for (int b = 0; b < nblk; ++b, ++u)
                 {
                     if ((u & (GV_WAVES - 1)) != wave) continue;
-                    const int tok = a.row_token[r0 + m];
+                    const int tok = tok1 >= 0 ? tok1 : a.row_token[r0 + m];
                     const int k = k0 + b * 128 + 2 * lane;
                     const uint32_t xv = ldg(a.x + (size_t)tok * a.H + k, 0);
                     const uint32_t sv = ldg(reinterpret_cast<const uint16_t*>(ex.suh[mat]) + k, 0);
@@ -214,6 +211,71 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
         for (int w = 0; w < WPM; ++w) s = s + red[((mat * WPM + w) * MX + m) * 128 + c];
         part[(size_t)m * NB * NM * 128 + mat * 128 + c] = s;
     }
+    (void)KS;
+}
+
+template <int MX, int NM>
+__global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
+{
+    int bid = blockIdx.x;
+    const int KS = NM == 2 ? a.KS_gu : a.KS_dn, NB = NM == 2 ? a.NB : a.NBH;
+    const int ks = bid % KS;
+    bid /= KS;
+    const int cb = bid % NB, g = bid / NB;
+    if (g >= *a.ngroups) return;
+    const int e = a.groups[3 * g], r0 = a.groups[3 * g + 1], nr = a.groups[3 * g + 2];
+    if (NM == 2 && group_skipped(a, e)) return;
+    gemv_unit<MX, NM>(a, ks, cb, e, r0, nr, -1);
+}
+
+// LDS of the routing phase of k_gemv_gu_route, inside the kernel's dynamic LDS (the GEMV reuses it afterwards): the
+// router wave's own, the picks, the group experts, and the one-wave dispatch's counts, offsets and token masks
+template <int J>
+struct RouteLds {
+    TopkLds tl;
+    int pe[64];
+    int gex[64];
+    int cnt[64 * (J + 1) + 1];
+    int off[64 * (J + 1) + 1];
+    alignas(8) uint64_t mask[64 * (J + 1) + 1];
+};
+
+// The gate / up GEMV of a one-token call that routes the token itself: wave 0 of every workgroup runs the router's
+// selection (the same picks everywhere; only workgroup 0 writes sel / w and the dispatch arrays that the later stages
+// read), and the workgroup takes its group from the picks: a one-token dispatch lists the picked experts in ascending
+// order, one row each (row g for the g-th), then the shared expert (row topk). Saves the route + dispatch launch and the
+// loads of the group record.
+template <int J>
+__global__ __launch_bounds__(GV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_gemv_gu_route(GvArgs a,
+                                                                                                          RouteFuse f)
+{
+    extern __shared__ uint32_t smem[];
+    RouteLds<J>& L = *reinterpret_cast<RouteLds<J>*>(smem);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, topk = f.ra.topk;
+    if (wave == 0)
+    {
+        RouterArgs ra = f.ra;
+        if (blockIdx.x != 0) ra.sel = nullptr;
+        const int pk = route_token_wave<J>(ra, 0, L.tl);
+        if (lane < topk) L.pe[lane] = pk;
+        wave_lds_sync();
+        if (lane < topk)
+        {
+            int rank = 0;
+            for (int j = 0; j < topk; ++j) rank += L.pe[j] < pk;     // the picks of a token are distinct experts
+            L.gex[rank] = pk;
+        }
+        if (blockIdx.x == 0) dispatch_wave<J + 1>(L.pe, topk, f.ra.E, 1, topk, f.sd, L.cnt, L.off, L.mask);
+    }
+    __syncthreads();
+    int bid = blockIdx.x;
+    const int ks = bid % a.KS_gu;
+    bid /= a.KS_gu;
+    const int cb = bid % a.NB, g = bid / a.NB;
+    if (g >= topk + (a.has_shared ? 1 : 0)) return;
+    const int e = g < topk ? L.gex[g] : a.E;
+    __syncthreads();                      // every wave has read the routing LDS before the GEMV reuses it
+    gemv_unit<1, 2>(a, ks, cb, e, g, 1, 0);
 }
 
 // ---- epilogues: 16 lanes per (row or token, 128-column block), 8 consecutive columns per lane -----------------------------
@@ -648,8 +710,16 @@ size_t decode_ws_bytes(const MoeShape& m)
 }
 
 // stages: bit i = BMX_STAGE i (GATE_UP, ACT, DOWN, COMBINE, DOWN_OUT; PREP launches nothing here: the GEMV rotates)
+// the routing gate / up GEMV for ceil(E / 64) = J
+template <int J>
+static void launch_gu_route(const GvArgs& a, const DecodePlan& p, const RouteFuse& f, size_t lds_gu, hipStream_t s)
+{
+    const size_t lds = lds_gu > sizeof(RouteLds<J>) ? lds_gu : sizeof(RouteLds<J>);
+    hipLaunchKernelGGL(k_gemv_gu_route<J>, dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds, s, a, f);
+}
+
 template <int MR>
-static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStream_t s)
+static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStream_t s, const RouteFuse* rf)
 {
     const size_t lds_gu = (size_t)2 * MR * (a.H / p.KS_gu) / 2 * 4 + (size_t)GV_WAVES * MR * 128 * 4;
     const size_t lds_dn = (size_t)MR * (a.I / p.KS_dn) / 2 * 4 + (size_t)GV_WAVES * MR * 128 * 4;
@@ -659,7 +729,21 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
         if (!(stages & (1 << st))) continue;
         GvArgs b = a;
         b.filter = f;
-        hipLaunchKernelGGL((k_gemv_part<MR, 2>), dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds_gu, s, b);
+        if (MR == 1 && f == 0 && rf)
+            switch (rf->J)
+            {
+                case 1: launch_gu_route<1>(b, p, *rf, lds_gu, s); break;
+                case 2: launch_gu_route<2>(b, p, *rf, lds_gu, s); break;
+                case 3: launch_gu_route<3>(b, p, *rf, lds_gu, s); break;
+                case 4: launch_gu_route<4>(b, p, *rf, lds_gu, s); break;
+                case 5: launch_gu_route<5>(b, p, *rf, lds_gu, s); break;
+                case 6: launch_gu_route<6>(b, p, *rf, lds_gu, s); break;
+                case 7: case 8: launch_gu_route<8>(b, p, *rf, lds_gu, s); break;
+                default: launch_gu_route<16>(b, p, *rf, lds_gu, s); break;
+            }
+        else
+            hipLaunchKernelGGL((k_gemv_part<MR, 2>), dim3((unsigned)(p.G_max * p.NB * p.KS_gu)), dim3(GV_THREADS), lds_gu, s,
+                               b);
     }
     if ((stages & (1 << BMX_STAGE_ACT)) && !a.act_in_down) launch_epilogue(a, BMX_STAGE_ACT, s);
     if (stages & (1 << BMX_STAGE_DOWN))
@@ -668,9 +752,46 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
     if (stages & (1 << BMX_STAGE_DOWN_OUT)) launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
 }
 
-int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
-                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages)
+// compute units of the current device (each device asked once)
+static int cu_count()
 {
+    static int n[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!n[dev])
+    {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        n[dev] = v;
+    }
+    return n[dev];
+}
+
+// The routing gate / up GEMV pays the routing at the start of every workgroup, so it takes the most k-splits (at most
+// the plan's) whose workgroups start in one round (5 per compute unit); a k-range that no longer fits the staged input
+// rows, a forced split (BMX_KS_GU) or no such count keeps the plan's. Same results within the layer tolerance (another
+// summation order of the k-split partials); bmx_decode_splits describes the separate route + GEMV path.
+static int one_round_ks(const DecodePlan& p, const MoeShape& m)
+{
+    const char* v = getenv("BMX_KS_GU");
+    if (v && *v) return p.KS_gu;
+    const long cap = 5L * cu_count(), units = (long)p.G_max * p.NB;
+    const int nblk = m.H / 128, max_kr = GV_LDS_X / (2 * 1 * 2);
+    for (int d = p.KS_gu; d >= 1; --d)
+    {
+        if (nblk % d) continue;
+        if (m.H / d > max_kr) break;
+        if (units * d <= cap) return d;
+    }
+    return p.KS_gu;
+}
+
+int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
+                          void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages,
+                          const RouteFuse* rf)
+{
+    if (rf && (m.T != 1 || rows_per_group_of(m.T) != 1 || !(stages & (1 << BMX_STAGE_GATE_UP))))
+        return set_error(BMX_ERR_ARG, "moe experts: routing inside the GEMV is for one-token calls with the gate / up stage");
     if (m.H % 128 || m.I % 128 || m.H <= 0 || m.I <= 0)
         return set_error(BMX_ERR_ARG, "moe experts: H (%d) and I (%d) must be multiples of 128", m.H, m.I);
     const DecodePlan p = decode_plan(m);
@@ -689,7 +810,9 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
     w += align_up(p.part_dn_bytes, 256);
     a.act_rows = act_rows ? static_cast<uint16_t*>(act_rows) : reinterpret_cast<uint16_t*>(w);
     a.y_rows = y_rows;
-    a.KS_gu = p.KS_gu; a.KS_dn = p.KS_dn; a.NB = p.NB; a.NBH = p.NBH; a.R_max = p.R_max;
+    DecodePlan q = p;                      // the launch's plan (the workspace keeps p's layout; q's partials fit in it)
+    if (rf) q.KS_gu = one_round_ks(p, m);
+    a.KS_gu = q.KS_gu; a.KS_dn = q.KS_dn; a.NB = q.NB; a.NBH = q.NBH; a.R_max = q.R_max;
     a.NE = m.E + (m.shared ? 1 : 0);
     a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
     a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
@@ -706,10 +829,10 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
                     !act_rows && m.H / 128 <= 16 && act_in_down_allowed();
     switch (rows_per_group_of(m.T))
     {
-        case 1: launch_mr<1>(a, p, stages, s); break;
-        case 2: launch_mr<2>(a, p, stages, s); break;
-        case 4: launch_mr<4>(a, p, stages, s); break;
-        default: launch_mr<8>(a, p, stages, s); break;
+        case 1: launch_mr<1>(a, q, stages, s, rf); break;
+        case 2: launch_mr<2>(a, p, stages, s, nullptr); break;
+        case 4: launch_mr<4>(a, p, stages, s, nullptr); break;
+        default: launch_mr<8>(a, p, stages, s, nullptr); break;
     }
     return check_launch("moe experts (decode path)");
 }

@@ -162,7 +162,10 @@ typedef struct bmx_router_desc {
 /* The whole layer call from router logits: router + dispatch (one kernel at decode sizes), expert products, combine.
  * The reference's per-layer sequence routing_fn -> Nv2.layer -> run_bszN -> cpu_split_combine (engine/tiers.py:707-739)
  * with the expert arithmetic of exllamav3. sel int64 [T, topk] and w fp16 [T, topk] receive the routing. logits_fp16
- * NULL: the logits are projected from x with router->weight first (bmx_router_logits, into the workspace). */
+ * NULL: the logits are projected from x with router->weight first (bmx_router_logits, into the workspace). One token on
+ * the decode path: the gate / up GEMV routes it and writes the dispatch itself (BMX_ROUTE_IN_GEMV=0: separate launch),
+ * with as many gate / up k-splits as start in one round, which can be fewer than bmx_decode_splits reports for the
+ * separate calls: the same routing, the output within the layer tolerance of theirs. */
 size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path);
 int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
                   int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
@@ -340,7 +343,8 @@ int bmx_cpu_expert_rows(const bmx_cpu_expert* ex, int H, int I, const uint16_t* 
  * thread is one), kept for later calls with the same count; calls are serialised on it. */
 int bmx_cpu_expert_rows_fast(const bmx_cpu_expert* ex, int H, int I, const uint16_t* x_fp16, int nr, int act,
                              int gated, float act_limit, float* y_rows, int threads);
-/* The device plan of a decode-path call of T tokens: k-splits of the gate / up and down GEMVs, and whether the gate / up
+/* The device plan of a decode-path call of T tokens (bmx_moe_forward and the stage entry points; a one-token
+ * bmx_moe_layer may take fewer gate / up splits): k-splits of the gate / up and down GEMVs, and whether the gate / up
  * epilogue sums the splits in four interleaved groups (small launches) or in sequence. */
 int bmx_decode_splits(const bmx_moe_desc* desc, int T, int* ks_gu, int* ks_dn, int* grouped_gu);
 /* out[i] = a[i].lo * b[i].lo + a[i].hi * b[i].hi + c[i] (fp16 pairs, fp32): bmx_cpu_dot2 emulates the device's

@@ -222,7 +222,7 @@ LAYERS = [
 
 
 @pytest.mark.parametrize("name,cfgname,T,rows,kw", LAYERS, ids=[l[0] for l in LAYERS])
-def test_layer_parity(cuda, oracle, name, cfgname, T, rows, kw):
+def test_layer_parity(cuda, oracle, monkeypatch, name, cfgname, T, rows, kw):
     import bmx
     from bmx import synth
     c = synth.CONFIGS[cfgname]
@@ -240,7 +240,18 @@ def test_layer_parity(cuda, oracle, name, cfgname, T, rows, kw):
     out = layer.run_bszN(x, sel, w).cpu().numpy()
     fused = layer.forward(x, lg).cpu().numpy()          # router + dispatch + experts + combine in one library call
     assert torch.equal(layer.sel, sel) and torch.equal(layer.w, w)
-    assert np.array_equal(fused, out)
+    if T == 1:
+        # one token: the gate / up GEMV routes it itself, with as many k-splits as start in one round. With the plan's
+        # own split count forced, the one call equals the separate calls bit for bit (the routing and the dispatch inside
+        # the GEMV are exact); by default it sums the splits in another order: within the layer tolerance.
+        from bmx import cpu_lane
+        monkeypatch.setenv("BMX_KS_GU", str(cpu_lane.decode_splits(layer.desc, 1)[0]))
+        forced = layer.forward(x, lg).cpu().numpy()
+        monkeypatch.delenv("BMX_KS_GU")
+        assert np.array_equal(forced, out)
+        assert np.abs(fused - out).max() < MAX_ABS and rel_rms(fused, out) < REL_RMS
+    else:
+        assert np.array_equal(fused, out)
     rows = list(range(T)) if rows is None else rows
     say("layer", name, "oracle rows", rows)
     want = oracle_layer(oracle, tab, x.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy(), rows)
