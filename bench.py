@@ -39,6 +39,48 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+class TimingEvent:
+    """A HIP event for timing only, created with hipEventDisableSystemFence: recording it skips the system-scope release
+    (an L2 writeback) that a default event performs, which costs microseconds of GPU time per record and would be
+    counted into a microsecond-scale kernel between two records. Elapsed times are read after a device synchronize."""
+    _hip = None
+
+    @classmethod
+    def hip(cls):
+        if cls._hip is None:
+            # the HIP runtime this process already runs (torch's; the library resolves to the same one)
+            path = next((l.split()[-1] for l in open("/proc/self/maps") if "libamdhip64" in l), "libamdhip64.so")
+            h = ctypes.CDLL(path)
+            h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self):
+        self.ev = ctypes.c_void_p()
+        rc = self.hip().hipEventCreateWithFlags(ctypes.byref(self.ev), 0x20000000)   # hipEventDisableSystemFence
+        if rc:
+            raise RuntimeError(f"hipEventCreateWithFlags: error {rc}")
+
+    def record(self, stream):
+        rc = self._hip.hipEventRecord(self.ev, stream)
+        if rc:
+            raise RuntimeError(f"hipEventRecord: error {rc}")
+
+    def elapsed_time(self, end):
+        ms = ctypes.c_float()
+        rc = self._hip.hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev)
+        if rc:
+            raise RuntimeError(f"hipEventElapsedTime: error {rc}")
+        return ms.value
+
+    def __del__(self):
+        if self._hip is not None and self.ev:
+            self._hip.hipEventDestroy(self.ev)
+
+
 def physical_cpus(limit):
     """CPUs of this process, one per physical core first (the reference's lane rule: one lane thread per core)."""
     allowed = sorted(os.sched_getaffinity(0))
@@ -492,34 +534,57 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
     del graph
     ms = min(ms_eager, ms_graph)
 
-    # per-stage timing with events on the launch stream (torch's current stream), same step sequence
+    # per-stage timing with events on the launch stream (torch's current stream): the same layer calls one stage set at
+    # a time (bmx_moe_layer_stages), so each stage runs the kernels the one-call step runs
     topk = layers[0].num_experts_per_tok
     path = L.bmx_resolve_path(T, topk, pa)
     prefill, mid = path == bmx._lib.PATH_PREFILL, path == bmx._lib.PATH_MID
     rpg = L.bmx_rows_per_group(T, topk, pa)
+    # a one-token decode call routes the token inside its gate / up GEMV (its route stage launches nothing)
+    fused_route = T == 1 and path == bmx._lib.PATH_DECODE and rpg == 1 and os.environ.get("BMX_ROUTE_IN_GEMV") != "0"
     sels, ws_ = [], []
     for p in range(P):
         sp, wp = layers[0].routing_fn(T, None, xs[p], {"logits": lgs[p]})
         sels.append(sp)
         ws_.append(wp)
     routes = [bmx.ops.dispatch(sels[p], E, 0, tabs[0].has_shared, rpg) for p in range(P)]
-    need_e = max(L.bmx_experts_workspace(ctypes.byref(l.desc), T, pa) for l in layers)
-    ews = torch.zeros(need_e, dtype=torch.uint8, device=dev)
-    out = torch.empty((T, H), dtype=torch.float32, device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    stages = ([("prep", bmx._lib.STAGE_PREP)] if prefill or mid else []) + [
+    stages = [("route", bmx._lib.STAGE_ROUTE)] + ([("prep", bmx._lib.STAGE_PREP)] if prefill or mid else []) + [
         ("gate_up", bmx._lib.STAGE_GATE_UP), ("act", bmx._lib.STAGE_ACT), ("down", bmx._lib.STAGE_DOWN),
         ("combine", bmx._lib.STAGE_COMBINE)]
     nst = steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(nst)]
-    for i in range(nst + warmup):
-        e = evs[i - warmup] if i >= warmup else None
+    evs = [[TimingEvent() for _ in range(len(stages) + 1)] for _ in range(nst)]
+
+    def staged_step(i, e):
         l, p = layers[i % NT], i % P
         for j, (_, st) in enumerate(stages):
-            if e: e[j].record()
-            bmx._lib.check(L.bmx_moe_stage(ctypes.byref(l.desc), st, Pp(xs[p]), T, ctypes.byref(routes[p].struct), None,
-                                           None, Pp(ws_[p]), Pp(out), Pp(ews), need_e, pa, s), "bmx_moe_stage")
-        if e: e[-1].record()
+            if e: e[j].record(s)
+            bmx._lib.check(L.bmx_moe_layer_stages(ctypes.byref(l.desc), ctypes.byref(l.router), Pp(xs[p]), Pp(lgs[p]), T,
+                                                  Pp(sel_b), Pp(w_b), Pp(out_b), Pp(lws), need, pa, 1 << st, s),
+                           "bmx_moe_layer_stages")
+        if e: e[-1].record(s)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warmup):
+        staged_step(i, None)
+    host_ms = (time.perf_counter() - t0) * 1e3 / max(1, warmup)      # host time to enqueue one staged step
+    torch.cuda.synchronize()
+    # Held-back timing: a bounded clock spin (torch.cuda._sleep) before each batch of steps keeps the stream busy while
+    # the host enqueues the batch, so the stages run back to back and the events time the kernels, not the host's
+    # launch gaps (the route stage of a one-token call launches nothing and reads as the event overhead)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    torch.cuda._sleep(1 << 21)
+    c1.record()
+    torch.cuda.synchronize()
+    cyc_per_ms = (1 << 21) / max(c0.elapsed_time(c1), 1e-3)
+    batch = 16
+    hold_cycles = int(min(50.0, 2.0 * batch * host_ms + 0.2) * cyc_per_ms)
+    for b0 in range(0, nst, batch):
+        torch.cuda._sleep(hold_cycles)
+        for i in range(b0, min(nst, b0 + batch)):
+            staged_step(warmup + i, evs[i])
     torch.cuda.synchronize()
     stage_ms = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j, (name, _) in enumerate(stages)}
     # algorithmic units of every timed step: trellis bytes of the unique experts touched, FLOPs of the routed rows
@@ -562,19 +627,26 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
                     "unit": "TFLOP/s", "frac": round(ach / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": traffic,
                     "algorithmic_flops": gu_flops, "kernel_us": round(gu_ms * 1e3, 3), "traffic_source": traffic_src,
                     "timing": "achieved uses the mean event-timed duration of the gate/up stage (one kernel launch) over "
-                              "the timed steps; kernel_us_rocprof is the committed trace's average for the same leg"}
+                              "the timed steps, enqueued behind a clock spin so the stages run back to back between "
+                              "timing-only events (no system-scope release); "
+                              "kernel_us_rocprof is the committed trace's average for the same leg"}
         if prof_us:
             roofline.update(kernel_us_rocprof=prof_us,
                             frac_rocprof=round(gu_flops / (prof_us * 1e-6) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4))
     else:
         gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
-        roofline = {"kernel": "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)",
+        kern = ("k_gemv_gu_route (BMX_STAGE_GATE_UP of the one-token layer call: routing + dispatch of the token, "
+                "then trellis decode + gate/up split-K GEMV)" if fused_route
+                else "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)")
+        roofline = {"kernel": kern,
                     "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "algorithmic_bytes": round(gu_bytes),
                     "kernel_us": round(gu_ms * 1e3, 3), "traffic_source": traffic_src,
                     "timing": "achieved uses the mean event-timed duration of the gate/up stage (one kernel launch) over "
-                              "the timed steps, each step on other experts; kernel_us_rocprof is the committed trace's "
-                              "average for the same leg (no event records around the kernel)"}
+                              "the timed steps, each step on other experts, enqueued behind a clock spin so the stages run "
+                              "back to back, between timing-only events (no system-scope release; an empty stage, the route "
+                              "stage of a one-token call, reads as the events' own cost); kernel_us_rocprof is the committed trace's average for the same leg (no event "
+                              "records around the kernel)"}
         if prof_us:
             roofline.update(kernel_us_rocprof=prof_us,
                             frac_rocprof=round(gu_bytes / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4))

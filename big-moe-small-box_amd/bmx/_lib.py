@@ -13,6 +13,7 @@ ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
 PATH_AUTO, PATH_DECODE, PATH_PREFILL, PATH_MID = 0, 1, 2, 3
 STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT, STAGE_PREP = 0, 1, 2, 3, 4, 5
 STAGE_GATE_UP_RESIDENT, STAGE_GATE_UP_STAGED = 6, 7
+STAGE_ROUTE = 8
 LANE_VRAM, LANE_ADMIT, LANE_HOME, LANE_CPU = 0, 1, 2, 3
 PLAN_MAXP, PLAN_MAXT = 64, 8
 
@@ -86,6 +87,8 @@ SIGNATURES = {
     "bmx_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "bmx_moe_layer_workspace": (_SZ, [ctypes.POINTER(MoeDesc), _I, _I]),
     "bmx_moe_layer": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _P, _SZ, _I, _P]),
+    "bmx_moe_layer_stages": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _P, _SZ, _I, _I,
+                                  _P]),
     "bmx_moe_layer_scratch": (_I, [ctypes.POINTER(MoeDesc), ctypes.POINTER(RouterDesc), _P, _P, _I, _P, _P, _P, _I, _P]),
     "bmx_slot_step": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, _I64, _I, _P]),
     "bmx_slot_copy": (_I, [ctypes.POINTER(SlotTable), _I, _P]),

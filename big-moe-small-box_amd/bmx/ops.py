@@ -172,3 +172,15 @@ def moe_layer(desc, router, x, logits, path=L.PATH_AUTO, workspace=None):
     check(lib().bmx_moe_layer(ctypes.byref(desc), ctypes.byref(router), _ptr(x), _ptr(logits), T, _ptr(sel), _ptr(w),
                               _ptr(out), _ptr(workspace), workspace.numel(), path, _stream()), "bmx_moe_layer")
     return out, sel, w
+
+
+def moe_layer_stages(desc, router, x, logits, sel, w, out, workspace, stages, path=L.PATH_AUTO):
+    """The stages in the mask `stages` (1 << STAGE_ROUTE, STAGE_PREP, STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN,
+    STAGE_COMBINE) of a moe_layer call into the caller's sel, w, out and workspace (at least
+    bmx_moe_layer_workspace bytes); calls over the stages in that order equal one moe_layer call bit for bit."""
+    _need(x, torch.float16, "x")
+    if logits is not None:
+        _need(logits, torch.float16, "logits")
+    check(lib().bmx_moe_layer_stages(ctypes.byref(desc), ctypes.byref(router), _ptr(x), _ptr(logits), x.shape[0],
+                                     _ptr(sel), _ptr(w), _ptr(out), _ptr(workspace), workspace.numel(), path, stages,
+                                     _stream()), "bmx_moe_layer_stages")

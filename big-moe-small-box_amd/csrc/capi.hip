@@ -373,28 +373,38 @@ size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path)
     return base + align_up((size_t)T * desc->E * 2, 256);
 }
 
-int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
-                  int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
-                  bmx_stream_t stream)
+// bmx_moe_layer and bmx_moe_layer_stages: the stages in `stages` (BMX_STAGE_ROUTE and the layer's expert stages) of
+// one layer call; every call of a staged sequence recomputes the same host-side plan, so the stages agree on the
+// workspace layout and the gate / up k-split count
+static int layer_call(const char* fn, const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16,
+                      const void* logits_fp16, int T, int64_t* sel, void* w_fp16, float* out, void* workspace,
+                      size_t workspace_bytes, int path, int stages, hipStream_t s)
 {
-    int rc = check_desc(desc, "bmx_moe_layer");
+    int rc = check_desc(desc, fn);
     if (rc) return rc;
-    if (!router) return set_error(BMX_ERR_ARG, "bmx_moe_layer: null router descriptor");
+    if (!router) return set_error(BMX_ERR_ARG, "%s: null router descriptor", fn);
     const int p = resolve_path(path, T, desc->topk);
-    if (p < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: unknown path %d", path);
-    if (T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_layer: T < 0");
+    if (p < 0) return set_error(BMX_ERR_ARG, "%s: unknown path %d", fn, path);
+    if (T < 0) return set_error(BMX_ERR_ARG, "%s: T < 0", fn);
+    if (!stages || (stages & ~(STAGES_LAYER | (1 << BMX_STAGE_ROUTE))))
+        return set_error(BMX_ERR_ARG, "%s: stage mask 0x%x (route, prep, gate / up, act, down and combine only)", fn,
+                         stages);
     if (T == 0) return BMX_OK;
-    if (!x_fp16 || !sel || !w_fp16 || !out || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_layer: null pointer");
+    if (!x_fp16 || !sel || !w_fp16 || !out || !workspace) return set_error(BMX_ERR_ARG, "%s: null pointer", fn);
     if (!logits_fp16 && !router->weight)
-        return set_error(BMX_ERR_ARG, "bmx_moe_layer: no logits and no router weight to project them with");
+        return set_error(BMX_ERR_ARG, "%s: no logits and no router weight to project them with", fn);
     const size_t need = bmx_moe_layer_workspace(desc, T, path);
-    if (workspace_bytes < need) return set_error(BMX_ERR_WORKSPACE, "bmx_moe_layer: workspace %zu < %zu", workspace_bytes, need);
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (workspace_bytes < need) return set_error(BMX_ERR_WORKSPACE, "%s: workspace %zu < %zu", fn, workspace_bytes, need);
+    const bool route = stages & (1 << BMX_STAGE_ROUTE);
+    stages &= STAGES_LAYER;
     if (!logits_fp16)
     {
         void* lg = static_cast<char*>(workspace) + bmx_moe_workspace(desc, T, path);
-        rc = launch_router_logits(x_fp16, router->weight, T, desc->H, desc->E, lg, s);
-        if (rc) return rc;
+        if (route)
+        {
+            rc = launch_router_logits(x_fp16, router->weight, T, desc->H, desc->E, lg, s);
+            if (rc) return rc;
+        }
         logits_fp16 = lg;
     }
     const MoeShape m = shape_of(desc, T);
@@ -414,21 +424,43 @@ int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const
         rc = route_fuse_args(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group, router->topk_group,
                              router->score_fn, router->renorm, router->scale, desc->first, sel, w_fp16, m.shared, rpg,
                              &r, &f);
-        if (rc) return rc;
-        return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER, &f);
+        if (rc || !stages) return rc;
+        return launch_decode_experts(m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, stages, &f);
     }
-    if (route_dispatch_small_fits(T, desc->E, desc->topk))
-        rc = launch_route_dispatch_small(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group,
-                                         router->topk_group, router->score_fn, router->renorm, router->scale,
-                                         desc->first, sel, w_fp16, m.shared, rpg, &r, s);
-    else
+    if (route)
     {
-        rc = launch_router(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group, router->topk_group,
-                           router->score_fn, router->renorm, router->scale, desc->first, sel, w_fp16, s);
-        if (!rc) rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr, 0, s);
+        if (route_dispatch_small_fits(T, desc->E, desc->topk))
+            rc = launch_route_dispatch_small(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group,
+                                             router->topk_group, router->score_fn, router->renorm, router->scale,
+                                             desc->first, sel, w_fp16, m.shared, rpg, &r, s);
+        else
+        {
+            rc = launch_router(logits_fp16, router->bias, T, desc->E, desc->topk, router->n_group, router->topk_group,
+                               router->score_fn, router->renorm, router->scale, desc->first, sel, w_fp16, s);
+            if (!rc)
+                rc = launch_dispatch(sel, T, desc->topk, desc->E, desc->first, m.shared, rpg, &r, dws, dws_bytes, nullptr,
+                                     0, s);
+        }
+        if (rc) return rc;
     }
-    if (rc) return rc;
-    return launch_experts(p, m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, STAGES_LAYER);
+    if (!stages) return BMX_OK;
+    return launch_experts(p, m, x_fp16, &r, nullptr, nullptr, ews, ews_bytes, out, w_fp16, s, stages);
+}
+
+int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
+                  int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
+                  bmx_stream_t stream)
+{
+    return layer_call("bmx_moe_layer", desc, router, x_fp16, logits_fp16, T, sel, w_fp16, out, workspace,
+                      workspace_bytes, path, STAGES_LAYER | (1 << BMX_STAGE_ROUTE), static_cast<hipStream_t>(stream));
+}
+
+int bmx_moe_layer_stages(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16,
+                         const void* logits_fp16, int T, int64_t* sel, void* w_fp16, float* out, void* workspace,
+                         size_t workspace_bytes, int path, int stages, bmx_stream_t stream)
+{
+    return layer_call("bmx_moe_layer_stages", desc, router, x_fp16, logits_fp16, T, sel, w_fp16, out, workspace,
+                      workspace_bytes, path, stages, static_cast<hipStream_t>(stream));
 }
 
 int bmx_moe_layer_scratch(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16,

@@ -790,8 +790,8 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
                           void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages,
                           const RouteFuse* rf)
 {
-    if (rf && (m.T != 1 || rows_per_group_of(m.T) != 1 || !(stages & (1 << BMX_STAGE_GATE_UP))))
-        return set_error(BMX_ERR_ARG, "moe experts: routing inside the GEMV is for one-token calls with the gate / up stage");
+    if (rf && (m.T != 1 || rows_per_group_of(m.T) != 1))
+        return set_error(BMX_ERR_ARG, "moe experts: routing inside the GEMV is for one-token calls");
     if (m.H % 128 || m.I % 128 || m.H <= 0 || m.I <= 0)
         return set_error(BMX_ERR_ARG, "moe experts: H (%d) and I (%d) must be multiples of 128", m.H, m.I);
     const DecodePlan p = decode_plan(m);

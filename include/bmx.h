@@ -170,6 +170,12 @@ size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path);
 int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
                   int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
                   bmx_stream_t stream);
+/* bmx_moe_layer one stage set at a time (bit BMX_STAGE_ROUTE, then PREP, GATE_UP, ACT, DOWN, COMBINE, in that order over
+ * calls with the same arguments and workspace): each call launches the kernels of its stages only, so a caller can time
+ * them or put work between them. The calls together equal one bmx_moe_layer call bit for bit. */
+int bmx_moe_layer_stages(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16,
+                         const void* logits_fp16, int T, int64_t* sel, void* w_fp16, float* out, void* workspace,
+                         size_t workspace_bytes, int path, int stages, bmx_stream_t stream);
 
 /* The same layer call with no workspace argument and no allocation: for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
@@ -205,7 +211,10 @@ enum bmx_stage {
     BMX_STAGE_PREP = 5,
     /* BMX_STAGE_GATE_UP split by desc->fresh: the groups of experts that were resident before the slot-table step, and
      * the groups of experts it admitted (run after their copies). Together they equal BMX_STAGE_GATE_UP. */
-    BMX_STAGE_GATE_UP_RESIDENT = 6, BMX_STAGE_GATE_UP_STAGED = 7
+    BMX_STAGE_GATE_UP_RESIDENT = 6, BMX_STAGE_GATE_UP_STAGED = 7,
+    /* bmx_moe_layer_stages only: the router projection (when no logits are given), then the router and the dispatch
+     * (these two are BMX_STAGE_GATE_UP's work instead where the one-token gate / up GEMV routes the token itself) */
+    BMX_STAGE_ROUTE = 8
 };
 int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T, const bmx_routes* routes,
                   void* act_rows_fp16, float* y_rows, const void* w_fp16, float* out, void* workspace,

@@ -264,6 +264,61 @@ def test_layer_parity(cuda, oracle, monkeypatch, name, cfgname, T, rows, kw):
     assert np.array_equal(out, out2)
 
 
+STAGED = [("c1 T1", "c1", 1, True), ("c2 T1", "c2", 1, False), ("c2 T1 projected", "c2", 1, True),
+          ("c2 T8", "c2", 8, False), ("c3 shape T128", "c3", 128, True)]
+
+
+@pytest.mark.parametrize("name,cfgname,T,project", STAGED, ids=[s[0] for s in STAGED])
+@pytest.mark.parametrize("route_in_gemv", ["1", "0"])
+def test_layer_stages_equal_one_call(cuda, monkeypatch, name, cfgname, T, project, route_in_gemv):
+    """bmx_moe_layer_stages over the stages one call at a time, and in two halves, gives the one-call layer's out, sel
+    and w bit for bit: with the one-token gate / up GEMV routing the token itself and without, with the router
+    projection in the route stage (no logits given) and without."""
+    import bmx
+    from bmx import synth
+    L = bmx._lib
+    monkeypatch.setenv("BMX_ROUTE_IN_GEMV", route_in_gemv)
+    c = synth.CONFIGS[cfgname]
+    tab = synth.table(cfgname, seed=11, device=cuda, E=min(c["E"], 64))
+    E = tab.E
+    x, lg, bias = synth.inputs(cfgname, T=T, seed=12, device=cuda)
+    lg = lg[:, :E].contiguous()
+    bias = bias[:E].contiguous() if bias is not None else None
+    rw = (torch.randn(E, tab.H, generator=torch.Generator().manual_seed(13)) * 0.02).half().to(cuda) if project else None
+    layer = bmx.MoELayer(tab, c["topk"], score=c["score"], bias=bias, n_group=c["n_group"] if E == c["E"] else 1,
+                         topk_group=c["topk_group"] if E == c["E"] else 1, renorm=c["renorm"], scale=c["scale"],
+                         router_weight=rw)
+    logits = None if project else lg
+    say("stages", name, "route_in_gemv", route_in_gemv, "one call")
+    out, sel, w = bmx.ops.moe_layer(layer.desc, layer.router, x, logits)
+    need = L.lib().bmx_moe_layer_workspace(layer.desc, T, L.PATH_AUTO)
+    one = [L.STAGE_ROUTE, L.STAGE_PREP, L.STAGE_GATE_UP, L.STAGE_ACT, L.STAGE_DOWN, L.STAGE_COMBINE]
+    for seq in ([1 << st for st in one], [sum(1 << st for st in one[:3]), sum(1 << st for st in one[3:])]):
+        ws = torch.full((need,), 0x7f, dtype=torch.uint8, device=cuda)
+        o2 = torch.full_like(out, float("nan"))
+        s2, w2 = torch.full_like(sel, -7), torch.full_like(w, float("nan"))
+        say("stages", name, "masks", [hex(m) for m in seq])
+        for m in seq:
+            bmx.ops.moe_layer_stages(layer.desc, layer.router, x, logits, s2, w2, o2, ws, m)
+        torch.cuda.synchronize()
+        assert torch.equal(s2, sel) and torch.equal(w2.view(torch.int16), w.view(torch.int16))
+        assert torch.equal(o2.view(torch.int32), out.view(torch.int32))
+
+
+def test_layer_stages_rejects_bad_mask(cuda):
+    import bmx
+    from bmx import synth
+    tab = synth.table("c1", seed=1, device=cuda, E=16)
+    x, lg, _ = synth.inputs("c1", T=1, seed=2, device=cuda)
+    layer = bmx.MoELayer(tab, 4)
+    o = torch.empty(1, tab.H, device=cuda)
+    s, w = torch.empty(1, 4, dtype=torch.int64, device=cuda), torch.empty(1, 4, dtype=torch.float16, device=cuda)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=cuda)
+    for m in (0, 1 << bmx._lib.STAGE_DOWN_OUT, 1 << 9):
+        with pytest.raises(bmx.BmxError, match="stage mask"):
+            bmx.ops.moe_layer_stages(layer.desc, layer.router, x, lg[:, :16].contiguous(), s, w, o, ws, m)
+
+
 def test_act_rows_match_oracle(cuda, oracle):
     """The fp16 down-input rows (rotated activation) equal the oracle's except where the fp32 vs exact accumulation
     of gate / up lands on the other side of an fp16 rounding boundary; a flipped gate / up value moves all 128 values
