@@ -99,7 +99,6 @@ __device__ __forceinline__ void gemv_any(int fmt, const uint8_t* mat, int tn, in
 
 template <int B>
 __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint16_t* dst);
-
 // ---- split-K grouped GEMV -> partial sums ------------------------------------------------------------------------------
 // NM = 2: gate and up of the same expert on rotated x rows (the rotation is computed here, per matrix suh); waves 0-1
 // take gate and waves 2-3 up, each half of the k-range, so a wave runs one format's code. NM = 1: down on the rotated
@@ -283,35 +282,38 @@ __global__ __launch_bounds__(GV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8
 // decode-size launch spreads over more CUs) for small ones.
 // acc[4 v + i] = sum over splits s = 0, 1, ... ks - 1 in that order of p[s * stride + off(v) + i], off = 0, 4, 128, 132
 // (NV = 4: gate 8 | up 8) or 0, 4 (NV = 2). The loads of B splits are issued together before their adds, so a long
-// split list costs one memory latency per B splits instead of one per split.
+// split list costs one memory latency per B splits instead of one per split; a last batch of fewer than B splits loads
+// the last split again in place of the missing ones (in bounds, no branch between the loads) and skips their adds.
+template <int NV, int B>
+__device__ __forceinline__ void sum_splits_batch(const float* p, size_t stride, int s, int ks, float (&acc)[NV * 4])
+{
+    const int n = ks - s < B ? ks - s : B;
+    f32x4 q[B][NV];
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+    {
+        const int sb = b < n ? s + b : ks - 1;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) q[b][v] = ldg4f(p + (size_t)sb * stride + (v & 1) * 4 + (v >> 1) * 128);
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+        if (b < n)
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[b][v][i];
+}
+
+// the first batch outside the loop: straight-line code, so its loads issue beside the caller's earlier ones (a loop
+// entry makes the compiler wait for every load in flight)
 template <int NV, int B>
 __device__ __forceinline__ void sum_splits(const float* p, size_t stride, int ks, float (&acc)[NV * 4])
 {
 #pragma unroll
     for (int i = 0; i < NV * 4; ++i) acc[i] = 0.0f;
-    int s = 0;
-    for (; s + B <= ks; s += B)
-    {
-        f32x4 q[B][NV];
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-#pragma unroll
-            for (int v = 0; v < NV; ++v) q[b][v] = ldg4f(p + (size_t)(s + b) * stride + (v & 1) * 4 + (v >> 1) * 128);
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-#pragma unroll
-            for (int v = 0; v < NV; ++v)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[b][v][i];
-    }
-    for (; s < ks; ++s)
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-        {
-            const f32x4 q = ldg4f(p + (size_t)s * stride + (v & 1) * 4 + (v >> 1) * 128);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[i];
-        }
+    if (ks > 0) sum_splits_batch<NV, B>(p, stride, 0, ks, acc);
+    for (int s = B; s < ks; s += B) sum_splits_batch<NV, B>(p, stride, s, ks, acc);
 }
 
 template <int UPW>
@@ -376,6 +378,16 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
 {
     const int lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
     const int nrows = a.offsets[a.NE], e = a.row_expert[r];
+    const int col = cb * 128 + 8 * j;
+    // the row's scale vectors first: their chain of loads (expert record, then vectors) overlaps the split sums' loads
+    u32x4 svg4 = {0u, 0u, 0u, 0u}, svu4 = svg4, sud4 = svg4;
+    if (r < nrows)
+    {
+        const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
+        svg4 = ldg4(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col);
+        svu4 = ldg4(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col);
+        sud4 = ldg4(reinterpret_cast<const uint16_t*>(ex.suh[2]) + col);
+    }
     float g[8], v[8];
     if (a.gu_half)
     {
@@ -399,14 +411,12 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
 #pragma unroll
         for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(gu[i])); v[i] = h2f(f2h_r(gu[8 + i])); }
     }
-    const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-    const int col = cb * 128 + 8 * j;
     had128_x8(g);
     had128_x8(v);
     float svg[8], svu[8], sud[8];
-    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col), svg);
-    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col), svu);
-    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.suh[2]) + col), sud);
+    unpack8(svg4, svg);
+    unpack8(svu4, svu);
+    unpack8(sud4, sud);
     float act[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -435,10 +445,11 @@ __device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float 
     const int j = threadIdx.x & 15;
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
+    const u32x4 sv4 = ldg4(reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 8 * j);   // before the split loads
     sum_splits<2, 8>(a.part_dn + ((size_t)r * a.NBH + cb) * 128 + 8 * j, (size_t)a.R_max * a.NBH * 128, a.KS_dn, y);
     had128_x8(y);
     float sv[8];
-    unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 8 * j), sv);
+    unpack8(sv4, sv);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = (y[i] * R_SCALE) * sv[i];
 }
@@ -509,14 +520,12 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
     store8f(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
 }
 
-// Small launches: one workgroup per (token, 128-column block); 16-lane group k computes slot k (the shared expert's row
-// is slot topk), then group 0 sums them in slot order: the same sums in the same order as k_dn_combine.
+// The combine of token t's 128-column block cb by one workgroup: 16-lane group k computes slot k (the shared expert's
+// row is slot topk) into ys[k], then group 0 sums them in slot order: the same sums in the same order as k_dn_combine.
+// ys: [topk + 1][128] floats and live: [topk + 1] ints of LDS.
 constexpr int CB_MAXS = 33;
-__global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
+__device__ __forceinline__ void combine_block(const GvArgs& a, int t, int cb, float (*ys)[128], int* live)
 {
-    __shared__ float ys[CB_MAXS][128];
-    __shared__ int live[CB_MAXS];
-    const int t = blockIdx.x / a.NBH, cb = blockIdx.x % a.NBH;
     const int k0 = threadIdx.x >> 4, j = threadIdx.x & 15;
     const int ns = a.topk + (a.has_shared ? 1 : 0);
     for (int k = k0; k < ns; k += GV_THREADS / 16)
@@ -525,7 +534,8 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
         if (k < a.topk)
         {
             r = a.inv[t * a.topk + k];
-            if (r < 0 || h2f(a.w[t * a.topk + k]) == 0.0f)
+            const float wk = h2f(a.w[t * a.topk + k]);      // loaded beside r, not after it
+            if (r < 0 || wk == 0.0f)
             {
                 if (j == 0) live[k] = 0;
                 continue;
@@ -567,6 +577,14 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = o[i] + ys[a.topk][8 * j + i];
     store8f(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
+}
+
+// Small launches: one workgroup per (token, 128-column block).
+__global__ __launch_bounds__(GV_THREADS) void k_dn_combine_par(GvArgs a)
+{
+    __shared__ float ys[CB_MAXS][128];
+    __shared__ int live[CB_MAXS];
+    combine_block(a, blockIdx.x / a.NBH, blockIdx.x % a.NBH, ys, live);
 }
 
 // ---- standalone combine ----------------------------------------------------------------------------------------------
