@@ -282,20 +282,53 @@ __global__ __launch_bounds__(GV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8
 // decode-size launch spreads over more CUs) for small ones.
 // acc[4 v + i] = sum over splits s = 0, 1, ... ks - 1 in that order of p[s * stride + off(v) + i], off = 0, 4, 128, 132
 // (NV = 4: gate 8 | up 8) or 0, 4 (NV = 2). The loads of B splits are issued together before their adds, so a long
-// split list costs one memory latency per B splits instead of one per split; a last batch of fewer than B splits loads
-// the last split again in place of the missing ones (in bounds, no branch between the loads) and skips their adds.
+// split list costs one memory latency per B splits instead of one per split.
 template <int NV, int B>
-__device__ __forceinline__ void sum_splits_batch(const float* p, size_t stride, int s, int ks, float (&acc)[NV * 4])
+__device__ __forceinline__ void sum_splits(const float* p, size_t stride, int ks, float (&acc)[NV * 4])
 {
-    const int n = ks - s < B ? ks - s : B;
+#pragma unroll
+    for (int i = 0; i < NV * 4; ++i) acc[i] = 0.0f;
+    int s = 0;
+    for (; s + B <= ks; s += B)
+    {
+        f32x4 q[B][NV];
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) q[b][v] = ldg4f(p + (size_t)(s + b) * stride + (v & 1) * 4 + (v >> 1) * 128);
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[b][v][i];
+    }
+    for (; s < ks; ++s)
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+        {
+            const f32x4 q = ldg4f(p + (size_t)s * stride + (v & 1) * 4 + (v >> 1) * 128);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[i];
+        }
+}
+
+// The same sums for the one-token launches, where a few workgroups wait on this chain of loads and their register count
+// does not matter: a short last batch also issues all its loads before the first add (not one round trip per split),
+// and the first batch sits outside the loop, in straight-line code, so its loads issue beside the caller's earlier ones
+// (a loop entry makes the compiler wait for every load in flight). The large launches keep sum_splits: this form needs
+// more registers, which costs them occupancy.
+template <int NV, int B>
+__device__ __forceinline__ void sum_splits_short_batch(const float* p, size_t stride, int s, int ks,
+                                                       float (&acc)[NV * 4])
+{
+    const int n = ks - s < B ? ks - s : B;       // uniform: the branches below split no wave
     f32x4 q[B][NV];
 #pragma unroll
     for (int b = 0; b < B; ++b)
-    {
-        const int sb = b < n ? s + b : ks - 1;
+        if (b < n)
 #pragma unroll
-        for (int v = 0; v < NV; ++v) q[b][v] = ldg4f(p + (size_t)sb * stride + (v & 1) * 4 + (v >> 1) * 128);
-    }
+            for (int v = 0; v < NV; ++v) q[b][v] = ldg4f(p + (size_t)(s + b) * stride + (v & 1) * 4 + (v >> 1) * 128);
 #pragma unroll
     for (int b = 0; b < B; ++b)
         if (b < n)
@@ -305,15 +338,13 @@ __device__ __forceinline__ void sum_splits_batch(const float* p, size_t stride, 
                 for (int i = 0; i < 4; ++i) acc[4 * v + i] = acc[4 * v + i] + q[b][v][i];
 }
 
-// the first batch outside the loop: straight-line code, so its loads issue beside the caller's earlier ones (a loop
-// entry makes the compiler wait for every load in flight)
 template <int NV, int B>
-__device__ __forceinline__ void sum_splits(const float* p, size_t stride, int ks, float (&acc)[NV * 4])
+__device__ __forceinline__ void sum_splits_short(const float* p, size_t stride, int ks, float (&acc)[NV * 4])
 {
 #pragma unroll
     for (int i = 0; i < NV * 4; ++i) acc[i] = 0.0f;
-    if (ks > 0) sum_splits_batch<NV, B>(p, stride, 0, ks, acc);
-    for (int s = B; s < ks; s += B) sum_splits_batch<NV, B>(p, stride, s, ks, acc);
+    if (ks > 0) sum_splits_short_batch<NV, B>(p, stride, 0, ks, acc);
+    for (int s = B; s < ks; s += B) sum_splits_short_batch<NV, B>(p, stride, s, ks, acc);
 }
 
 template <int UPW>
@@ -402,7 +433,7 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
         const size_t stride = (size_t)a.R_max * a.NB * 256;
         const float* p = a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j + (size_t)q * stride;
         float gu[16];
-        sum_splits<4, B>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
+        sum_splits_short<4, B>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
 #pragma unroll
         for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor16_f(gu[i]);
 #pragma unroll
@@ -439,14 +470,28 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi_w(GvArgs a)
     gu_epi_wave<4>(a, r, cb, a.act_rows + (size_t)r * a.I + cb * 128);
 }
 
-// down output of row r, block cb, lane's 8 columns: sum of the splits -> H128 * R * svh
+// down output of row r, block cb, lane's 8 columns: sum of the splits -> H128 * R * svh. SHORT (one-token launches): the
+// scale vector is loaded before the split sums (its chain of loads overlaps theirs) and the sums take sum_splits_short.
+template <bool SHORT>
 __device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float (&y)[8])
 {
     const int j = threadIdx.x & 15;
     const int e = a.row_expert[r];
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-    const u32x4 sv4 = ldg4(reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 8 * j);   // before the split loads
-    sum_splits<2, 8>(a.part_dn + ((size_t)r * a.NBH + cb) * 128 + 8 * j, (size_t)a.R_max * a.NBH * 128, a.KS_dn, y);
+    const uint16_t* svp = reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 8 * j;
+    const float* pp = a.part_dn + ((size_t)r * a.NBH + cb) * 128 + 8 * j;
+    const size_t stride = (size_t)a.R_max * a.NBH * 128;
+    u32x4 sv4;
+    if (SHORT)
+    {
+        sv4 = ldg4(svp);
+        sum_splits_short<2, 8>(pp, stride, a.KS_dn, y);
+    }
+    else
+    {
+        sum_splits<2, 8>(pp, stride, a.KS_dn, y);
+        sv4 = ldg4(svp);
+    }
     had128_x8(y);
     float sv[8];
     unpack8(sv4, sv);
@@ -469,7 +514,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_epi(GvArgs a)
     const int r = u / a.NBH, cb = u % a.NBH;
     if (r >= a.offsets[a.NE]) return;
     float y[8];
-    down_out8(a, r, cb, y);
+    down_out8<UPW == 1>(a, r, cb, y);
     store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
 }
 
@@ -489,7 +534,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
         const int r = a.inv[t * a.topk + k];
         const float wk = h2f(a.w[t * a.topk + k]);
         if (r < 0 || wk == 0.0f) continue;
-        down_out8(a, r, cb, y);
+        down_out8<false>(a, r, cb, y);
         if (a.y_rows) store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -501,7 +546,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
     if (a.has_shared)
     {
         const int r = a.offsets[a.E] + t;
-        down_out8(a, r, cb, y);
+        down_out8<false>(a, r, cb, y);
         if (a.y_rows) store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
         if (a.sh_gate)
         {
@@ -543,7 +588,7 @@ __device__ __forceinline__ void combine_block(const GvArgs& a, int t, int cb, fl
         }
         else r = a.offsets[a.E] + t;
         float y[8];
-        down_out8(a, r, cb, y);
+        down_out8<true>(a, r, cb, y);
         if (a.y_rows) store8f(a.y_rows + (size_t)r * a.H + cb * 128 + 8 * j, y);
 #pragma unroll
         for (int i = 0; i < 8; ++i) ys[k][8 * j + i] = y[i];
