@@ -70,3 +70,20 @@ def test_geometry_known_answers():
     assert ExpertTable.geometry(4096, 2048, [(2, 2, 2)]) == (3145728, 6291456, 9437184)
     assert ExpertTable.geometry(5120, 2304, [(1, 1, 1)]) == (3686400, 7372800, 11059200)
     assert ExpertTable.geometry(5120, 2304, [(0, 0, 0)])[0] == 2949120
+
+
+def test_layer_stages_mask_checks():
+    """bmx_moe_layer_stages refuses a mask outside route / prep / gate-up / act / down / combine (before any device
+    work, so on the host), and a zero-token call with a valid mask does nothing."""
+    import bmx
+    B = bmx._lib
+    L = bmx.lib()
+    d = B.MoeDesc(4096, 1536, 288, 8, 0, 0, 1, 0.0, ctypes.c_void_p(1), ctypes.c_void_p(2))
+    r = B.RouterDesc()
+    for m in (0, 1 << B.STAGE_DOWN_OUT, 1 << B.STAGE_GATE_UP_STAGED, 1 << 9):
+        assert L.bmx_moe_layer_stages(ctypes.byref(d), ctypes.byref(r), None, None, 0, None, None, None, None, 0, 0, m,
+                                      None) == B.BMX_ERR_ARG
+        assert b"stage mask" in L.bmx_last_error()
+    ok = (1 << B.STAGE_ROUTE) | (1 << B.STAGE_GATE_UP)
+    assert L.bmx_moe_layer_stages(ctypes.byref(d), ctypes.byref(r), None, None, 0, None, None, None, None, 0, 0, ok,
+                                  None) == 0
