@@ -587,6 +587,24 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
             staged_step(warmup + i, evs[i])
     torch.cuda.synchronize()
     stage_ms = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j, (name, _) in enumerate(stages)}
+    gu_sep_ms = None
+    if fused_route:
+        # the same steps with the routing in its own launch (BMX_ROUTE_IN_GEMV=0, read at each call): the gate / up GEMV
+        # alone (k_gemv_part<1,2>, the plan's k-splits), for the roofline's view of the GEMV without the routing
+        os.environ["BMX_ROUTE_IN_GEMV"] = "0"
+        try:
+            for i in range(warmup):
+                staged_step(i, None)
+            torch.cuda.synchronize()
+            for b0 in range(0, nst, batch):
+                torch.cuda._sleep(hold_cycles)
+                for i in range(b0, min(nst, b0 + batch)):
+                    staged_step(warmup + i, evs[i])
+            torch.cuda.synchronize()
+            j = [n for n, _ in stages].index("gate_up")
+            gu_sep_ms = statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs)
+        finally:
+            del os.environ["BMX_ROUTE_IN_GEMV"]
     # algorithmic units of every timed step: trellis bytes of the unique experts touched, FLOPs of the routed rows
     gu_bytes = dn_bytes = 0
     rows_tot = 0
@@ -650,6 +668,12 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         if prof_us:
             roofline.update(kernel_us_rocprof=prof_us,
                             frac_rocprof=round(gu_bytes / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4))
+        if gu_sep_ms:
+            sep = gu_bytes / (gu_sep_ms * 1e-3) / 1e9
+            roofline.update(gemv_without_routing={
+                "kernel": "k_gemv_part<1,2> (the same steps with the routing in its own launch, BMX_ROUTE_IN_GEMV=0)",
+                "kernel_us": round(gu_sep_ms * 1e3, 3), "achieved": round(sep, 1),
+                "frac": round(sep / HBM_PEAK_GBPS, 4)})
     scores = {0: "softmax", 1: "sigmoid"}[c["score"]] + ("+bias" if c["bias"] else "")
     if c["n_group"] > 1:
         scores = f"group-limited ({c['n_group']} groups, top-{c['topk_group']}) {scores}"
