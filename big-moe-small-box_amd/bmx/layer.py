@@ -80,7 +80,8 @@ class MoELayer:
         if self.slots is None:
             return sel, w, False
         if getattr(self.slots, "planned", False):
-            sel_gpu, w_gpu, _, seq = self.slots.step_planned(li, sel, w, z, True, first=self.routing_first)
+            sel_gpu, w_gpu, _, seq = self.slots.step_planned(li, sel, w, z, True, first=self.routing_first,
+                                                             bsz=bsz)
             if self.slots.cpu_ready and z is not None and bsz <= L.PLAN_MAXT and sel.numel() <= L.PLAN_MAXP:
                 self._cpu_seq = seq
             return sel_gpu.view(sel.shape), w_gpu.view(w.shape), self._cpu_seq is not None

@@ -147,6 +147,8 @@ def moe_experts(desc, x, routes, path=L.PATH_AUTO, with_act=False):
 
 
 def combine(y_rows, routes, w, H):
+    """bmx_combine: the weighted slot-ordered sum of the expert rows, the shared expert's row added with weight 1 (a
+    layer with a gated shared expert is combined by its own layer call, which applies sigmoid(x . g))."""
     T, topk = routes.T, routes.topk
     out = torch.empty((T, H), dtype=torch.float32, device=y_rows.device)
     check(lib().bmx_combine(_ptr(y_rows), _ptr(routes.inv), _ptr(w), _ptr(routes.offsets), T, topk, H, routes.E,

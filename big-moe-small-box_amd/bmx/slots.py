@@ -251,13 +251,23 @@ class ExpertSlots:
                 "bmx_copy_agent_cpu_lane")
         self.cpu_ready = True
 
-    def step_planned(self, li, sel, w, x=None, admit=True, *, first=None):
+    def step_planned(self, li, sel, w, x=None, admit=True, *, first=None, bsz=None):
         """A planned step of layer li (bmx_slot_step_planned): publishes the call to the agent's planner, waits for its
-        reply and applies it. sel int64 [n], w fp16 [n] (device; n = T * topk), x fp16 [T, H] (the call's rows, for the
-        CPU lane) or None. Returns (sel_gpu, w_gpu, lanes, seq): the selection the GPU computes, each pick's lane, and
-        the step's sequence number (for cpu_add)."""
-        T = sel.shape[0] if sel.dim() == 2 else 1
-        topk = sel.numel() // max(T, 1)
+        reply and applies it. sel int64 [T, topk], w fp16 [T, topk] (device), x fp16 [T, H] (the call's rows, for the
+        CPU lane) or None; bsz: T, required when sel is not two-dimensional (a flattened [T * topk] selection). Returns
+        (sel_gpu, w_gpu, lanes, seq): the selection the GPU computes, each pick's lane, and the step's sequence number
+        (for cpu_add)."""
+        if bsz is not None:
+            T = int(bsz)
+            if T <= 0 or sel.numel() % T:
+                raise ValueError(f"ExpertSlots.step_planned: {sel.numel()} picks are not bsz = {T} tokens of topk")
+        elif sel.dim() == 2:
+            T = sel.shape[0]
+        else:
+            raise ValueError("ExpertSlots.step_planned: sel must be [T, topk], or pass bsz with a flattened selection")
+        topk = sel.numel() // T
+        if w.numel() != sel.numel():
+            raise ValueError("ExpertSlots.step_planned: w must hold one weight per pick")
         sel = sel.reshape(-1)
         if sel.dtype != torch.int64 or not sel.is_contiguous():
             sel = sel.long().contiguous()

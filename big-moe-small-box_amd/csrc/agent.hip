@@ -218,13 +218,16 @@ static void plan_reply(bmx_copy_agent* a, const PlanReq& r, PlanRep& p, CpuJob* 
     std::stable_sort(miss.begin(), miss.end(), [&](int x, int y) {
         return r.cnt[x] != r.cnt[y] ? r.cnt[x] > r.cnt[y] : r.ex[x] < r.ex[y];
     });
-    double g = pol.gpu_base_us + pol.gpu_hit_us * nres, c = 0.0;
+    // start times: the GPU's at its base plus the hits (0 with nothing resident), the CPU lane's at its base whenever it
+    // may take a miss, so the base sits on both sides of the comparison (engine/kernels/nv2/nv2_host.cpp:1017-1018)
+    double g = nres ? pol.gpu_base_us + pol.gpu_hit_us * nres : 0.0;
+    double c = (cpu_ok && !miss.empty()) ? pol.cpu_base_us : 0.0;
     int ncpu = 0;
     for (int u : miss)
     {
         const bool home = pol.home_single && r.ntok > 1 && r.cnt[u] == 1;
         const double gc = home ? pol.gpu_home_us : pol.gpu_admit_us;
-        const double cc = (ncpu == 0 ? pol.cpu_base_us : 0.0) + pol.cpu_expert_us + pol.cpu_token_us * (r.cnt[u] - 1);
+        const double cc = pol.cpu_expert_us + pol.cpu_token_us * (r.cnt[u] - 1);
         if (cpu_ok && ncpu < pol.max_cpu && std::max(c + cc, g) <= std::max(c, g + gc))
         {
             p.lane[u] = BMX_LANE_CPU;

@@ -18,6 +18,8 @@
 
 #include <stdlib.h>
 
+#include <atomic>
+
 namespace bmx {
 
 constexpr int GV_WAVES = 4;
@@ -815,19 +817,22 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
     if (stages & (1 << BMX_STAGE_DOWN_OUT)) launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
 }
 
-// compute units of the current device (each device asked once)
+// Compute units of the current device (each device asked once; threads that race on the first call store the same
+// value). BMX_CU_COUNT overrides it, so a test can take the split count another device would take.
 static int cu_count()
 {
-    static int n[64];
+    static std::atomic<int> n[64];
+    const char* ov = getenv("BMX_CU_COUNT");
+    if (ov && *ov && atoi(ov) > 0) return atoi(ov);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!n[dev])
+    int v = n[dev].load(std::memory_order_relaxed);
+    if (!v)
     {
-        int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        n[dev] = v;
+        n[dev].store(v, std::memory_order_relaxed);
     }
-    return n[dev];
+    return v;
 }
 
 // The routing gate / up GEMV pays the routing at the start of every workgroup, so it takes the most k-splits (at most

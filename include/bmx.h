@@ -165,7 +165,9 @@ typedef struct bmx_router_desc {
  * NULL: the logits are projected from x with router->weight first (bmx_router_logits, into the workspace). One token on
  * the decode path: the gate / up GEMV routes it and writes the dispatch itself (BMX_ROUTE_IN_GEMV=0: separate launch),
  * with as many gate / up k-splits as start in one round, which can be fewer than bmx_decode_splits reports for the
- * separate calls: the same routing, the output within the layer tolerance of theirs. */
+ * separate calls: the same routing, the output within the layer tolerance of theirs. That count follows the device's
+ * compute-unit count (5 workgroups per unit), so one-token outputs can differ in their last bits between devices or
+ * partition modes with other unit counts (BMX_CU_COUNT overrides the count; BMX_KS_GU forces the plan's splits). */
 size_t bmx_moe_layer_workspace(const bmx_moe_desc* desc, int T, int path);
 int bmx_moe_layer(const bmx_moe_desc* desc, const bmx_router_desc* router, const void* x_fp16, const void* logits_fp16,
                   int T, int64_t* sel, void* w_fp16, float* out, void* workspace, size_t workspace_bytes, int path,
@@ -382,14 +384,17 @@ int bmx_dot2_f32_f16(const uint32_t* a, const uint32_t* b, const float* c, float
 #define BMX_PLAN_MAXT 8
 enum { BMX_LANE_VRAM = 0, BMX_LANE_ADMIT = 1, BMX_LANE_HOME = 2, BMX_LANE_CPU = 3 };
 /* The planner: list scheduling of a call's non-resident experts onto two lanes by estimated finish time (the
- * reference's rule, nv2_host.cpp:1030-1041). The GPU's time starts at gpu_base_us + gpu_hit_us per resident expert, the
- * CPU lane's at 0. The experts not resident are taken by picks descending, then expert ascending; each costs the GPU
+ * reference's rule, engine/kernels/nv2/nv2_host.cpp:1017-1030). The GPU's time starts at gpu_base_us + gpu_hit_us per
+ * resident expert, or at 0 when no expert of the call is resident; the CPU lane's starts at cpu_base_us when the lane
+ * is eligible (cpu_on, a CPU lane set up, the call's picks and rows travel with the request) and some expert is not
+ * resident, else at 0. The experts not resident are taken by picks descending, then expert ascending (the reference
+ * breaks equal pick counts by its cache's recency score first, which this table does not keep); each costs the GPU
  * gpu_admit_us (gpu_home_us when home_single is set, the call has several tokens and only one picked the expert: run
  * from the home rather than take a slot for one read) and the CPU lane cpu_expert_us + cpu_token_us per pick beyond the
- * first, plus cpu_base_us for the lane's first expert of the call; it goes to the CPU lane when cpu_on, fewer than
- * max_cpu are there already, the call's picks and rows travel with the request and the later of the two finish times
- * is then no later than with the GPU taking it; else to the GPU (BMX_LANE_HOME or BMX_LANE_ADMIT). Default (no policy
- * set): cpu_on 0, home_single 0, every miss BMX_LANE_ADMIT. */
+ * first; it goes to the CPU lane when the lane is eligible, fewer than max_cpu are there already and the later of the
+ * two finish times is then no later than with the GPU taking it, max(c + cost_cpu, g) <= max(c, g + cost_gpu); else to
+ * the GPU (BMX_LANE_HOME or BMX_LANE_ADMIT). Default (no policy set): cpu_on 0, home_single 0, every miss
+ * BMX_LANE_ADMIT. */
 typedef struct bmx_plan_policy {
     int32_t cpu_on, max_cpu, home_single;
     int32_t cpu_fast;          /* 1: the agent's CPU jobs use bmx_cpu_expert_rows_fast; 0: the exact lane */
@@ -422,7 +427,9 @@ int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t*
 int bmx_host_device_ptr(void* host, uint64_t* device_addr);
 
 /* Combine: out[t] = sum over k ascending of w[t, k] * y_rows[inv[t, k]] (picks with inv < 0 or w = 0 skipped), then
- * + y_rows[offsets[E] + t] when has_shared (x16_red_k order, engine/kernels/x16/x16_dev.cu:354-384). */
+ * + y_rows[offsets[E] + t] when has_shared (x16_red_k order, engine/kernels/x16/x16_dev.cu:354-384). The shared row is
+ * added with weight 1: a layer with a gated shared expert (bmx_moe_desc.shared_gate, weight sigmoid(x . g)) is combined
+ * by the layer calls (bmx_moe_forward, bmx_moe_layer, BMX_STAGE_COMBINE of bmx_moe_stage), not by this entry. */
 int bmx_combine(const float* y_rows, const int32_t* inv, const void* w_fp16, const int32_t* offsets, int T, int topk,
                 int H, int E, int has_shared, float* out, bmx_stream_t stream);
 

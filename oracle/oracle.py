@@ -282,20 +282,23 @@ PLAN_DEFAULT = dict(cpu_on=0, max_cpu=0, home_single=0, gpu_base_us=0.0, gpu_hit
 
 def plan_lanes(ex, res, cnt, ntok, npicks, rows, policy=None, cpu_ready=True):
     """The planner's lanes for a request (include/bmx.h bmx_plan_policy; the reference's two-lane rule,
-    engine/kernels/nv2/nv2_host.cpp:1030-1041): residents LANE_VRAM; the rest by picks descending then expert
-    ascending, each to the CPU lane when that keeps the later of the two estimated finish times no later than the GPU
-    taking it (and the lane is on, not full, and the call's picks and rows came with the request), else to the GPU
-    (LANE_HOME for a single-pick expert of a multi-token call under home_single, else LANE_ADMIT). rows: the request
-    carried the call's input rows."""
+    engine/kernels/nv2/nv2_host.cpp:1017-1030): residents LANE_VRAM; the GPU's estimated time starts at its base plus
+    the hits (0 when nothing is resident), the CPU lane's at its base when it is eligible (on, set up, the call's picks
+    and rows came with the request) and some expert misses; the misses by picks descending then expert ascending, each
+    to the CPU lane when that keeps the later of the two finish times no later than the GPU taking it (and the lane is
+    not full), else to the GPU (LANE_HOME for a single-pick expert of a multi-token call under home_single, else
+    LANE_ADMIT). rows: the request carried the call's input rows."""
     p = dict(PLAN_DEFAULT, **(policy or {}))
     lanes = np.full(len(ex), LANE_VRAM, np.int32)
     cpu_ok = bool(p["cpu_on"]) and cpu_ready and rows and npicks <= PLAN_MAXP and ntok <= PLAN_MAXT
-    g = p["gpu_base_us"] + p["gpu_hit_us"] * int(np.sum(res != 0))
-    c, ncpu = 0.0, 0
-    for u in sorted((u for u in range(len(ex)) if not res[u]), key=lambda u: (-int(cnt[u]), int(ex[u]))):
+    nres = int(np.sum(res != 0))
+    misses = sorted((u for u in range(len(ex)) if not res[u]), key=lambda u: (-int(cnt[u]), int(ex[u])))
+    g = p["gpu_base_us"] + p["gpu_hit_us"] * nres if nres else 0.0
+    c, ncpu = (p["cpu_base_us"] if cpu_ok and misses else 0.0), 0
+    for u in misses:
         home = bool(p["home_single"]) and ntok > 1 and cnt[u] == 1
         gc = p["gpu_home_us"] if home else p["gpu_admit_us"]
-        cc = (p["cpu_base_us"] if ncpu == 0 else 0.0) + p["cpu_expert_us"] + p["cpu_token_us"] * (int(cnt[u]) - 1)
+        cc = p["cpu_expert_us"] + p["cpu_token_us"] * (int(cnt[u]) - 1)
         if cpu_ok and ncpu < p["max_cpu"] and max(c + cc, g) <= max(c, g + gc):
             lanes[u] = LANE_CPU
             c += cc

@@ -255,13 +255,38 @@ def test_layer_parity(cuda, oracle, monkeypatch, name, cfgname, T, rows, kw):
     rows = list(range(T)) if rows is None else rows
     say("layer", name, "oracle rows", rows)
     want = oracle_layer(oracle, tab, x.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy(), rows)
-    got = out[rows]
-    err_abs, err_rel = float(np.abs(got - want).max()), rel_rms(got, want)
-    say("layer", name, "max_abs", err_abs, "rel_rms", err_rel, "|out| rms", float(np.sqrt(np.mean(want ** 2))))
-    assert err_abs < MAX_ABS and err_rel < REL_RMS
+    # both the separate calls and the one-call layer (the path a one-token caller runs) against the oracle directly
+    for what, res in (("separate calls", out), ("one call", fused)):
+        got = res[rows]
+        err_abs, err_rel = float(np.abs(got - want).max()), rel_rms(got, want)
+        say("layer", name, what, "max_abs", err_abs, "rel_rms", err_rel, "|out| rms",
+            float(np.sqrt(np.mean(want ** 2))))
+        assert err_abs < MAX_ABS and err_rel < REL_RMS, what
     # deterministic: same bits on a second call
     out2 = layer.run_bszN(x, sel, w).cpu().numpy()
     assert np.array_equal(out, out2)
+
+
+@pytest.mark.parametrize("cus", [16, 40, 80])
+def test_one_token_layer_on_fewer_compute_units(cuda, oracle, monkeypatch, cus):
+    """The one-token layer call takes its gate / up k-split count from the device's compute units: with the count
+    overridden (another device or partition mode) the split count and the summation order change, and the output stays
+    within the layer tolerance of the oracle."""
+    import bmx
+    from bmx import synth
+    c = synth.CONFIGS["c2"]
+    tab = synth.table("c2", seed=1, device=cuda)
+    x, lg, bias = synth.inputs("c2", T=1, seed=2, device=cuda)
+    layer = bmx.MoELayer(tab, c["topk"], score=c["score"], bias=bias, n_group=c["n_group"], topk_group=c["topk_group"],
+                         renorm=c["renorm"], scale=c["scale"])
+    monkeypatch.setenv("BMX_CU_COUNT", str(cus))
+    say("one-token layer, compute units", cus)
+    got = layer.forward(x, lg).cpu().numpy()
+    monkeypatch.delenv("BMX_CU_COUNT")
+    want = oracle_layer(oracle, tab, x.cpu().numpy(), layer.sel.cpu().numpy(), layer.w.cpu().numpy(), [0])
+    err_abs, err_rel = float(np.abs(got - want).max()), rel_rms(got, want)
+    say("one-token layer, compute units", cus, "max_abs", err_abs, "rel_rms", err_rel)
+    assert err_abs < MAX_ABS and err_rel < REL_RMS
 
 
 STAGED = [("c1 T1", "c1", 1, True), ("c2 T1", "c2", 1, False), ("c2 T1 projected", "c2", 1, True),

@@ -38,7 +38,9 @@ def check_logits(got, z, W, oracle):
     return float((got != exact.astype(np.float16)).mean())
 
 
-@pytest.mark.parametrize("T,E,H", [(1, 288, 4096), (5, 64, 2048), (33, 384, 4096), (513, 1000, 1024), (7, 256, 5120)])
+@pytest.mark.parametrize("T,E,H", [(1, 288, 4096), (5, 64, 2048), (33, 384, 4096), (513, 1000, 1024), (7, 256, 5120),
+                                   # H = 64 mod 128: the projection's half-block tail
+                                   (3, 64, 576), (40, 288, 2112), (1, 96, 64)])
 def test_router_logits_projection(cuda, oracle, T, E, H):
     import bmx
     rng = np.random.default_rng(T * 7 + E)

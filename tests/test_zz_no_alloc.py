@@ -82,3 +82,27 @@ def test_scratch_layer_refuses_oversized_calls(cuda):
                                    P(dummy), P(dummy), P(dummy), bmx.PATH_PREFILL, s)
     assert rc == bmx._lib.BMX_ERR_WORKSPACE
     assert "scratch array" in lib.bmx_last_error().decode()
+
+
+@pytest.mark.parametrize("cfg,E", [("c2", 288), ("c1", 64)])
+def test_scratch_layer_against_oracle(cuda, oracle, cfg, E):
+    """One one-token scratch call (the full C2 / C1 layer) against the oracle directly: 1e-2 max-abs, 1e-3 relative
+    RMS, with the picks and weights the call wrote."""
+    from bmx import synth
+    layer = make_layer(cfg, E, cuda)
+    x, lg, _ = synth.inputs(cfg, T=1, seed=40, device=cuda)
+    lg = lg[:, :E].contiguous()
+    say("scratch layer vs oracle", cfg, "E", E)
+    sel, w, out = layer_call(layer, x, lg, 0, scratch=True)
+    tab = layer.table
+    s, wn = sel.cpu().numpy(), w.cpu().numpy()
+    exps = [None] * tab.E
+    for e in sorted(set(int(v) for v in s.ravel() if 0 <= v < tab.E)):
+        exps[e] = tab.host_expert(e)
+    shared = tab.host_expert(tab.E) if tab.has_shared else None
+    want = oracle.moe_forward(exps, 0, shared, tab.H, tab.I, x.cpu().numpy(), s, wn, rows=np.arange(1, dtype=np.int32))
+    got = out.cpu().numpy()
+    err = float(np.abs(got - want).max())
+    rel = float(np.sqrt(np.mean((got.astype(np.float64) - want) ** 2)) / np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    say("scratch layer vs oracle", cfg, "max_abs", err, "rel_rms", rel)
+    assert err < 1e-2 and rel < 1e-3
