@@ -115,6 +115,7 @@ SIGNATURES = {
     "bmx_cpu_lane_add": (_I, [_P, _I64, _P, _I, _P]),
     "bmx_copy_agent_plan_stats": (_I, [_P, _P]),
     "bmx_slot_stage_async": (_I, [_P, _P, _P, _I, _P]),
+    "bmx_slot_stage_rows": (_I, [ctypes.POINTER(SlotTable), _I, _P, _I, ctypes.c_uint64, _I, _P]),
     "bmx_host_device_ptr": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
 }
 

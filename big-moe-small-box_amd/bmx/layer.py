@@ -77,7 +77,13 @@ class MoELayer:
         step: returns the selection the GPU computes (CPU-lane picks masked) and whether a CPU job may add to this call
         (combine() adds it), as the reference's Nv2.layer (engine/nv2.py:374-437)."""
         self._cpu_seq = None
+        self._staged = None
         if self.slots is None:
+            return sel, w, False
+        if self.slots.stage_prefill(li, sel, first=self.routing_first):
+            # a prefill-size call (the reference's staged call, engine/nv2.py:378-386): hits marked, nothing admitted,
+            # the layer's table points at the staging arena until its products are done
+            self._staged = li
             return sel, w, False
         if getattr(self.slots, "planned", False):
             sel_gpu, w_gpu, _, seq = self.slots.step_planned(li, sel, w, z, True, first=self.routing_first,
@@ -99,6 +105,15 @@ class MoELayer:
         rw = rw.view(x.shape[0], -1)
         if rw.dtype != torch.float16 or not rw.is_contiguous():
             rw = rw.half().contiguous()
+        staged, self._staged = getattr(self, "_staged", None), None
+        if self.slots is not None and staged is not None:
+            # every expert's table entry points at a slot or at the staging arena: the plain layer, then the restore
+            need = L.lib().bmx_moe_workspace(self.slot_desc, x.shape[0], path)
+            if self._ws is None or self._ws.numel() < need:
+                self._ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+            self.out_bszn = ops.moe_forward(self.slot_desc, x, sel, rw, path, self._ws)
+            self.slots.stage_restore(staged)
+            return self.out_bszn
         if self.slots is not None:
             self.out_bszn = self._run_slots(x, sel, rw, path)
             return self.out_bszn

@@ -66,6 +66,18 @@ class ExpertSlots:
         self.seq = [0] * self.L               # dma: sequence number of each layer's last step
         self.planned = False                  # dma: layer calls use planned steps (plan())
         self.cpu_ready = False                # dma: the agent has a CPU lane (cpu_lane())
+        self.last_seq = 0                     # dma: the last sequence number the agent was given
+        # staged prefill (stage_prefill): calls of at least stage_min picks admit nothing; each layer's experts that are
+        # not resident are copied into one of two staging arenas one layer ahead on a copy stream
+        self.stage_min = 8192                 # picks (the reference's EC_STAGE_MIN default, engine/tiers.py:673)
+        self.cstream = None
+        self.st_buf = [None, None]            # staging arenas, uint8 [n * rec] each
+        self.st_ready = [None, None]          # event: the arena's last staging copies done
+        self.st_open = False
+        self.st_last = None                   # layer of the last staged call of the open forward
+        self.st_layers = {}                   # li -> (experts np.int32, experts on the device, copy runs)
+        self.st_sub = set()                   # layers whose copies are enqueued in this forward
+        self.st_stats = dict(forwards=0, layers=0, experts=0, bytes=0)
         if copies == "dma":
             homes = (ctypes.c_uint64 * (self.L * self.E))(*[t.addr[e][0] for t in layers for e in range(t.E)])
             nb = (ctypes.c_int64 * (self.L * self.E * 3))(*[t.mat_bytes(e, m) for t in layers for e in range(t.E)
@@ -123,6 +135,7 @@ class ExpertSlots:
                                                 ctypes.c_void_p(sel.data_ptr()), sel.numel(), int(first), int(admit),
                                                 ctypes.byref(q), ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_step_agent")
             self.seq[li] = q.value
+            self.last_seq = max(self.last_seq, q.value)
             return None
         if self.last_copied is not None:       # the previous step's copies read the job buffer this step rewrites
             cur.wait_event(self.last_copied)
@@ -161,6 +174,7 @@ class ExpertSlots:
                                                     ctypes.c_void_p(guess.data_ptr()), n, int(first), lim,
                                                     ctypes.byref(q), ctypes.c_void_p(cur.cuda_stream)),
                     "bmx_slot_prefetch_agent")
+            self.last_seq = max(self.last_seq, q.value)
             return None
         b = self.pf_calls & 1
         self.pf_calls += 1
@@ -289,6 +303,7 @@ class ExpertSlots:
                                               ctypes.byref(q), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
                 "bmx_slot_step_planned")
         self.seq[li] = q.value
+        self.last_seq = max(self.last_seq, q.value)
         return sel_gpu, w_gpu, lanes, q.value
 
     def cpu_add(self, seq, out):
@@ -316,6 +331,129 @@ class ExpertSlots:
         c = (ctypes.c_size_t * n)(*nbytes)
         s = stream or torch.cuda.current_stream()
         L.check(L.lib().bmx_slot_stage_async(a, b, c, n, ctypes.c_void_p(s.cuda_stream)), "bmx_slot_stage_async")
+
+    # ---- staged prefill ----
+    def stage_prefill(self, li, sel, *, first=None):
+        """The slot table's part of a prefill-size layer call (engine/nv2.py:378-386 with the staging hook of
+        engine/tiers.py:406-463): returns False (and ends an open staged forward) when sel holds fewer than stage_min
+        picks. Otherwise marks the hits only (a step that admits nothing, the reference's _ec_hits), and makes layer
+        li's table point at a staging arena that holds every expert of the layer not resident in a slot: the copies
+        home -> arena (li % 2) run on a copy stream, enqueued one layer ahead (layer li + 1's go into the other arena
+        while layer li computes), and the current stream waits for layer li's. Residency is snapshotted when a forward
+        starts (its first staged call, or a call to a layer at or before the last one; this synchronises), and stays as
+        it is because staged calls admit nothing. After the layer's expert products, stage_restore(li) points the
+        entries back. The shared expert is not in the slot table and is read where it lives."""
+        if sel.numel() < self.stage_min:
+            if self.st_open:
+                self.stage_end()
+            return False
+        if not self.st_open or self.st_last is None or li <= self.st_last or li not in self.st_layers:
+            self._stage_begin(li)
+        self.step(li, sel.reshape(-1), admit=False, first=first)
+        cur = torch.cuda.current_stream()
+        if li not in self.st_sub:
+            self._stage_submit(li)
+        b = li % 2
+        cur.wait_event(self.st_ready[b])
+        ex, idx, runs = self.st_layers[li]
+        if len(ex):
+            L.check(L.lib().bmx_slot_stage_rows(ctypes.byref(self.struct), li, ctypes.c_void_p(idx.data_ptr()),
+                                                len(ex), self.st_buf[b].data_ptr(), 0, ctypes.c_void_p(cur.cuda_stream)),
+                    "bmx_slot_stage_rows")
+        if li + 1 in self.st_layers and li + 1 not in self.st_sub:
+            self._stage_submit(li + 1)            # the next layer into the other arena, behind this layer's products
+        self.st_last = li
+        self.st_stats["layers"] += 1
+        self.st_stats["experts"] += len(ex)
+        return True
+
+    def stage_restore(self, li):
+        """After a staged call's expert products (stream order): layer li's staged entries back at their homes."""
+        if li not in self.st_layers:
+            return
+        ex, idx, _ = self.st_layers[li]
+        if len(ex):
+            L.check(L.lib().bmx_slot_stage_rows(ctypes.byref(self.struct), li, ctypes.c_void_p(idx.data_ptr()),
+                                                len(ex), 0, 1, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                    "bmx_slot_stage_rows")
+
+    def stage_end(self):
+        """Close a staged forward (the next prefill-size call snapshots residency again). The arenas are kept."""
+        self.st_open, self.st_last, self.st_sub = False, None, set()
+
+    def stage_release(self):
+        """Close a staged forward and free the staging arenas."""
+        self.stage_end()
+        self.st_buf, self.st_ready = [None, None], [None, None]
+
+    def _stage_begin(self, li0):
+        """A staged forward from layer li0: wait for every copy in flight, snapshot residency, plan each later layer's
+        copies (home -> staging record j of its j-th non-resident expert; the matrices a record holds, merged into one
+        copy where they are adjacent at both ends), size the arenas."""
+        import numpy as np
+        self.stage_end()
+        cur = torch.cuda.current_stream()
+        if self.agent is not None:
+            self.check()
+            if self.last_seq:
+                L.check(L.lib().bmx_copy_wait(self.agent, int(self.last_seq), 1, ctypes.c_void_p(cur.cuda_stream)),
+                        "bmx_copy_wait")
+        else:
+            for ev in [self.last_copied] + list(self.pf_copied):
+                if ev is not None:
+                    cur.wait_event(ev)
+        snap = self.slotof.view(self.L, self.E).cpu().numpy()       # synchronises
+        dev = self.arena.device
+        self.st_layers, nmax = {}, 0
+        for lj in range(li0, self.L):
+            t = self.layers[lj]
+            ex = np.flatnonzero(snap[lj] < 0).astype(np.int32)
+            base, offs, runs = t.arena.data_ptr(), (0, t.off_u, t.off_d), []
+            for j, e in enumerate(ex.tolist()):
+                for m in range(3):
+                    src, dst, nb = base + e * t.rec + offs[m], j * t.rec + offs[m], t.mat_bytes(e, m)
+                    if runs:
+                        s0, d0, n0 = runs[-1]
+                        gap = src - (s0 + n0)
+                        if gap == dst - (d0 + n0) and 0 <= gap <= 4096:
+                            runs[-1] = (s0, d0, src + nb - s0)
+                            continue
+                    runs.append((src, dst, nb))
+            self.st_layers[lj] = (ex, torch.from_numpy(ex).to(dev), runs)
+            nmax = max(nmax, len(ex))
+        need = nmax * self.layers[0].rec
+        if self.cstream is None:
+            self.cstream = torch.cuda.Stream(device=dev)
+        for b in range(2):
+            if self.st_buf[b] is None or self.st_buf[b].numel() < need:
+                self.st_buf[b] = None
+                buf = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+                buf.record_stream(self.cstream)
+                self.st_buf[b] = buf
+        self.st_open = True
+        self.st_stats["forwards"] += 1
+
+    def _stage_submit(self, lj):
+        """Enqueue layer lj's staging copies into arena lj % 2 on the copy stream, behind everything the current stream
+        has enqueued so far (the products of the layer that last read that arena, and its restore)."""
+        b = lj % 2
+        _, _, runs = self.st_layers[lj]
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream())
+        self.cstream.wait_event(ev)
+        if runs:
+            base = self.st_buf[b].data_ptr()
+            n = len(runs)
+            src = (ctypes.c_void_p * n)(*[r[0] for r in runs])
+            dst = (ctypes.c_void_p * n)(*[base + r[1] for r in runs])
+            nb = (ctypes.c_size_t * n)(*[r[2] for r in runs])
+            L.check(L.lib().bmx_slot_stage_async(src, dst, nb, n, ctypes.c_void_p(self.cstream.cuda_stream)),
+                    "bmx_slot_stage_async")
+            self.st_stats["bytes"] += sum(r[2] for r in runs)
+        ready = torch.cuda.Event()
+        ready.record(self.cstream)
+        self.st_ready[b] = ready
+        self.st_sub.add(lj)
 
     def stats(self):
         """(hits, misses, admissions, steps without a victim, evictions, prefetch admissions, prefetched experts used,

@@ -451,6 +451,46 @@ __global__ __launch_bounds__(256) void k_slot_copy(bmx_slot_table t, int li, int
     }
 }
 
+// Staged prefill: layer li's table entries of experts ex[j] (local ids, j < n) point at staging record j (base + j rec,
+// the slot geometry) when restore = 0; with restore = 1 each points back at where the expert lives now: its slot if
+// it is resident, else its home.
+__global__ __launch_bounds__(256) void k_stage_rows(bmx_slot_table t, int li, const int32_t* __restrict__ ex, int n,
+                                                    uint64_t base, int restore)
+{
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const int e = ex[j];
+    if (e < 0 || e >= t.E) return;
+    bmx_expert* tab = reinterpret_cast<bmx_expert*>(t.tables[li]);
+    uint64_t a0, a1, a2;
+    if (!restore)
+    {
+        a0 = base + (uint64_t)j * (uint64_t)t.rec;
+        a1 = a0 + (uint64_t)t.off_u;
+        a2 = a0 + (uint64_t)t.off_d;
+    }
+    else
+    {
+        const int s = t.slotof[(size_t)li * t.E + e];
+        if (s >= 0)
+        {
+            a0 = t.slot_base[s];
+            a1 = a0 + (uint64_t)t.off_u;
+            a2 = a0 + (uint64_t)t.off_d;
+        }
+        else
+        {
+            const uint64_t* h = t.home + ((size_t)li * t.E + e) * 3;
+            a0 = h[0];
+            a1 = h[1];
+            a2 = h[2];
+        }
+    }
+    tab[e].tr[0] = a0;
+    tab[e].tr[1] = a1;
+    tab[e].tr[2] = a2;
+}
+
 static int check_table(const bmx_slot_table* t, const char* who)
 {
     if (!t) return set_error(BMX_ERR_ARG, "%s: null table", who);
@@ -593,6 +633,21 @@ int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t*
         if (e != hipSuccess) return set_error(BMX_ERR_HIP, "bmx_slot_stage_async: copy %d: %s", i, hipGetErrorString(e));
     }
     return BMX_OK;
+}
+
+int bmx_slot_stage_rows(const bmx_slot_table* t, int li, const int32_t* experts, int n, uint64_t base, int restore,
+                        bmx_stream_t stream)
+{
+    int rc = check_table(t, "bmx_slot_stage_rows");
+    if (rc) return rc;
+    if (li < 0 || li >= t->L || n < 0 || n > t->E || (n && !experts))
+        return set_error(BMX_ERR_ARG, "bmx_slot_stage_rows: bad layer %d or expert count %d (<= E = %d)", li, n, t->E);
+    if (!restore && n && (!base || base % 256))
+        return set_error(BMX_ERR_ARG, "bmx_slot_stage_rows: staging base must be a 256-byte aligned address");
+    if (!n) return BMX_OK;
+    hipLaunchKernelGGL(k_stage_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       *t, li, experts, n, base, restore ? 1 : 0);
+    return check_launch("bmx_slot_stage_rows");
 }
 
 int bmx_host_device_ptr(void* host, uint64_t* device_addr)

@@ -423,6 +423,13 @@ int bmx_cpu_lane_add(bmx_copy_agent* agent, int64_t seq, float* out, int T, bmx_
 /* Host-planned staging: n copies src[i] -> dst[i] of bytes[i] (hipMemcpyAsync, e.g. pinned host -> slot), in order on
  * stream (the reference's stage_layer, engine/kernels/nv2/nv2_host.cpp:1558-1593). */
 int bmx_slot_stage_async(const void* const* src, void* const* dst, const size_t* bytes, int n, bmx_stream_t stream);
+/* Staged prefill (prefill-size calls admit nothing: engine/tiers.py:395-463): restore = 0 points layer li's table entries
+ * of experts[j] (device int32, local ids, j < n <= E) at staging record j, base + j * rec with the slot geometry (the
+ * reference's index_copy_ of the staging addresses into the layer's pointer rows, engine/tiers.py:441-451); restore = 1
+ * points each back at where the expert lives now, its slot if resident, else its home (nv_restore_k,
+ * engine/kernels/nv2/nv2_dev.cu:554-566). base: device address, 256-byte aligned. Stream-ordered, one small kernel. */
+int bmx_slot_stage_rows(const bmx_slot_table* t, int li, const int32_t* experts, int n, uint64_t base, int restore,
+                        bmx_stream_t stream);
 /* Device-visible address of pinned host memory (hipHostGetDevicePointer), for bmx_slot_table.home. */
 int bmx_host_device_ptr(void* host, uint64_t* device_addr);
 
