@@ -320,13 +320,20 @@ def bench_c4(args):
     tstruct = ctypes.byref(slots.struct)
     seq, pseq, seqs = ctypes.c_int64(), ctypes.c_int64(), [0] * NL
 
-    def token(tok):
+    # timeline phases of a layer call (the reference's per-layer split, engine/nv2.py:836-901): an event before each
+    PHASES = ("route", "step", "dispatch", "moe_resident", "copy_wait_gate_up", "moe_staged", "copy_wait_down",
+              "down_combine", "cpu_add")
+
+    def token(tok, evs=None):
         s = torch.cuda.current_stream()
         sp = ctypes.c_void_p(s.cuda_stream)
+        mark = (lambda li, k: evs[li][k].record(sp)) if evs is not None else (lambda li, k: None)
         for li in range(NL):
+            mark(li, 0)
             lgp = ctypes.c_void_p(lg_all.data_ptr() + (li * NTOK + tok) * E * 2)
             bmx._lib.check(L.bmx_router_topk(lgp, P(biases[li]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0, P(sel),
                                              P(w), sp), "router")
+            mark(li, 1)
             if CPUL:
                 bmx._lib.check(L.bmx_slot_step_planned(tstruct, slots.agent, li, P(sel), P(w), 1, topk, 0, 1, P(x),
                                                        P(sel_g), P(w_g), None, ctypes.byref(seq), sp), "planned step")
@@ -365,12 +372,16 @@ def bench_c4(args):
                 ev.record(side)
                 pf_copied[b] = ev
             gs, gw_ = (sel_g, w_g) if CPUL else (sel, w)
+            mark(li, 2)
             bmx._lib.check(L.bmx_dispatch(P(gs), 1, topk, E, 0, 1, rpg, ctypes.byref(routes.struct), P(dws), dws_n, sp),
                            "dispatch")
             d = ctypes.byref(descs[li])
             o = ctypes.c_void_p(out.data_ptr() + li * H * 4)
-            for st in (bmx._lib.STAGE_GATE_UP_RESIDENT, "gu", bmx._lib.STAGE_GATE_UP_STAGED, bmx._lib.STAGE_ACT, "dn",
-                       bmx._lib.STAGE_DOWN, bmx._lib.STAGE_COMBINE):
+            for k, st in enumerate((bmx._lib.STAGE_GATE_UP_RESIDENT, "gu", bmx._lib.STAGE_GATE_UP_STAGED,
+                                    bmx._lib.STAGE_ACT, "dn", bmx._lib.STAGE_DOWN, bmx._lib.STAGE_COMBINE)):
+                ph = (3, 4, 5, None, 6, 7, None)[k]
+                if ph is not None:
+                    mark(li, ph)
                 if isinstance(st, str):
                     if DMA:
                         bmx._lib.check(L.bmx_copy_wait_layer(slots.agent, li, 0 if st == "gu" else 1, sp), "copy wait")
@@ -379,9 +390,13 @@ def bench_c4(args):
                     continue
                 bmx._lib.check(L.bmx_moe_stage(d, st, P(x), 1, ctypes.byref(routes.struct), None, None, P(gw_), o,
                                                P(ws), ws_n, 1, sp), "stage")
+            mark(li, 8)
             if CPUL:
                 bmx._lib.check(L.bmx_cpu_lane_add(slots.agent, seqs[li], o, 1, sp), "cpu lane add")
+            mark(li, 9)
 
+    steps, warmup = (args.steps, args.warmup) if args.config == "c4" else (args.c4_steps, min(args.warmup, 5))
+    args = argparse.Namespace(**dict(vars(args), steps=steps, warmup=warmup))
     for i in range(args.warmup):
         token(i % NTOK)
     torch.cuda.synchronize()
@@ -397,9 +412,41 @@ def bench_c4(args):
     d = [b - a for a, b in zip(st0, st1)]
     exp_bytes = layers[0].expert_bytes(0)
     staged = (d[2] + d[5]) * exp_bytes
+    # timeline: the same token loop once more with a timing event before each phase of every layer call (kept out of
+    # the timed loop above, whose figure has no events in it)
+    nt = max(1, args.timeline_steps)
+    evs = [[[TimingEvent() for _ in range(len(PHASES) + 1)] for _ in range(NL)] for _ in range(nt)]
+    for i in range(nt):
+        token((args.warmup + args.steps + i) % NTOK, evs[i])
+    torch.cuda.synchronize()
+    parts = {ph: statistics.mean(evs[i][li][k].elapsed_time(evs[i][li][k + 1]) * 1e3 for i in range(nt)
+                                 for li in range(NL)) for k, ph in enumerate(PHASES)}
+    layer_us = [evs[i][li][0].elapsed_time(evs[i][li][-1]) * 1e3 for i in range(nt) for li in range(NL)]
+    timeline = {"n": nt * NL, "tokens": nt, "us_layer_mean": round(sum(parts.values()), 1),
+                "parts_us_mean": {k: round(v, 2) for k, v in parts.items()},
+                "copy_wait_us_mean": round(parts["copy_wait_gate_up"] + parts["copy_wait_down"], 2),
+                "compute_us_mean": round(sum(v for k, v in parts.items() if not k.startswith("copy_wait")), 2),
+                "us_layer_p50": round(statistics.median(layer_us), 1) if layer_us else None,
+                "timing": "timing-only events (no system-scope release) on the compute stream before each phase of every "
+                          "layer call, in a separate loop of the same tokens; copy_wait_* is the time the stream spends "
+                          "in the one-lane kernel waiting for the copies of the layer's admissions (the part of the copy "
+                          "no compute hides)"}
+    log(f"bench c4: timeline {timeline['parts_us_mean']}")
+    h2d = measure_h2d()
+    link = staged / (ms * 1e-3 * args.steps) / 1e9
+    roofline = {"kernel": "home -> slot copies of the misses (copy agent, SDMA engines)" if DMA else
+                          "home -> slot copies of the misses (copy kernel on a side stream)",
+                "bound": "pcie", "achieved": round(link, 2), "peak": round(h2d, 2), "unit": "GB/s",
+                "frac": round(link / h2d, 4), "traffic": round(staged / args.steps),
+                "peak_source": "one 1 GiB pinned host -> device hipMemcpyAsync timed in this run (PCIe Gen5 x16: 64 GB/s "
+                               "per direction published)",
+                "floor_us_per_token": round(staged / args.steps / (h2d * 1e9) * 1e6, 1),
+                "achieved_source": "misses' expert bytes per token (admissions + prefetches x 7,077,888 B) over the timed "
+                                   "loop's time per token"}
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(layers[0], sel.repeat(4, 1), w.repeat(4, 1))
+        cpu = cpu_baseline(layers[0], sel.repeat(4, 1), w.repeat(4, 1),
+                           budget_s=args.cpu_budget if args.config == "c4" else min(4.0, args.cpu_budget))
         if cpu:
             per_layer = cpu["us_per_layer"] / 4
             cpu = {"value": round(1e6 / (per_layer * NL), 3), "unit": "tokens/s", "cores": cpu["cores"], "kind": "reference",
@@ -437,13 +484,117 @@ def bench_c4(args):
         "hit_rate": round(d[0] / max(1, d[0] + d[1]), 4),
         "staged_bytes_per_token": staged / args.steps,
         "staged_gbps": round(staged / (ms * 1e-3 * args.steps) / 1e9, 2),
-        "roofline": None,
+        "timeline": timeline,
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     if DMA:
         log(f"bench c4: copy agent {slots.agent_status()}")
         slots.close()
+    return res
+
+
+def measure_h2d(nbytes=1 << 30, reps=3):
+    """Pinned host -> device copy rate (GB/s, best of reps) of one nbytes hipMemcpyAsync on a side stream."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    side = torch.cuda.Stream()
+    best = 0.0
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(side):
+            a.record()
+            dst.copy_(src, non_blocking=True)
+            b.record()
+        b.synchronize()
+        best = max(best, nbytes / (a.elapsed_time(b) * 1e-3) / 1e9)
+    del src, dst
+    return best
+
+
+def bench_staged(args, cpu=None):
+    """Staged prefill of the DeepSeek-shaped layer with its experts at home in pinned host memory: NL layers (their homes
+    in NH distinct arenas, layer li reading the bytes of arena li % NH), a VRAM slot table of 30 % of the experts warmed
+    with each layer's most popular ones, Zipf(1.1) routing with a per-layer permutation, 8192-token chunks. A step is one
+    chunk through the NL layers: per layer the router, the hits-only slot step with the staging of every non-resident
+    expert one layer ahead (ExpertSlots.stage_prefill: copies into two staging arenas on a copy stream), the layer's
+    products and combine, the table restore. Bound: the PCIe link (the non-resident experts' bytes cross it once)."""
+    import numpy as np
+    import torch
+    import bmx
+    from bmx import synth
+    dev = torch.device("cuda:0")
+    c = synth.CONFIGS["c3"]
+    NL, NH, E, H, I, topk, T = args.staged_layers, min(4, args.staged_layers), c["E"], c["H"], c["I"], c["topk"], c["T"]
+    S = int(round(0.30 * NL * E))
+    log(f"bench prefill_staged: {NL} layers x {E} experts (homes: {NH} pinned arenas), {S} VRAM slots, {T} tokens")
+    fm = synth.formats("c3", E, False)
+    layers = []
+    for li in range(NL):
+        if li < NH:
+            t = bmx.ExpertTable.random(H, I, E, fm, seed=3000 + li, device=dev, home="host")
+        else:
+            h = layers[li % NH]
+            t = bmx.ExpertTable(H, I, h.arena, h.fmt, h.suh, h.svh, h.off_u, h.off_d, E, False)
+        layers.append(t)
+    slots = bmx.ExpertSlots(layers, S, maxj=16, copies="kernel")
+    kw = dict(score=c["score"], renorm=c["renorm"], scale=c["scale"], n_group=c["n_group"], topk_group=c["topk_group"])
+    mods = [bmx.MoELayer(layers[li], topk, slots=slots, li=li, **kw) for li in range(NL)]
+    per = S // NL
+    lgs = []
+    for li in range(NL):
+        perm = np.random.default_rng(7000 + li).permutation(E)
+        slots.warm(li, [int(e) for e in perm[:per]])
+        lgs.append(torch.from_numpy(synth.zipf_logits(T, E, 1.1, seed=7000 + li)).to(dev))
+    x = torch.from_numpy(np.random.default_rng(0).standard_normal((T, H)).astype(np.float16)).to(dev)
+    torch.cuda.synchronize()
+
+    def forward():
+        for li, m in enumerate(mods):
+            sel, w = m.routing_fn(T, None, x, {"logits": lgs[li]})
+            sel, w, _ = m.layer(li, sel, w, x, T)
+            m.run_bszN(x, sel, w)
+
+    steps, warmup = max(1, args.staged_steps), 1
+    for _ in range(warmup):
+        forward()
+    torch.cuda.synchronize()
+    st0 = dict(slots.st_stats)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        forward()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    st1 = dict(slots.st_stats)
+    staged_bytes = (st1["bytes"] - st0["bytes"]) / steps
+    staged_experts = (st1["experts"] - st0["experts"]) / steps
+    h2d = measure_h2d()
+    link = staged_bytes / (ms * 1e-3) / 1e9
+    us_layer = ms * 1e3 / NL
+    res = {
+        "workload": f"c3 staged prefill: {NL} layers of {E} routed experts top-{topk} group-limited (8 groups, top-4), "
+                    f"H {H}, I {I}, EXL3 2/3 mixed, {T} tokens per chunk; routed experts at home in pinned host memory "
+                    f"({NH} distinct arenas), a VRAM slot table of {S} slots (30 %) warmed with each layer's top {per} "
+                    f"experts; every non-resident expert staged into one of two arenas one layer ahead",
+        "T": T, "layers": NL, "steps": steps, "warmup": warmup, "path": "prefill (staged)",
+        "value": round(T * 1e3 / (ms / NL), 2), "unit": "tokens/s",
+        "us_per_layer": round(us_layer, 1), "ms_per_chunk": round(ms, 3),
+        "staged_experts_per_layer": round(staged_experts / NL, 1),
+        "staged_bytes_per_layer": round(staged_bytes / NL),
+        "roofline": {"kernel": "home -> staging arena copies (hipMemcpyAsync on a copy stream, one layer ahead)",
+                     "bound": "pcie", "achieved": round(link, 2), "peak": round(h2d, 2), "unit": "GB/s",
+                     "frac": round(link / h2d, 4), "traffic": round(staged_bytes / NL),
+                     "floor_us_per_layer": round(staged_bytes / NL / (h2d * 1e9) * 1e6, 1),
+                     "peak_source": "one 1 GiB pinned host -> device hipMemcpyAsync timed in this run (PCIe Gen5 x16: 64 "
+                                    "GB/s per direction published)",
+                     "achieved_source": "bytes staged per chunk over the chunk's time (layers computing while the next "
+                                        "layer's experts are copied)"},
+        "cpu_baseline": cpu,
+    }
+    log(f"bench prefill_staged: {us_layer:.0f} us per layer, {link:.1f} GB/s staged of {h2d:.1f} GB/s measured H2D")
+    slots.close()
+    return res
 
 
 # Legs of the default run: (config, tokens per step, input batches rotated over, distinct layer tables rotated over).
@@ -456,6 +607,8 @@ LEGS = {
     "decode_t8": ("c2", 8, 16, 1),
     "c1": ("c1", 1, 64, 32),
     "c5": ("c5", 16, 16, 1),
+    "prefill_staged": None,       # bench_staged: the c3 layer stack with its experts in pinned host memory
+    "c4": None,                   # bench_c4: the 43-layer decode stack with the expert-slot table
 }
 HEADLINE_LEGS = ("decode", "prefill")
 
@@ -484,7 +637,7 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
     torch.cuda.synchronize()
     L = bmx.lib()
     Pp = lambda t: ctypes.c_void_p(t.data_ptr())
-    pa = {"auto": 0, "decode": 1, "prefill": 2, "mid": 3}[args.path]
+    pa = {"auto": 0, "decode": 1, "prefill": 2, "mid": 3, "split": 4}[args.path]
     need = max(L.bmx_moe_layer_workspace(ctypes.byref(l.desc), T, pa) for l in layers)
     lws = torch.zeros(need, dtype=torch.uint8, device=dev)
     sel_b = torch.empty((T, topk), dtype=torch.int64, device=dev)
@@ -539,6 +692,7 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
     topk = layers[0].num_experts_per_tok
     path = L.bmx_resolve_path(T, topk, pa)
     prefill, mid = path == bmx._lib.PATH_PREFILL, path == bmx._lib.PATH_MID
+    split = path == bmx._lib.PATH_SPLIT
     rpg = L.bmx_rows_per_group(T, topk, pa)
     # a one-token decode call routes the token inside its gate / up GEMV (its route stage launches nothing)
     fused_route = T == 1 and path == bmx._lib.PATH_DECODE and rpg == 1 and os.environ.get("BMX_ROUTE_IN_GEMV") != "0"
@@ -549,7 +703,7 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         ws_.append(wp)
     routes = [bmx.ops.dispatch(sels[p], E, 0, tabs[0].has_shared, rpg) for p in range(P)]
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    stages = [("route", bmx._lib.STAGE_ROUTE)] + ([("prep", bmx._lib.STAGE_PREP)] if prefill or mid else []) + [
+    stages = [("route", bmx._lib.STAGE_ROUTE)] + ([("prep", bmx._lib.STAGE_PREP)] if prefill or mid or split else []) + [
         ("gate_up", bmx._lib.STAGE_GATE_UP), ("act", bmx._lib.STAGE_ACT), ("down", bmx._lib.STAGE_DOWN),
         ("combine", bmx._lib.STAGE_COMBINE)]
     nst = steps
@@ -626,8 +780,9 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
     cpu = None
     if with_cpu and not args.no_cpu:
         n_cpu = T if T <= 64 else 64
-        cpu = cpu_baseline(tabs[0], sels[0][:n_cpu], ws_[0][:n_cpu])
-    kind = "prefill" if prefill else "mid" if mid else "decode"
+        cpu = cpu_baseline(tabs[0], sels[0][:n_cpu], ws_[0][:n_cpu],
+                           budget_s=args.cpu_budget if leg in HEADLINE_LEGS else min(4.0, args.cpu_budget))
+    kind = "prefill" if prefill else "mid" if mid else "split" if split else "decode"
     traffic = traffic_src = prof_us = None
     tpath = os.path.join(REPO, "profiles", f"{kind}_{cfg}_t{T}.json")
     if os.path.exists(tpath):
@@ -655,6 +810,9 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
         kern = ("k_gemv_gu_route (BMX_STAGE_GATE_UP of the one-token layer call: routing + dispatch of the token, "
                 "then trellis decode + gate/up split-K GEMV)" if fused_route
+                else "k_gemv_part<gate/up> + k_mid_gemm<false> (BMX_STAGE_GATE_UP of the split path: the GEMV over the "
+                     "experts with few rows, then the MFMA kernel over those with many; the two launches timed as one "
+                     "stage)" if split
                 else "k_gemv_part<gate/up> (BMX_STAGE_GATE_UP: trellis decode + gate/up split-K GEMV)")
         roofline = {"kernel": kern,
                     "bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -709,7 +867,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=None, help="with --config: tokens per step")
     ap.add_argument("--config", default=None, help="one workload instead of the legs (c1, c2, c3, c5; c4: the stack)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--path", choices=["auto", "decode", "mid", "prefill"], default="auto",
+    ap.add_argument("--path", choices=["auto", "decode", "mid", "prefill", "split"], default="auto",
                     help="expert-products path (auto: the library's choice for the batch)")
     ap.add_argument("--prefetch", type=int, default=0, metavar="N",
                     help="c4: layer-ahead prefetch of up to N guessed experts of the next layer per layer (0: off)")
@@ -724,6 +882,12 @@ def main():
     ap.add_argument("--cpu-max", type=int, default=2, help="c4 --cpu-lane: most misses a layer call puts on the CPU")
     ap.add_argument("--cpu-expert-us", type=float, default=125.0,
                     help="c4 --cpu-lane: the planner's CPU cost of one expert until the lane's first job is timed")
+    ap.add_argument("--timeline-steps", type=int, default=10, help="c4: tokens of the per-layer timeline loop")
+    ap.add_argument("--c4-steps", type=int, default=30, help="timed tokens of the c4 leg in the default run")
+    ap.add_argument("--staged-layers", type=int, default=8, help="prefill_staged: layers of the stack")
+    ap.add_argument("--staged-steps", type=int, default=3, help="prefill_staged: timed chunks through the stack")
+    ap.add_argument("--cpu-budget", type=float, default=8.0,
+                    help="seconds of CPU-lane calls per thread setting (headline legs; the others take at most 4)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -732,7 +896,8 @@ def main():
               f"GPUs is not implemented)", file=sys.stderr)
         sys.exit(2)
     if args.config == "c4":
-        return bench_c4(args)
+        print(json.dumps(bench_c4(args)), flush=True)
+        return
     import torch
     if args.calib_copy:
         src = torch.empty(args.calib_copy << 18, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -752,10 +917,25 @@ def main():
         for name in args.legs.split(","):
             if name not in LEGS:
                 raise SystemExit(f"bench.py: unknown leg {name!r} (legs: {', '.join(LEGS)})")
-            legs.append((name,) + LEGS[name])
+            legs.append((name,) + (LEGS[name] or ()))
     results = []
-    for name, cfg, T, P, NT in legs:
-        results.append(bench_leg(name, cfg, T, P, NT, args, with_cpu=name in HEADLINE_LEGS or args.config is not None))
+    for leg in legs:
+        name = leg[0]
+        if name == "c4":
+            r = bench_c4(args)
+            r = dict(r, leg="c4", ms=r["ms_per_step"], T=1)
+        elif name == "prefill_staged":
+            pf = next((x for x in results if x["leg"] == "prefill"), None)
+            cpu = None
+            if pf is not None and pf.get("cpu_baseline"):
+                cpu = dict(pf["cpu_baseline"], sample="the prefill leg's sample (the same layer shape, experts in RAM): "
+                                                      + pf["cpu_baseline"]["sample"])
+            r = bench_staged(args, cpu)
+            r = dict(r, leg="prefill_staged", ms=r["ms_per_chunk"] / r["layers"])
+        else:
+            _, cfg, T, P, NT = leg
+            r = bench_leg(name, cfg, T, P, NT, args, with_cpu=True)
+        results.append(r)
         torch.cuda.empty_cache()
     head = results[0]
     res = {

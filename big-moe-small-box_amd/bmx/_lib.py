@@ -10,7 +10,7 @@ TF_K2, TF_K25, TF_K3, TF_K4 = 0, 1, 2, 3
 TILE_BYTES = {TF_K2: 64, TF_K25: 80, TF_K3: 96, TF_K4: 128}
 SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSP = 0, 1, 2
 ACT_SILU, ACT_GELU, ACT_RELU2, ACT_SILU_OAI = 0, 1, 2, 3
-PATH_AUTO, PATH_DECODE, PATH_PREFILL, PATH_MID = 0, 1, 2, 3
+PATH_AUTO, PATH_DECODE, PATH_PREFILL, PATH_MID, PATH_SPLIT = 0, 1, 2, 3, 4
 STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT, STAGE_PREP = 0, 1, 2, 3, 4, 5
 STAGE_GATE_UP_RESIDENT, STAGE_GATE_UP_STAGED = 6, 7
 STAGE_ROUTE = 8

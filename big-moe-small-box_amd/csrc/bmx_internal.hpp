@@ -63,6 +63,12 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
                           void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages,
                           const RouteFuse* rf = nullptr);
 int decode_rows_per_group(int T);
+// split path (BMX_PATH_SPLIT): the decode GEMVs for experts with few rows, the mid-size MFMA GEMMs for experts with at
+// least split_min_rows() rows, in one call; ws layout [part_gu][part_dn][act rows][xt]
+int split_min_rows();
+size_t split_ws_bytes(const MoeShape& m);
+int launch_split_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
+                         void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages);
 int launch_combine(const float* y_rows, const int32_t* inv, const void* w, const int32_t* offsets, int T, int topk,
                    int H, int E, int has_shared, float* out, hipStream_t s);
 int launch_zero_i32(int32_t* p, int n, hipStream_t s);

@@ -112,13 +112,17 @@ static bool route_in_gemv_allowed()
     return !(v && *v == '0');
 }
 
+// AUTO below the prefill and mid-size thresholds: the split path from BMX_SPLIT_MIN_TOKENS tokens (an expert can reach
+// the split path's row threshold only when the call has that many tokens), else the GEMV path
 static int resolve_path(int path, int T, int topk)
 {
-    if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL || path == BMX_PATH_MID) return path;
+    if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL || path == BMX_PATH_MID || path == BMX_PATH_SPLIT)
+        return path;
     if (path != BMX_PATH_AUTO) return -1;
     const long rows = (long)T * topk;
     if (rows >= env_rows("BMX_PREFILL_MIN_ROWS", 512)) return BMX_PATH_PREFILL;
     if (rows >= env_rows("BMX_MID_MIN_ROWS", 1L << 30)) return BMX_PATH_MID;
+    if (T >= env_rows("BMX_SPLIT_MIN_TOKENS", 8) && T >= split_min_rows()) return BMX_PATH_SPLIT;
     return BMX_PATH_DECODE;
 }
 
@@ -130,7 +134,8 @@ static int path_rows_per_group(int path, int T)
 
 static size_t experts_ws_bytes(int path, const MoeShape& m)
 {
-    return path == BMX_PATH_PREFILL ? prefill_ws_bytes(m) : path == BMX_PATH_MID ? mid_ws_bytes(m) : decode_ws_bytes(m);
+    return path == BMX_PATH_PREFILL ? prefill_ws_bytes(m) : path == BMX_PATH_MID ? mid_ws_bytes(m)
+           : path == BMX_PATH_SPLIT ? split_ws_bytes(m) : decode_ws_bytes(m);
 }
 
 static int launch_experts(int path, const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
@@ -140,6 +145,8 @@ static int launch_experts(int path, const MoeShape& m, const void* x, const bmx_
         return launch_prefill_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
     if (path == BMX_PATH_MID)
         return launch_mid_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
+    if (path == BMX_PATH_SPLIT)
+        return launch_split_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
     return launch_decode_experts(m, x, r, y_rows, act_rows, ws, ws_bytes, combine_out, combine_w, s, stages);
 }
 

@@ -18,6 +18,7 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 
 namespace bmx {
@@ -226,6 +227,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
     if (g >= *a.ngroups) return;
     const int e = a.groups[3 * g], r0 = a.groups[3 * g + 1], nr = a.groups[3 * g + 2];
     if (NM == 2 && group_skipped(a, e)) return;
+    if (split_heavy(a, e)) return;          // split path: the mid-size kernel takes this expert's rows
     gemv_unit<MX, NM>(a, ks, cb, e, r0, nr, -1);
 }
 
@@ -379,7 +381,8 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     else
     {
         float gu[16];
-        sum_splits<4, 4>(a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j, (size_t)a.R_max * a.NB * 256, a.KS_gu, gu);
+        sum_splits<4, 4>(a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j, (size_t)a.R_max * a.NB * 256,
+                         row_splits<false>(a, r), gu);
 #pragma unroll
         for (int i = 0; i < 8; ++i) { g[i] = h2f(f2h_r(gu[i])); v[i] = h2f(f2h_r(gu[8 + i])); }
     }
@@ -435,7 +438,8 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
         const size_t stride = (size_t)a.R_max * a.NB * 256;
         const float* p = a.part_gu + ((size_t)r * a.NB + cb) * 256 + 8 * j + (size_t)q * stride;
         float gu[16];
-        sum_splits_short<4, B>(p, 4 * stride, (a.KS_gu - q + 3) / 4, gu);
+        const int ks = r < nrows ? row_splits<false>(a, r) : a.KS_gu;
+        sum_splits_short<4, B>(p, 4 * stride, (ks - q + 3) / 4, gu);
 #pragma unroll
         for (int i = 0; i < 16; ++i) gu[i] = gu[i] + xor16_f(gu[i]);
 #pragma unroll
@@ -484,14 +488,15 @@ __device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float 
     const float* pp = a.part_dn + ((size_t)r * a.NBH + cb) * 128 + 8 * j;
     const size_t stride = (size_t)a.R_max * a.NBH * 128;
     u32x4 sv4;
+    const int ks = row_splits<true>(a, r);
     if (SHORT)
     {
         sv4 = ldg4(svp);
-        sum_splits_short<2, 8>(pp, stride, a.KS_dn, y);
+        sum_splits_short<2, 8>(pp, stride, ks, y);
     }
     else
     {
-        sum_splits<2, 8>(pp, stride, a.KS_dn, y);
+        sum_splits<2, 8>(pp, stride, ks, y);
         sv4 = ldg4(svp);
     }
     had128_x8(y);
@@ -906,5 +911,108 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
 }
 
 int decode_rows_per_group(int T) { return rows_per_group_of(T); }
+
+// ---- split path ---------------------------------------------------------------------------------------------------------
+// Experts with at least this many rows in a call go to the mid-size MFMA kernel (one trellis decode per 32 rows, products
+// on MFMA); the others stay on the GEMV (one decode per group of up to 8 rows, fdot2 per row). BMX_SPLIT_MIN_ROWS
+// overrides it.
+int split_min_rows()
+{
+    const char* v = getenv("BMX_SPLIT_MIN_ROWS");
+    const int n = (v && *v) ? atoi(v) : 4;
+    return n < 1 ? 1 : n;
+}
+
+size_t split_ws_bytes(const MoeShape& m)
+{
+    const DecodePlan p = decode_plan(m);
+    int ksg = 1, ksd = 1;
+    split_mid_splits(m, &ksg, &ksd);
+    const size_t R = (size_t)p.R_max;
+    return align_up((size_t)std::max(p.KS_gu, ksg) * R * p.NB * 256 * 4, 256) +
+           align_up((size_t)std::max(p.KS_dn, ksd) * R * p.NBH * 128 * 4, 256) + align_up(R * m.I * 2, 256) +
+           align_up((size_t)2 * R * m.H * 2, 256);
+}
+
+// One call over both kernels: the heavy experts' rows (counts[e] >= split_min) on k_mid_gemm over (expert, 32-row chunk)
+// units, the others' on k_gemv_part over the dispatch's groups (heavy groups skipped); both write the same partial
+// layout, each row with its own kernel's k-split count, which the epilogues read per row. Order on the stream: prep of
+// the heavy rows, gate / up (GEMV, then mid), epilogue, down (GEMV, then mid), combine.
+int launch_split_experts(const MoeShape& m, const void* x, const bmx_routes* r, float* y_rows, void* act_rows,
+                         void* ws, size_t ws_bytes, float* combine_out, const void* combine_w, hipStream_t s, int stages)
+{
+    if (m.H % 128 || m.I % 128 || m.H <= 0 || m.I <= 0)
+        return set_error(BMX_ERR_ARG, "moe experts: H (%d) and I (%d) must be multiples of 128", m.H, m.I);
+    if (ws_bytes < split_ws_bytes(m))
+        return set_error(BMX_ERR_WORKSPACE, "moe experts: workspace %zu < %zu", ws_bytes, split_ws_bytes(m));
+    if (!r->row_expert || !r->counts || !r->uexp || !r->nuniq)
+        return set_error(BMX_ERR_ARG, "moe experts: split path needs the routes' counts, uexp, nuniq and row_expert");
+    const DecodePlan p = decode_plan(m);
+    int ksg = 1, ksd = 1;
+    split_mid_splits(m, &ksg, &ksd);
+    const size_t R = (size_t)p.R_max;
+    char* w = static_cast<char*>(ws);
+    GvArgs a;
+    a.experts = m.experts; a.shared = m.shared_ex; a.E = m.E; a.H = m.H; a.I = m.I; a.act = m.act; a.gated = m.gated;
+    a.limit = m.limit;
+    a.x = static_cast<const uint16_t*>(x);
+    a.row_token = r->row_token; a.groups = r->groups; a.ngroups = r->ngroups; a.row_expert = r->row_expert;
+    a.part_gu = reinterpret_cast<float*>(w);
+    w += align_up((size_t)std::max(p.KS_gu, ksg) * R * p.NB * 256 * 4, 256);
+    a.part_dn = reinterpret_cast<float*>(w);
+    w += align_up((size_t)std::max(p.KS_dn, ksd) * R * p.NBH * 128 * 4, 256);
+    uint16_t* own_act = reinterpret_cast<uint16_t*>(w);
+    a.act_rows = act_rows ? static_cast<uint16_t*>(act_rows) : own_act;
+    w += align_up(R * m.I * 2, 256);
+    a.xt = reinterpret_cast<uint16_t*>(w);
+    a.y_rows = y_rows;
+    a.KS_gu = p.KS_gu; a.KS_dn = p.KS_dn; a.NB = p.NB; a.NBH = p.NBH; a.R_max = p.R_max;
+    a.NE = m.E + (m.shared ? 1 : 0);
+    a.out = combine_out; a.w = static_cast<const uint16_t*>(combine_w); a.inv = r->inv; a.offsets = r->offsets;
+    a.T = m.T; a.topk = m.topk; a.has_shared = m.shared;
+    a.fresh = m.fresh;
+    a.sh_gate = m.shared_gate;
+    a.filter = 0;
+    a.act_in_down = 0;
+    a.gu_half = 0;
+    a.split_min = split_min_rows();
+    a.split_chunks = (m.T + 31) / 32;          // an expert has at most one row per token
+    a.KS_gu_mid = ksg;
+    a.KS_dn_mid = ksd;
+    a.counts = r->counts; a.uexp = r->uexp; a.nuniq = r->nuniq;
+    GvArgs b = a;                              // the mid-size kernel's view: its own k-splits
+    b.KS_gu = ksg;
+    b.KS_dn = ksd;
+    const int nu_max = (int)std::min<long>((long)m.T * m.topk, m.E) + (m.shared ? 1 : 0);
+    const int MR = rows_per_group_of(m.T);
+    auto gemv = [&](int st) {
+        switch (MR)
+        {
+            case 1: launch_mr<1>(a, p, st, s, nullptr); break;
+            case 2: launch_mr<2>(a, p, st, s, nullptr); break;
+            case 4: launch_mr<4>(a, p, st, s, nullptr); break;
+            default: launch_mr<8>(a, p, st, s, nullptr); break;
+        }
+    };
+    if (stages & (1 << BMX_STAGE_PREP)) launch_split_mid(b, BMX_STAGE_PREP, nu_max, s);
+    for (int f = 0; f < 3; ++f)
+    {
+        const int st = f == 0 ? BMX_STAGE_GATE_UP : f == 1 ? BMX_STAGE_GATE_UP_RESIDENT : BMX_STAGE_GATE_UP_STAGED;
+        if (!(stages & (1 << st))) continue;
+        gemv(1 << st);
+        GvArgs bf = b;
+        bf.filter = f;
+        launch_split_mid(bf, st, nu_max, s);
+    }
+    if (stages & (1 << BMX_STAGE_ACT)) launch_epilogue(a, BMX_STAGE_ACT, s);
+    if (stages & (1 << BMX_STAGE_DOWN))
+    {
+        gemv(1 << BMX_STAGE_DOWN);
+        launch_split_mid(b, BMX_STAGE_DOWN, nu_max, s);
+    }
+    if (stages & (1 << BMX_STAGE_COMBINE)) launch_epilogue(a, BMX_STAGE_COMBINE, s);
+    if (stages & (1 << BMX_STAGE_DOWN_OUT)) launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
+    return check_launch("moe experts (split path)");
+}
 
 }  // namespace bmx

@@ -36,7 +36,29 @@ struct GvArgs {
                                // epilogue's own rounding of that split's sum (RN of 0.0f + product): same bits downstream
     const uint16_t* sh_gate;   // fp16 [H] or null: the shared expert's output is scaled by sigmoid(x[t] . sh_gate)
     int pf_pairs = 0;          // prefill: two consecutive 128-row groups of one expert run as one 256-row tile
+    // split path: experts with at least split_min rows (counts[e]) run on the mid-size MFMA kernel, in units of up to 32
+    // rows (split_chunks per expert, taken over the unique experts uexp[0 .. *nuniq)), the others on the GEMV; a row's
+    // partials then have KS_gu_mid / KS_dn_mid splits when its expert is heavy, KS_gu / KS_dn otherwise. 0: off
+    int split_min = 0;
+    int split_chunks = 0;
+    int KS_gu_mid = 0, KS_dn_mid = 0;
+    const int32_t* counts = nullptr;
+    const int32_t* uexp = nullptr;
+    const int32_t* nuniq = nullptr;
 };
+
+// split path: expert e (a local id, E for the shared expert) runs on the mid-size MFMA kernel
+__device__ __forceinline__ bool split_heavy(const GvArgs& a, int e)
+{
+    return a.split_min > 0 && a.counts[e] >= a.split_min;
+}
+// k-splits of the gate / up (DN = false) or down (DN = true) partials of dispatch row r (r < the rows of the call)
+template <bool DN>
+__device__ __forceinline__ int row_splits(const GvArgs& a, int r)
+{
+    if (a.split_min > 0 && a.counts[a.row_expert[r]] >= a.split_min) return DN ? a.KS_dn_mid : a.KS_gu_mid;
+    return DN ? a.KS_dn : a.KS_gu;
+}
 
 // The shared expert's gate of token t, sigmoid(x[t] . sh_gate), by the calling 16-lane group (every lane of the group
 // gets it): lane j sums x[h] sh_gate[h] over h = 128 b + 8 j + i, b ascending then i = 0 .. 7, one fp32 fma each (fp16
@@ -114,5 +136,11 @@ __device__ __forceinline__ int lane_col(int lane, int c)
 
 // epilogue kernels of moe_decode.hip, launched with the partial layout above (any k-split count)
 int launch_epilogue(const GvArgs& a, int stage, hipStream_t s);
+
+// split path, moe_prefill.hip: the k-splits of the mid-size kernel for a call, and the launch of the heavy experts' prep
+// (BMX_STAGE_PREP), gate / up GEMMs (any gate / up stage, with a.filter) or down GEMMs (BMX_STAGE_DOWN); a carries
+// the mid-size splits in KS_gu / KS_dn
+void split_mid_splits(const MoeShape& m, int* ks_gu, int* ks_dn);
+void launch_split_mid(const GvArgs& a, int stage, int nu_max, hipStream_t s);
 
 }  // namespace bmx

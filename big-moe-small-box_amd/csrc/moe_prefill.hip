@@ -40,6 +40,7 @@ __global__ __launch_bounds__(256) void k_pf_prep(GvArgs a)
     const int j = threadIdx.x & 15, run = (int)(u % nrun), mat = (int)((u / nrun) & 1), r = (int)(u / nrun / 2);
     if (r >= a.offsets[a.NE]) return;
     const int e = a.row_expert[r];
+    if (a.split_min && !split_heavy(a, e)) return;      // split path: the GEMV rotates the other rows itself
     const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
     const uint16_t* xr = a.x + (size_t)a.row_token[r] * a.H + 8 * j;
     const uint16_t* su = reinterpret_cast<const uint16_t*>(ex.suh[mat]) + 8 * j;
@@ -621,11 +622,26 @@ __global__ __launch_bounds__(MID_WAVES * 64) void k_mid_gemm(GvArgs a)
     jb.nb128 = nb128;
     if (DOWN) { jb.g = lid / NB2; jb.mat = 2; jb.cb = lid % NB2; }
     else { jb.g = lid / (2 * NB2); jb.mat = (lid / NB2) & 1; jb.cb = lid % NB2; }
-    if (jb.g >= *a.ngroups) return;
-    jb.e = a.groups[3 * jb.g];
-    if (!DOWN && group_skipped(a, jb.e)) return;
-    jb.r0 = a.groups[3 * jb.g + 1];
-    jb.nr = a.groups[3 * jb.g + 2];
+    if (a.split_min)
+    {
+        // split path: units over (unique expert, chunk of 32 rows); only the heavy experts' rows are computed here
+        const int u = jb.g / a.split_chunks, q = jb.g % a.split_chunks;
+        if (u >= *a.nuniq) return;
+        jb.e = a.uexp[u];
+        const int c = a.counts[jb.e];
+        if (c < a.split_min || MID_M * q >= c) return;
+        if (!DOWN && group_skipped(a, jb.e)) return;
+        jb.r0 = a.offsets[jb.e] + MID_M * q;
+        jb.nr = min(MID_M, c - MID_M * q);
+    }
+    else
+    {
+        if (jb.g >= *a.ngroups) return;
+        jb.e = a.groups[3 * jb.g];
+        if (!DOWN && group_skipped(a, jb.e)) return;
+        jb.r0 = a.groups[3 * jb.g + 1];
+        jb.nr = a.groups[3 * jb.g + 2];
+    }
     jb.ex = jb.e == a.E ? a.shared : a.experts + jb.e;
     jb.K = DOWN ? a.I : a.H;
     jb.N = DOWN ? a.H : a.I;
@@ -780,6 +796,29 @@ int launch_mid_experts(const MoeShape& m, const void* x, const bmx_routes* r, fl
     if (!rc && (stages & (1 << BMX_STAGE_DOWN_OUT))) rc = launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
     if (rc) return rc;
     return check_launch("moe experts (mid-size path)");
+}
+
+// ---- split path: the heavy experts' share ---------------------------------------------------------------------------
+void split_mid_splits(const MoeShape& m, int* ks_gu, int* ks_dn)
+{
+    const MidPlan p = mid_plan(m);
+    *ks_gu = p.KS_gu;
+    *ks_dn = p.KS_dn;
+}
+
+// The prep of the heavy experts' rows and their mid-size GEMMs. a: the split path's arguments with KS_gu / KS_dn set to
+// the mid-size splits (KS_gu_mid / KS_dn_mid); nu_max: the most unique experts a call can have.
+void launch_split_mid(const GvArgs& a, int stage, int nu_max, hipStream_t s)
+{
+    const long units = (long)nu_max * a.split_chunks;
+    if (stage == BMX_STAGE_PREP)
+        hipLaunchKernelGGL(k_pf_prep, prep_grid(a.R_max, a.H), dim3(256), 0, s, a);
+    else if (stage == BMX_STAGE_DOWN)
+        hipLaunchKernelGGL(k_mid_gemm<true>, dim3((unsigned)(units * ((a.NBH + 1) / 2) * a.KS_dn)), dim3(MID_WAVES * 64),
+                           0, s, a);
+    else
+        hipLaunchKernelGGL(k_mid_gemm<false>, dim3((unsigned)(units * 2 * ((a.NB + 1) / 2) * a.KS_gu)),
+                           dim3(MID_WAVES * 64), 0, s, a);
 }
 
 size_t prefill_ws_bytes(const MoeShape& m)

@@ -408,9 +408,15 @@ def test_full_size_properties_c2_t8(cuda):
     s2[:, 3] = tab.E
     w2 = w.clone()
     w2[:, 3] = 0
-    a = bmx.ops.moe_forward(d, x, s2, w)
-    b = bmx.ops.moe_forward(d, x, sel, w2)
-    assert torch.equal(a, b) and not torch.equal(a, out)
+    # on the GEMV path every row is computed on its own: a dropped pick and a weight-0 pick give the same bits. AUTO takes
+    # the split path here, where a row's kernel follows its expert's row count, which the weight-0 pick still adds to:
+    # the other rows of that expert may move to the MFMA kernel, within the layer tolerance
+    a = bmx.ops.moe_forward(d, x, s2, w, bmx.PATH_DECODE)
+    b = bmx.ops.moe_forward(d, x, sel, w2, bmx.PATH_DECODE)
+    assert torch.equal(a, b) and not torch.equal(a, bmx.ops.moe_forward(d, x, sel, w, bmx.PATH_DECODE))
+    a2 = bmx.ops.moe_forward(d, x, s2, w)
+    b2 = bmx.ops.moe_forward(d, x, sel, w2)
+    assert float((a2 - b2).abs().max()) < 1e-2 and float((a2 - a).abs().max()) < 1e-2
     full = bmx.ops.moe_forward(tab.desc(8), x, sel, w)
     only_shared = bmx.ops.moe_forward(tab.desc(8), x, sel, torch.zeros_like(w))
     assert torch.allclose(full, out + only_shared, rtol=1e-5, atol=1e-5)
