@@ -112,8 +112,9 @@ static bool route_in_gemv_allowed()
     return !(v && *v == '0');
 }
 
-// AUTO below the prefill and mid-size thresholds: the split path from BMX_SPLIT_MIN_TOKENS tokens (an expert can reach
-// the split path's row threshold only when the call has that many tokens), else the GEMV path
+// AUTO below the prefill and mid-size thresholds: the split path (the GEMV or the mid-size GEMMs, chosen on the device
+// from the call's rows per expert) from BMX_SPLIT_MIN_TOKENS tokens, the GEMV path below (at 8 tokens the split path's
+// idle launches cost 3 % of the GLM-shaped layer, and few rows per expert are the rule there)
 static int resolve_path(int path, int T, int topk)
 {
     if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL || path == BMX_PATH_MID || path == BMX_PATH_SPLIT)
@@ -122,7 +123,7 @@ static int resolve_path(int path, int T, int topk)
     const long rows = (long)T * topk;
     if (rows >= env_rows("BMX_PREFILL_MIN_ROWS", 512)) return BMX_PATH_PREFILL;
     if (rows >= env_rows("BMX_MID_MIN_ROWS", 1L << 30)) return BMX_PATH_MID;
-    if (T >= env_rows("BMX_SPLIT_MIN_TOKENS", 8) && T >= split_min_rows()) return BMX_PATH_SPLIT;
+    if (T >= env_rows("BMX_SPLIT_MIN_TOKENS", 16)) return BMX_PATH_SPLIT;
     return BMX_PATH_DECODE;
 }
 

@@ -219,6 +219,13 @@ __device__ __forceinline__ void gemv_unit(const GvArgs& a, int ks, int cb, int e
 template <int MX, int NM>
 __global__ __launch_bounds__(GV_THREADS) void k_gemv_part(GvArgs a)
 {
+    if (NM == 2 && a.split_min > a.T && a.filter != 2 && split_callwide(a))
+    {
+        // split path, every expert on the mid-size kernel: this launch rotates the rows for it instead
+        const long units = 2L * a.offsets[a.NE] * ((a.H / 128 + PREP_BPU - 1) / PREP_BPU);
+        for (long u = (long)blockIdx.x * 16 + (threadIdx.x >> 4); u < units; u += (long)gridDim.x * 16) prep_unit(a, u);
+        return;
+    }
     int bid = blockIdx.x;
     const int KS = NM == 2 ? a.KS_gu : a.KS_dn, NB = NM == 2 ? a.NB : a.NBH;
     const int ks = bid % KS;
@@ -913,14 +920,28 @@ int launch_decode_experts(const MoeShape& m, const void* x, const bmx_routes* r,
 int decode_rows_per_group(int T) { return rows_per_group_of(T); }
 
 // ---- split path ---------------------------------------------------------------------------------------------------------
-// Experts with at least this many rows in a call go to the mid-size MFMA kernel (one trellis decode per 32 rows, products
-// on MFMA); the others stay on the GEMV (one decode per group of up to 8 rows, fdot2 per row). BMX_SPLIT_MIN_ROWS
-// overrides it.
+// The mid-size MFMA kernel decodes an expert once per 32 rows and multiplies on MFMA; the GEMV decodes once per group of
+// up to 8 rows and pays an fdot2 per row and weight, but has the shorter start. Measured on the 16-token speculative-
+// verify batch (the DeepSeek shape, 4-6 rows per expert): GEMV 172.6, mid-size 128.6 us; on the GLM shape at 8 tokens
+// (1.5 rows per expert): GEMV 225.7, mid-size 293. Mixing the two per expert in one call runs both kernels back to back
+// and measured worse than either alone (151-168 us, 255-278 us), so the choice is per call: all experts on the
+// mid-size kernel when the call averages at least BMX_SPLIT_RATIO rows per unique expert (default 2.5), else all on the
+// GEMV; BMX_SPLIT_MIN_ROWS = n also sends experts with at least n rows to the mid-size kernel in a GEMV call (off by
+// default: on the GEMV-chosen calls measured, 16- and 32-token batches of both shapes, it only added the idle cost of
+// walking the units).
 int split_min_rows()
 {
     const char* v = getenv("BMX_SPLIT_MIN_ROWS");
-    const int n = (v && *v) ? atoi(v) : 4;
+    const int n = (v && *v) ? atoi(v) : (1 << 30);
     return n < 1 ? 1 : n;
+}
+
+static int split_ratio2()
+{
+    const char* v = getenv("BMX_SPLIT_RATIO");
+    const double r = (v && *v) ? atof(v) : 2.5;
+    const int q = (int)(2.0 * r + 0.5);
+    return q < 0 ? 0 : q;
 }
 
 size_t split_ws_bytes(const MoeShape& m)
@@ -934,7 +955,7 @@ size_t split_ws_bytes(const MoeShape& m)
            align_up((size_t)2 * R * m.H * 2, 256);
 }
 
-// One call over both kernels: the heavy experts' rows (counts[e] >= split_min) on k_mid_gemm over (expert, 32-row chunk)
+// One call over both kernels: the heavy experts' rows (split_heavy) on k_mid_gemm over (expert, 32-row chunk)
 // units, the others' on k_gemv_part over the dispatch's groups (heavy groups skipped); both write the same partial
 // layout, each row with its own kernel's k-split count, which the epilogues read per row. Order on the stream: prep of
 // the heavy rows, gate / up (GEMV, then mid), epilogue, down (GEMV, then mid), combine.
@@ -976,6 +997,7 @@ int launch_split_experts(const MoeShape& m, const void* x, const bmx_routes* r, 
     a.act_in_down = 0;
     a.gu_half = 0;
     a.split_min = split_min_rows();
+    a.split_ratio2 = split_ratio2() > 0 ? split_ratio2() : 1 << 30;
     a.split_chunks = (m.T + 31) / 32;          // an expert has at most one row per token
     a.KS_gu_mid = ksg;
     a.KS_dn_mid = ksd;
@@ -994,7 +1016,9 @@ int launch_split_experts(const MoeShape& m, const void* x, const bmx_routes* r, 
             default: launch_mr<8>(a, p, st, s, nullptr); break;
         }
     };
-    if (stages & (1 << BMX_STAGE_PREP)) launch_split_mid(b, BMX_STAGE_PREP, nu_max, s);
+    // the heavy rows' rotation: a kernel of its own when single experts can be heavy; otherwise the gate / up GEMV's
+    // launch does it when the call goes to the mid-size kernel (its groups are idle then)
+    if ((stages & (1 << BMX_STAGE_PREP)) && a.split_min <= m.T) launch_split_mid(b, BMX_STAGE_PREP, nu_max, s);
     for (int f = 0; f < 3; ++f)
     {
         const int st = f == 0 ? BMX_STAGE_GATE_UP : f == 1 ? BMX_STAGE_GATE_UP_RESIDENT : BMX_STAGE_GATE_UP_STAGED;

@@ -36,10 +36,13 @@ struct GvArgs {
                                // epilogue's own rounding of that split's sum (RN of 0.0f + product): same bits downstream
     const uint16_t* sh_gate;   // fp16 [H] or null: the shared expert's output is scaled by sigmoid(x[t] . sh_gate)
     int pf_pairs = 0;          // prefill: two consecutive 128-row groups of one expert run as one 256-row tile
-    // split path: experts with at least split_min rows (counts[e]) run on the mid-size MFMA kernel, in units of up to 32
-    // rows (split_chunks per expert, taken over the unique experts uexp[0 .. *nuniq)), the others on the GEMV; a row's
-    // partials then have KS_gu_mid / KS_dn_mid splits when its expert is heavy, KS_gu / KS_dn otherwise. 0: off
+    // split path (split_min > 0): an expert is heavy when the call averages at least split_ratio2 / 2 rows per expert
+    // (every expert then is), or when it has at least split_min rows itself. Heavy experts run on the mid-size MFMA
+    // kernel, in units of up to 32 rows (split_chunks per expert, taken over the unique experts uexp[0 .. *nuniq)), the
+    // others on the GEMV; a row's partials have KS_gu_mid / KS_dn_mid splits when its expert is heavy, KS_gu / KS_dn
+    // otherwise. 0: off
     int split_min = 0;
+    int split_ratio2 = 0;
     int split_chunks = 0;
     int KS_gu_mid = 0, KS_dn_mid = 0;
     const int32_t* counts = nullptr;
@@ -47,16 +50,19 @@ struct GvArgs {
     const int32_t* nuniq = nullptr;
 };
 
-// split path: expert e (a local id, E for the shared expert) runs on the mid-size MFMA kernel
+// split path: expert e (a local id, E for the shared expert) runs on the mid-size MFMA kernel (the call's rows over
+// its unique experts, both from the dispatch, decide it for every expert at once; a very heavy expert goes there anyway)
 __device__ __forceinline__ bool split_heavy(const GvArgs& a, int e)
 {
-    return a.split_min > 0 && a.counts[e] >= a.split_min;
+    if (a.split_min <= 0) return false;
+    if (2 * a.offsets[a.NE] >= a.split_ratio2 * *a.nuniq) return true;
+    return a.split_min <= a.T && a.counts[e] >= a.split_min;
 }
 // k-splits of the gate / up (DN = false) or down (DN = true) partials of dispatch row r (r < the rows of the call)
 template <bool DN>
 __device__ __forceinline__ int row_splits(const GvArgs& a, int r)
 {
-    if (a.split_min > 0 && a.counts[a.row_expert[r]] >= a.split_min) return DN ? a.KS_dn_mid : a.KS_gu_mid;
+    if (split_heavy(a, a.row_expert[r])) return DN ? a.KS_dn_mid : a.KS_gu_mid;
     return DN ? a.KS_dn : a.KS_gu;
 }
 
@@ -81,6 +87,43 @@ __device__ __forceinline__ float shared_gate16(const uint16_t* x, const uint16_t
     acc = acc + dpp_f<0x4E>(acc);      // lane ^ 2
     acc = acc + dpp_f<0xB1>(acc);      // lane ^ 1
     return sigmoid_fixed(acc);
+}
+
+// split path: the call averages enough rows per unique expert to run every expert on the mid-size kernel
+__device__ __forceinline__ bool split_callwide(const GvArgs& a)
+{
+    return 2 * a.offsets[a.NE] >= a.split_ratio2 * *a.nuniq;
+}
+
+// Rotated gate / up input of one dispatch row for the MFMA paths, xt = RN16(H128(x * suh) * R), by a 16-lane group: unit
+// u = (row, matrix, run of PREP_BPU 128-blocks), 8 consecutive inputs per lane. Split path: heavy experts' rows only.
+constexpr int PREP_BPU = 4;
+__device__ __forceinline__ void prep_unit(const GvArgs& a, long u)
+{
+    const int nblk = a.H / 128, nrun = (nblk + PREP_BPU - 1) / PREP_BPU;
+    const int j = threadIdx.x & 15, run = (int)(u % nrun), mat = (int)((u / nrun) & 1), r = (int)(u / nrun / 2);
+    if (r >= a.offsets[a.NE]) return;
+    const int e = a.row_expert[r];
+    if (a.split_min && !split_heavy(a, e)) return;      // split path: the GEMV rotates the other rows itself
+    const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
+    const uint16_t* xr = a.x + (size_t)a.row_token[r] * a.H + 8 * j;
+    const uint16_t* su = reinterpret_cast<const uint16_t*>(ex.suh[mat]) + 8 * j;
+    uint16_t* dst = a.xt + ((size_t)mat * a.R_max + r) * a.H + 8 * j;
+#pragma unroll
+    for (int i = 0; i < PREP_BPU; ++i)
+    {
+        const int b = run * PREP_BPU + i;
+        if (b >= nblk) break;
+        float v[8], s[8];
+        unpack8(ldg4(xr + 128 * b), v);
+        unpack8(ldg4(su + 128 * b), s);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = v[q] * s[q];
+        had128_x8(v);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = v[q] * R_SCALE;
+        *reinterpret_cast<u32x4*>(dst + 128 * b) = pack8_r(v);
+    }
 }
 
 // group filter of the split gate / up stages (the shared expert, index E, is never fresh)

@@ -15,6 +15,8 @@
 //   (k_dn_combine): rotation * svh, slots summed in slot order (shared with the decode path)
 #include "moe_kernels.hpp"
 
+#include <algorithm>
+
 namespace bmx {
 
 constexpr int PF_M = 128;                    // rows per group
@@ -32,34 +34,9 @@ __device__ __forceinline__ int xcd_block(int bid, int nblk)
 }
 
 // ---- rotated inputs: 16 lanes per (row, matrix, run of PREP_BPU 128-blocks), 8 consecutive inputs per lane -------------
-constexpr int PREP_BPU = 4;
 __global__ __launch_bounds__(256) void k_pf_prep(GvArgs a)
 {
-    const int nblk = a.H / 128, nrun = (nblk + PREP_BPU - 1) / PREP_BPU;
-    const long u = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int j = threadIdx.x & 15, run = (int)(u % nrun), mat = (int)((u / nrun) & 1), r = (int)(u / nrun / 2);
-    if (r >= a.offsets[a.NE]) return;
-    const int e = a.row_expert[r];
-    if (a.split_min && !split_heavy(a, e)) return;      // split path: the GEMV rotates the other rows itself
-    const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
-    const uint16_t* xr = a.x + (size_t)a.row_token[r] * a.H + 8 * j;
-    const uint16_t* su = reinterpret_cast<const uint16_t*>(ex.suh[mat]) + 8 * j;
-    uint16_t* dst = a.xt + ((size_t)mat * a.R_max + r) * a.H + 8 * j;
-#pragma unroll
-    for (int i = 0; i < PREP_BPU; ++i)
-    {
-        const int b = run * PREP_BPU + i;
-        if (b >= nblk) break;
-        float v[8], s[8];
-        unpack8(ldg4(xr + 128 * b), v);
-        unpack8(ldg4(su + 128 * b), s);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = v[q] * s[q];
-        had128_x8(v);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = v[q] * R_SCALE;
-        *reinterpret_cast<u32x4*>(dst + 128 * b) = pack8_r(v);
-    }
+    prep_unit(a, (long)blockIdx.x * 16 + (threadIdx.x >> 4));
 }
 
 static dim3 prep_grid(int R_max, int H)
@@ -610,12 +587,12 @@ __device__ __forceinline__ void mid_run_any(const PfJob& jb, const uint8_t* mat_
     else mid_run<F, 0>(jb, mat_base, asrc, s0, n, acc0, acc1);
 }
 
+// One unit of the mid-size GEMM: (group or heavy-expert chunk, matrix, 256-column block, k-split) from its index lid.
 template <bool DOWN>
-__global__ __launch_bounds__(MID_WAVES * 64) void k_mid_gemm(GvArgs a)
+__device__ __forceinline__ void mid_unit(const GvArgs& a, int lid)
 {
     const int nb128 = DOWN ? a.NBH : a.NB;
     const int NB2 = (nb128 + 1) / 2, KS = DOWN ? a.KS_dn : a.KS_gu;
-    int lid = xcd_block(blockIdx.x, gridDim.x);
     const int ksp = lid % KS;
     lid /= KS;
     PfJob jb;
@@ -629,7 +606,7 @@ __global__ __launch_bounds__(MID_WAVES * 64) void k_mid_gemm(GvArgs a)
         if (u >= *a.nuniq) return;
         jb.e = a.uexp[u];
         const int c = a.counts[jb.e];
-        if (c < a.split_min || MID_M * q >= c) return;
+        if (MID_M * q >= c || !split_heavy(a, jb.e)) return;
         if (!DOWN && group_skipped(a, jb.e)) return;
         jb.r0 = a.offsets[jb.e] + MID_M * q;
         jb.nr = min(MID_M, c - MID_M * q);
@@ -670,6 +647,28 @@ __global__ __launch_bounds__(MID_WAVES * 64) void k_mid_gemm(GvArgs a)
         const float y = acc0[v] + acc1[v];
         if (DOWN) a.part_dn[(r * a.NBH + cbo) * 128 + col] = y;
         else a.part_gu[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] = y;
+    }
+}
+
+template <bool DOWN>
+__global__ __launch_bounds__(MID_WAVES * 64) void k_mid_gemm(GvArgs a)
+{
+    if (!a.split_min)
+    {
+        mid_unit<DOWN>(a, xcd_block(blockIdx.x, gridDim.x));
+        return;
+    }
+    // split path: a grid of at most MID_SPLIT_WGS workgroups loops over the units of the call's unique experts, so a call
+    // that keeps every expert on the GEMV pays for few idle workgroups (none past the first check when no expert can
+    // reach split_min rows)
+    if (a.split_min > a.T + 1 && 2 * a.offsets[a.NE] < a.split_ratio2 * *a.nuniq) return;
+    const int nb128 = DOWN ? a.NBH : a.NB;
+    const int per = (DOWN ? 1 : 2) * ((nb128 + 1) / 2) * (DOWN ? a.KS_dn : a.KS_gu);
+    const int units = *a.nuniq * a.split_chunks * per;
+    for (int lid = blockIdx.x; lid < units; lid += gridDim.x)
+    {
+        mid_unit<DOWN>(a, lid);
+        __syncthreads();          // the unit's LDS stages are read out before the next unit writes them
     }
 }
 
@@ -808,16 +807,19 @@ void split_mid_splits(const MoeShape& m, int* ks_gu, int* ks_dn)
 
 // The prep of the heavy experts' rows and their mid-size GEMMs. a: the split path's arguments with KS_gu / KS_dn set to
 // the mid-size splits (KS_gu_mid / KS_dn_mid); nu_max: the most unique experts a call can have.
+constexpr long MID_SPLIT_WGS = 1024;
+
 void launch_split_mid(const GvArgs& a, int stage, int nu_max, hipStream_t s)
 {
     const long units = (long)nu_max * a.split_chunks;
     if (stage == BMX_STAGE_PREP)
         hipLaunchKernelGGL(k_pf_prep, prep_grid(a.R_max, a.H), dim3(256), 0, s, a);
     else if (stage == BMX_STAGE_DOWN)
-        hipLaunchKernelGGL(k_mid_gemm<true>, dim3((unsigned)(units * ((a.NBH + 1) / 2) * a.KS_dn)), dim3(MID_WAVES * 64),
-                           0, s, a);
+        hipLaunchKernelGGL(k_mid_gemm<true>, dim3((unsigned)std::min(MID_SPLIT_WGS, units * ((a.NBH + 1) / 2) * a.KS_dn)),
+                           dim3(MID_WAVES * 64), 0, s, a);
     else
-        hipLaunchKernelGGL(k_mid_gemm<false>, dim3((unsigned)(units * 2 * ((a.NB + 1) / 2) * a.KS_gu)),
+        hipLaunchKernelGGL(k_mid_gemm<false>,
+                           dim3((unsigned)std::min(MID_SPLIT_WGS, units * 2 * ((a.NB + 1) / 2) * a.KS_gu)),
                            dim3(MID_WAVES * 64), 0, s, a);
 }
 

@@ -47,10 +47,11 @@ enum bmx_act { BMX_ACT_SILU = 0, BMX_ACT_GELU = 1, BMX_ACT_RELU2 = 2, BMX_ACT_SI
 /* expert-products path: DECODE = bandwidth-bound grouped GEMVs (the reference's bsz-N decode kernel,
  * engine/kernels/x16/x16_dev.cu:205-392), PREFILL = grouped GEMMs on MFMA in groups of 128 rows (the reference's staged
  * prefill call, engine/tiers.py:673-700), MID = grouped GEMMs on MFMA in groups of 32 rows with k-splits (decode batches
- * of several tokens per expert), SPLIT = both in one call, chosen per expert on the device from the dispatch's row
- * counts: experts with at least BMX_SPLIT_MIN_ROWS rows (default 4) on the MID kernels, the rest on the DECODE GEMVs.
- * AUTO picks PREFILL from BMX_PREFILL_MIN_ROWS routed rows (T * topk; default 512), MID from BMX_MID_MIN_ROWS, SPLIT from
- * BMX_SPLIT_MIN_TOKENS tokens (default 8; environment variables), DECODE below. */
+ * of several tokens per expert), SPLIT = the DECODE or the MID kernels chosen on the device from the dispatch: every
+ * expert on the MID kernels when the call has at least BMX_SPLIT_RATIO rows per unique expert (default 2.5), else on the
+ * DECODE GEMVs except experts with at least BMX_SPLIT_MIN_ROWS rows (default 32). AUTO picks PREFILL from
+ * BMX_PREFILL_MIN_ROWS routed rows (T * topk; default 512), MID from BMX_MID_MIN_ROWS, SPLIT from BMX_SPLIT_MIN_TOKENS
+ * tokens (default 16; environment variables), DECODE below. */
 enum bmx_path { BMX_PATH_AUTO = 0, BMX_PATH_DECODE = 1, BMX_PATH_PREFILL = 2, BMX_PATH_MID = 3, BMX_PATH_SPLIT = 4 };
 
 /* One expert: three EXL3 linears (gate [H->I], up [H->I], down [I->H]). Device-resident array, one entry per expert.

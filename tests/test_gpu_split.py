@@ -38,8 +38,14 @@ def mixed_routes(T, topk, E, seed):
     return sel
 
 
+# (BMX_SPLIT_RATIO, BMX_SPLIT_MIN_ROWS, which experts are heavy): per expert by its rows; every expert (the call's rows
+# per expert reach the ratio); none
+MODES = [("1000", "4", "rows"), ("0.5", "1000", "all"), ("1000", "1000", "none")]
+
+
+@pytest.mark.parametrize("ratio,min_rows,heavy", MODES, ids=[m[2] for m in MODES])
 @pytest.mark.parametrize("cfg,T,E", [("c5", 16, 64), ("c2", 16, 48), ("c2", 9, 32)])
-def test_split_rows_follow_their_kernel(cuda, monkeypatch, cfg, T, E):
+def test_split_rows_follow_their_kernel(cuda, monkeypatch, cfg, T, E, ratio, min_rows, heavy):
     import bmx
     from bmx import synth
     L = bmx._lib
@@ -49,7 +55,8 @@ def test_split_rows_follow_their_kernel(cuda, monkeypatch, cfg, T, E):
     topk = c["topk"]
     sel = torch.from_numpy(mixed_routes(T, topk, E, 63)).to(cuda)
     desc = tab.desc(topk)
-    monkeypatch.setenv("BMX_SPLIT_MIN_ROWS", "4")
+    monkeypatch.setenv("BMX_SPLIT_MIN_ROWS", min_rows)
+    monkeypatch.setenv("BMX_SPLIT_RATIO", ratio)
     rows = {}
     for name, path in (("split", L.PATH_SPLIT), ("decode", L.PATH_DECODE), ("mid", L.PATH_MID)):
         r = bmx.ops.dispatch(sel, E, 0, tab.has_shared, bmx.lib().bmx_rows_per_group(T, topk, path))
@@ -64,19 +71,23 @@ def test_split_rows_follow_their_kernel(cuda, monkeypatch, cfg, T, E):
         r0, r1 = int(offs[e]), int(offs[e + 1])
         if r1 <= r0:
             continue
-        ref = rows["mid" if counts[e] >= 4 else "decode"][0]
+        is_heavy = heavy == "all" or (heavy == "rows" and counts[e] >= 4)
+        ref = rows["mid" if is_heavy else "decode"][0]
         got = rows["split"][0]
         assert np.array_equal(got[r0:r1].view(np.uint32), ref[r0:r1].view(np.uint32)), (cfg, e, int(counts[e]))
-        if counts[e] >= 4:
+        if is_heavy:
             nheavy += 1
         else:
             nlight += 1
-    say("split rows", cfg, T, E, "heavy experts", nheavy, "light experts", nlight)
-    assert nheavy >= 3 and nlight >= 3
+    say("split rows", cfg, T, E, heavy, "heavy experts", nheavy, "light experts", nlight)
+    if heavy == "rows":
+        assert nheavy >= 3 and nlight >= 3
+    else:
+        assert (nlight if heavy == "all" else nheavy) == 0
 
 
-@pytest.mark.parametrize("thr", ["1", "4", "1000"])
-def test_split_layer_against_oracle(cuda, oracle, monkeypatch, thr):
+@pytest.mark.parametrize("thr,ratio", [("1", "1000"), ("4", "1000"), ("1000", "1000"), ("1000", "0.5"), ("32", "2.5")])
+def test_split_layer_against_oracle(cuda, oracle, monkeypatch, thr, ratio):
     import bmx
     from bmx import synth
     c = synth.CONFIGS["c2"]
@@ -87,7 +98,8 @@ def test_split_layer_against_oracle(cuda, oracle, monkeypatch, thr):
     w = (np.random.default_rng(74).random((T, c["topk"])) * 0.5 + 0.1).astype(np.float16)
     layer = bmx.MoELayer(tab, c["topk"], score=c["score"], renorm=c["renorm"], scale=c["scale"])
     monkeypatch.setenv("BMX_SPLIT_MIN_ROWS", thr)
-    say("split layer vs oracle, threshold", thr)
+    monkeypatch.setenv("BMX_SPLIT_RATIO", ratio)
+    say("split layer vs oracle, threshold", thr, "ratio", ratio)
     out = layer.run_bszN(x, torch.from_numpy(sel).to(cuda), torch.from_numpy(w).to(cuda), bmx.PATH_SPLIT).cpu().numpy()
     rows = [0, 3, 11]
     used = sorted(set(int(e) for e in sel[rows].ravel()))
@@ -102,9 +114,10 @@ def test_split_layer_against_oracle(cuda, oracle, monkeypatch, thr):
     assert err < MAX_ABS and rel < REL_RMS
 
 
-def test_split_path_with_slot_table_stages(cuda):
+def test_split_path_with_slot_table_stages(cuda, monkeypatch):
     """A slot-table layer call of 16 tokens (AUTO: the split path) computes the resident experts' gate / up first and the
-    admitted ones after their copies, on both kernels: outputs bit-identical to the same layer fully resident."""
+    admitted ones after their copies, on both kernels (the per-expert rule at 4 rows: experts 3 and 7 and the ones
+    that happen to reach 4 rows on the mid-size kernel): outputs bit-identical to the same layer fully resident."""
     import bmx
     from bmx import synth
     from test_gpu_slots import small_layers
@@ -116,6 +129,8 @@ def test_split_path_with_slot_table_stages(cuda):
     st = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(2)]
     rf = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(2)]
     assert bmx.lib().bmx_resolve_path(T, topk, bmx.PATH_AUTO) == bmx.PATH_SPLIT
+    monkeypatch.setenv("BMX_SPLIT_MIN_ROWS", "4")
+    monkeypatch.setenv("BMX_SPLIT_RATIO", "1000")
     for step in range(6):
         li = step % 2
         x = torch.from_numpy(np.random.default_rng(90 + step).standard_normal((T, H)).astype(np.float16)).cuda()
