@@ -385,4 +385,44 @@ __device__ __forceinline__ float act_gate(int act, int gated, float g, float u, 
     return __fmul_rn(x, u);
 }
 
+// The same activations evaluated with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each; exp(x)
+// as exp2(x log2 e)) instead of the fixed sequence and correctly rounded divisions: for the prefill path, whose rows
+// no host lane replays. The results differ from act_gate's in the last bits of fp32, before the epilogue's rotation and
+// its single fp16 rounding.
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
+
+__device__ __forceinline__ float act_gate_fast(int act, int gated, float g, float u, float limit)
+{
+    if (act == BMX_ACT_SILU_OAI)
+    {
+        if (limit != 0.0f)
+        {
+            g = fminf(g, limit);
+            u = fminf(fmaxf(u, -limit), limit);
+        }
+        const float glu = g * rcp_hw(1.0f + exp_hw(-1.702f * g));
+        return (u + 1.0f) * glu;
+    }
+    float x;
+    if (!gated) x = fmaxf(0.0f, u);
+    else if (act == BMX_ACT_SILU) x = g * rcp_hw(1.0f + exp_hw(-g));
+    else if (act == BMX_ACT_GELU)
+    {
+        const float t = 0.797884560803f * (g + 0.044715f * g * g * g);
+        x = (0.5f * g) * (1.0f - 2.0f * rcp_hw(exp_hw(2.0f * t) + 1.0f));
+    }
+    else
+    {
+        x = fmaxf(0.0f, g);
+        x = x * x;
+    }
+    if (limit != 0.0f)
+    {
+        u = fminf(fmaxf(u, -limit), limit);
+        x = fminf(x, limit);
+    }
+    return x * u;
+}
+
 }  // namespace bmx

@@ -404,7 +404,8 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     for (int i = 0; i < 8; ++i)
     {
         const float gi = (g[i] * R_SCALE) * svg[i], ui = (v[i] * R_SCALE) * svu[i];
-        act[i] = act_gate(a.act, a.gated, gi, ui, a.limit) * sud[i];
+        act[i] = (a.fast_act ? act_gate_fast(a.act, a.gated, gi, ui, a.limit) : act_gate(a.act, a.gated, gi, ui, a.limit)) *
+                 sud[i];
     }
     had128_x8(act);
 #pragma unroll

@@ -36,6 +36,7 @@ struct GvArgs {
                                // epilogue's own rounding of that split's sum (RN of 0.0f + product): same bits downstream
     const uint16_t* sh_gate;   // fp16 [H] or null: the shared expert's output is scaled by sigmoid(x[t] . sh_gate)
     int pf_pairs = 0;          // prefill: two consecutive 128-row groups of one expert run as one 256-row tile
+    int fast_act = 0;          // prefill: the gate / up epilogue's activation by act_gate_fast (hardware exp2 / rcp)
     // split path (split_min > 0): an expert is heavy when the call averages at least split_ratio2 / 2 rows per expert
     // (every expert then is), or when it has at least split_min rows itself. Heavy experts run on the mid-size MFMA
     // kernel, in units of up to 32 rows (split_chunks per expert, taken over the unique experts uexp[0 .. *nuniq)), the

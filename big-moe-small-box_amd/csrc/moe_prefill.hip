@@ -701,6 +701,13 @@ static bool prefill_pairs_allowed()
     return !(v && *v == '0');
 }
 
+// BMX_PF_FAST_ACT=0: the prefill path's epilogue keeps the fixed-sequence activation of the decode path
+static bool prefill_fast_act()
+{
+    const char* v = getenv("BMX_PF_FAST_ACT");
+    return !(v && *v == '0');
+}
+
 // ---- mid-size path ------------------------------------------------------------------------------------------------------
 struct MidPlan {
     int NB, NBH, G_max, R_max, KS_gu, KS_dn;
@@ -864,6 +871,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.act_in_down = 0;
     a.gu_half = 1;
     a.pf_pairs = prefill_pairs_allowed() ? 1 : 0;
+    a.fast_act = prefill_fast_act() ? 1 : 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
         hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);

@@ -53,7 +53,8 @@ def make_layer(cfg, E, cuda):
 
 
 @pytest.mark.parametrize("cfg,E,T1,T2,path", [("c2", 288, 8, 1, 0), ("c2", 64, 16, 3, 3), ("c5", 64, 16, 2, 3),
-                                              ("c1", 64, 4, 1, 1), ("c3", 64, 24, 5, 2)])
+                                              ("c1", 64, 4, 1, 1), ("c3", 64, 24, 5, 2), ("c5", 384, 16, 2, 0),
+                                              ("c2", 288, 20, 16, 4)])
 def test_scratch_layer_matches_workspace_layer(cuda, cfg, E, T1, T2, path):
     from bmx import synth
     layer = make_layer(cfg, E, cuda)
