@@ -792,10 +792,9 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         traffic_src = (f"loaded from the committed profiles/{kind}_{cfg}_t{T}.json ({tr.get('measured', 'date not recorded')}"
                        f"; command in profiles/{kind}_{cfg}_t{T}.md): rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the "
                        f"same workload, scaled by a plain copy's counters; not measured in this run")
-    if prefill or mid:
+    if prefill:
         ach = gu_flops / (gu_ms * 1e-3) / 1e12
-        kern = ("k_pf_gemm<false> (BMX_STAGE_GATE_UP: trellis decode + gate/up MFMA grouped GEMM, 128-row groups)" if prefill
-                else "k_mid_gemm<false> (BMX_STAGE_GATE_UP: trellis decode + gate/up MFMA in 32-row groups, k-split)")
+        kern = "k_pf_gemm<false> (BMX_STAGE_GATE_UP: trellis decode + gate/up MFMA grouped GEMM, 128-row groups)"
         roofline = {"kernel": kern, "bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(ach / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": traffic,
                     "algorithmic_flops": gu_flops, "kernel_us": round(gu_ms * 1e3, 3), "traffic_source": traffic_src,
@@ -810,6 +809,8 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
         kern = ("k_gemv_gu_route (BMX_STAGE_GATE_UP of the one-token layer call: routing + dispatch of the token, "
                 "then trellis decode + gate/up split-K GEMV)" if fused_route
+                else "k_mid_gemm<false> (BMX_STAGE_GATE_UP of the mid-size path: trellis decode + gate/up MFMA in 32-row "
+                     "groups, k-split; a decode-size call, so the roofline is the quantized bytes against HBM)" if mid
                 else "k_gemv_part<gate/up> + k_mid_gemm<false> (BMX_STAGE_GATE_UP of the split path: the GEMV over the "
                      "experts with few rows, then the MFMA kernel over those with many; the two launches timed as one "
                      "stage)" if split
@@ -826,6 +827,10 @@ def bench_leg(leg, cfg, T, P, NT, args, with_cpu):
         if prof_us:
             roofline.update(kernel_us_rocprof=prof_us,
                             frac_rocprof=round(gu_bytes / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4))
+        if mid:
+            mf = gu_flops / (gu_ms * 1e-3) / 1e12
+            roofline.update(mfma_view={"achieved": round(mf, 2), "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(mf / MFMA_FP16_PEAK_TFLOPS, 4), "algorithmic_flops": gu_flops})
         if gu_sep_ms:
             sep = gu_bytes / (gu_sep_ms * 1e-3) / 1e9
             roofline.update(gemv_without_routing={

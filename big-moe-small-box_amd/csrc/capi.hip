@@ -97,8 +97,8 @@ static bmx_routes routes_at(char* base, const RoutesLayout& L)
 
 constexpr int STAGES_LAYER = (1 << BMX_STAGE_PREP) | (1 << BMX_STAGE_GATE_UP) | (1 << BMX_STAGE_ACT) | (1 << BMX_STAGE_DOWN) | (1 << BMX_STAGE_COMBINE);
 
-// AUTO: the GEMV path below BMX_MID_MIN_ROWS routed rows (T * topk), the mid-size MFMA path below
-// BMX_PREFILL_MIN_ROWS, the prefill MFMA path from there up
+// AUTO: the GEMV path below BMX_MID_MIN_TOKENS tokens, the mid-size MFMA path below BMX_PREFILL_MIN_ROWS routed rows
+// (T * topk), the prefill MFMA path from there up
 static long env_rows(const char* name, long dflt)
 {
     const char* v = getenv(name);
@@ -112,9 +112,12 @@ static bool route_in_gemv_allowed()
     return !(v && *v == '0');
 }
 
-// AUTO below the prefill and mid-size thresholds: the split path (the GEMV or the mid-size GEMMs, chosen on the device
-// from the call's rows per expert) from BMX_SPLIT_MIN_TOKENS tokens, the GEMV path below (at 8 tokens the split path's
-// idle launches cost 3 % of the GLM-shaped layer, and few rows per expert are the rule there)
+// AUTO below the prefill threshold: the mid-size MFMA path from BMX_MID_MIN_TOKENS tokens (8), the GEMV path below.
+// Measured on MI355X (layer us, GEMV / mid-size): GLM-shaped (H 4096, I 1536) T 4 135 / 146, T 6 196 / 190, T 8 234 /
+// 219, T 16 354 / 316, T 32 533 / 432; DeepSeek-shaped (H 4096, I 2048, Zipf routing) T 6 165 / 168, T 8 201 / 193,
+// T 32 524 / 450; 16 tokens on ~10 experts 180 / 107; the 64-expert H 2048 layer crosses over later (T 8 72 / 83, T 16
+// 98 / 94). The split path (BMX_PATH_SPLIT) is never chosen here: the mid-size path alone is faster wherever the split
+// path would send a call to the MFMA kernels.
 static int resolve_path(int path, int T, int topk)
 {
     if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL || path == BMX_PATH_MID || path == BMX_PATH_SPLIT)
@@ -122,8 +125,7 @@ static int resolve_path(int path, int T, int topk)
     if (path != BMX_PATH_AUTO) return -1;
     const long rows = (long)T * topk;
     if (rows >= env_rows("BMX_PREFILL_MIN_ROWS", 512)) return BMX_PATH_PREFILL;
-    if (rows >= env_rows("BMX_MID_MIN_ROWS", 1L << 30)) return BMX_PATH_MID;
-    if (T >= env_rows("BMX_SPLIT_MIN_TOKENS", 16)) return BMX_PATH_SPLIT;
+    if (T >= env_rows("BMX_MID_MIN_TOKENS", 8)) return BMX_PATH_MID;
     return BMX_PATH_DECODE;
 }
 

@@ -78,13 +78,21 @@ __device__ __forceinline__ void step_barrier()
 // 32 nb + L % 32 as 4 dwords (rows 2d, 2d + 1 in dword d). Stream positions 32 HALF .. 32 HALF + 31 of a lane's strip are
 // columns HALF and HALF + 2 of its four, all 16 rows: two columns' worth of fragments. col0: the first column of the
 // lane's 128-column half of the block.
+// The lane index as a value the compiler cannot hoist: LDS addresses derived from it are recomputed where they are used
+// (a few VALU per step) instead of being kept live across the k-loop, which costs the mid-size kernel its occupancy.
+__device__ __forceinline__ int fresh_lane()
+{
+    int l = threadIdx.x & 63;
+    asm volatile("" : "+v"(l));
+    return l;
+}
+
 template <int F, int HALF>
 __device__ __forceinline__ void decode_half(const uint32_t (&own)[Fmt<F>::TB / 16], u32x4* __restrict__ stage, int kt,
-                                            int col0)
+                                            int col0, int lane)
 {
     constexpr int NW = Fmt<F>::TB / 16;
     constexpr RingTab<F> tab;
-    const int lane = threadIdx.x & 63;
     // every word of the window is consumed here (a half strip reads only some of them): keeps the prefetched registers
     // allocated until now instead of reused while their load is in flight, which would force a wait on it
 #pragma unroll
@@ -282,7 +290,7 @@ __device__ __forceinline__ void pf_decoder(const PfJob& jb, const uint8_t* mat_b
     auto ak = [&](int step) { return 64 * min(step, KT - 1); };
     auto dec = [&](const uint32_t (&w)[NW], u32x4* stage) {
         if constexpr (PAIR) decode_quarter<F, HALF, SUB>(w, stage, kt, 0);
-        else decode_half<F, HALF>(w, stage, kt, 128 * th);
+        else decode_half<F, HALF>(w, stage, kt, 128 * th, threadIdx.x & 63);
     };
     auto fetch = [&](PfArow (&a)[NA], int step) {
 #pragma unroll
@@ -500,18 +508,19 @@ __device__ __forceinline__ void mid_a_fetch(MidArow& r, const uint16_t* rowp, in
     r.d[1] = ldg(p, 1);
 }
 
-__device__ __forceinline__ void mid_a_store(const MidArow& r, u32x4* __restrict__ stage)
+__device__ __forceinline__ void mid_a_store(const MidArow& r, u32x4* __restrict__ stage, int lane)
 {
-    const int lane = threadIdx.x & 63, row = 4 * (threadIdx.x >> 6) + (lane >> 4), piece = lane & 15;
+    const int row = 4 * (threadIdx.x >> 6) + (lane >> 4), piece = lane & 15;
     uint2* p = reinterpret_cast<uint2*>(stage + row * 8 + ((piece >> 1) ^ ((row >> 1) & 7))) + (piece & 1);
     *p = make_uint2(r.d[0], r.d[1]);
 }
 
-// the wave's 32-column block of one step: 4 MFMAs, k 16 each, alternating between two accumulators
-__device__ __forceinline__ void mid_mfma_step(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, f32x16& acc0,
-                                              f32x16& acc1)
+// the wave's 32-column block of one step: 4 MFMAs, k 16 each, into one accumulator (the MFMA units are lightly used
+// here; a second accumulator would cost the 16 VGPRs that keep the kernel at 128)
+__device__ __forceinline__ void mid_mfma_step(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, f32x16& acc,
+                                              int lane)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6;
     f16x8 fa[4], fb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -520,16 +529,14 @@ __device__ __forceinline__ void mid_mfma_step(const u32x4* __restrict__ sa, cons
         fa[ks] = __builtin_bit_cast(f16x8, sa[(lane & 31) * 8 + slot]);
         fb[ks] = __builtin_bit_cast(f16x8, sb[fi * 64 + bsw(fi, lane)]);
     }
-    acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[0], fb[0], acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1], fb[1], acc1, 0, 0, 0);
-    acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[2], fb[2], acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[3], fb[3], acc1, 0, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks], fb[ks], acc, 0, 0, 0);
 }
 
 // steps s0 .. s0 + n - 1 of the unit; straight-line like pf_decoder (loads past the last step re-read it)
 template <int F, int HALF>
 __device__ __forceinline__ void mid_run(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int s0, int n,
-                                        f32x16& acc0, f32x16& acc1)
+                                        f32x16& acc)
 {
     constexpr int TB = Fmt<F>::TB, NW = TB / 16;
     const int lane = threadIdx.x & 63, d = threadIdx.x >> 6;
@@ -542,49 +549,44 @@ __device__ __forceinline__ void mid_run(const PfJob& jb, const uint8_t* mat_base
     const uint16_t* rowp = asrc + (size_t)(jb.r0 + min(arow, jb.nr - 1)) * jb.K + 4 * (lane & 15);
     auto wp = [&](int i) { return p + (size_t)(s0 + min(i, n - 1)) * step_bytes; };
     auto ak = [&](int i) { return 64 * (s0 + min(i, n - 1)); };
-    uint32_t w0[NW], w1[NW], w2[NW];
-    MidArow a0, a1, a2;
+    // the lane index once per call, opaque to the compiler: the LDS addresses derived from it are this copy's own (the
+    // compiler cannot merge them above the format switch, where every copy's set would be live at once)
+    const int ln = fresh_lane();
+    uint32_t w0[NW], w1[NW];
+    MidArow a0, a1;
     mid_a_fetch(a0, rowp, ak(0));
     mid_a_fetch(a1, rowp, ak(1));
-    mid_a_fetch(a2, rowp, ak(2));
     load_words(w0, wp(0));
     load_words(w1, wp(1));
-    load_words(w2, wp(2));
-    decode_half<F, HALF>(w0, pf_b0, kt, 128 * th);
-    mid_a_store(a0, mid_a0);
+    decode_half<F, HALF>(w0, pf_b0, kt, 128 * th, ln);
+    mid_a_store(a0, mid_a0, ln);
     step_barrier();
-    // step i: the MFMAs of stage i % 2, the decode of step i + 1 into the other stage, the fetch of step i + 3
-    for (int i = 0; i < n; i += 3)
+    // step i: the MFMAs of stage i % 2, the decode of step i + 1 into the other stage, the fetch of step i + 2 (two
+    // register sets: the kernel fits 128 VGPRs, so two workgroups share a CU)
+    for (int i = 0; i < n; i += 2)
     {
-        mid_a_fetch(a0, rowp, ak(i + 3));
-        load_words(w0, wp(i + 3));
-        mid_mfma_step(mid_a_stage(i & 1), b_stage(i & 1), acc0, acc1);
-        decode_half<F, HALF>(w1, b_stage((i + 1) & 1), kt, 128 * th);
-        mid_a_store(a1, mid_a_stage((i + 1) & 1));
+        mid_a_fetch(a0, rowp, ak(i + 2));
+        load_words(w0, wp(i + 2));
+        mid_mfma_step(mid_a0, pf_b0, acc, ln);
+        decode_half<F, HALF>(w1, pf_b1, kt, 128 * th, ln);
+        mid_a_store(a1, mid_a1, ln);
         step_barrier();
         if (i + 1 >= n) break;
-        mid_a_fetch(a1, rowp, ak(i + 4));
-        load_words(w1, wp(i + 4));
-        mid_mfma_step(mid_a_stage((i + 1) & 1), b_stage((i + 1) & 1), acc0, acc1);
-        decode_half<F, HALF>(w2, b_stage(i & 1), kt, 128 * th);
-        mid_a_store(a2, mid_a_stage(i & 1));
-        step_barrier();
-        if (i + 2 >= n) break;
-        mid_a_fetch(a2, rowp, ak(i + 5));
-        load_words(w2, wp(i + 5));
-        mid_mfma_step(mid_a_stage(i & 1), b_stage(i & 1), acc0, acc1);
-        decode_half<F, HALF>(w0, b_stage((i + 1) & 1), kt, 128 * th);
-        mid_a_store(a0, mid_a_stage((i + 1) & 1));
+        mid_a_fetch(a1, rowp, ak(i + 3));
+        load_words(w1, wp(i + 3));
+        mid_mfma_step(mid_a1, pf_b1, acc, ln);
+        decode_half<F, HALF>(w0, pf_b0, kt, 128 * th, ln);
+        mid_a_store(a0, mid_a0, ln);
         step_barrier();
     }
 }
 
 template <int F>
 __device__ __forceinline__ void mid_run_any(const PfJob& jb, const uint8_t* mat_base, const uint16_t* asrc, int s0, int n,
-                                            f32x16& acc0, f32x16& acc1)
+                                            f32x16& acc)
 {
-    if ((threadIdx.x >> 6) & 1) mid_run<F, 1>(jb, mat_base, asrc, s0, n, acc0, acc1);
-    else mid_run<F, 0>(jb, mat_base, asrc, s0, n, acc0, acc1);
+    if ((threadIdx.x >> 6) & 1) mid_run<F, 1>(jb, mat_base, asrc, s0, n, acc);
+    else mid_run<F, 0>(jb, mat_base, asrc, s0, n, acc);
 }
 
 // One unit of the mid-size GEMM: (group or heavy-expert chunk, matrix, 256-column block, k-split) from its index lid.
@@ -625,33 +627,34 @@ __device__ __forceinline__ void mid_unit(const GvArgs& a, int lid)
     const int n = jb.K / 64 / KS, s0 = ksp * n;
     const uint16_t* asrc = DOWN ? a.act_rows : a.xt + (size_t)jb.mat * a.R_max * a.H;
     const uint8_t* base = reinterpret_cast<const uint8_t*>(jb.ex->tr[jb.mat]);
-    f32x16 acc0 = f32x16{}, acc1 = f32x16{};
+    f32x16 acc = f32x16{};
     switch (jb.ex->fmt[jb.mat])
     {
-        case BMX_TF_K2: mid_run_any<BMX_TF_K2>(jb, base, asrc, s0, n, acc0, acc1); break;
-        case BMX_TF_K25: mid_run_any<BMX_TF_K25>(jb, base, asrc, s0, n, acc0, acc1); break;
-        case BMX_TF_K3: mid_run_any<BMX_TF_K3>(jb, base, asrc, s0, n, acc0, acc1); break;
-        default: mid_run_any<BMX_TF_K4>(jb, base, asrc, s0, n, acc0, acc1); break;
+        case BMX_TF_K2: mid_run_any<BMX_TF_K2>(jb, base, asrc, s0, n, acc); break;
+        case BMX_TF_K25: mid_run_any<BMX_TF_K25>(jb, base, asrc, s0, n, acc); break;
+        case BMX_TF_K3: mid_run_any<BMX_TF_K3>(jb, base, asrc, s0, n, acc); break;
+        default: mid_run_any<BMX_TF_K4>(jb, base, asrc, s0, n, acc); break;
     }
     // accumulator element v of lane L: row 8 (v / 4) + 4 (L / 32) + v % 4, column L % 32 of the wave's 32-column block
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int cbo = 2 * jb.cb + (wave >> 2);
     if (cbo >= nb128) return;
     const int col = 32 * (wave & 3) + (lane & 31);
+    // row stride of the partial layout (floats); the lane's first row 4 (lane / 32)
+    const int rs = DOWN ? a.NBH * 128 : a.NB * 256;
+    const size_t r0 = (size_t)ksp * a.R_max + jb.r0 + 4 * (lane >> 5);
+    float* out = (DOWN ? a.part_dn + cbo * 128 : a.part_gu + cbo * 256 + jb.mat * 128) + r0 * rs + col;
 #pragma unroll
     for (int v = 0; v < 16; ++v)
     {
-        const int row = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row >= jb.nr) continue;
-        const size_t r = (size_t)ksp * a.R_max + jb.r0 + row;
-        const float y = acc0[v] + acc1[v];
-        if (DOWN) a.part_dn[(r * a.NBH + cbo) * 128 + col] = y;
-        else a.part_gu[(r * a.NB + cbo) * 256 + jb.mat * 128 + col] = y;
+        const int dr = 8 * (v >> 2) + (v & 3);
+        if (dr + 4 * (lane >> 5) >= jb.nr) continue;
+        out[(size_t)dr * rs] = acc[v];
     }
 }
 
 template <bool DOWN>
-__global__ __launch_bounds__(MID_WAVES * 64) void k_mid_gemm(GvArgs a)
+__global__ __launch_bounds__(MID_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_mid_gemm(GvArgs a)
 {
     if (!a.split_min)
     {
@@ -714,11 +717,14 @@ struct MidPlan {
     size_t xt_bytes, part_gu_bytes, act_bytes, part_dn_bytes;
 };
 
-// k-split: the most splits that keep at least 16 k-steps each (BMX_MID_MIN_STEPS) (the routing, unknown here, may put all rows
-// on a few experts; splits keep the workgroup count up then, at the price of partial sums the epilogue adds)
-static int mid_split(int ksteps)
+// k-split: the most splits that keep at least 16 k-steps each, gate / up (BMX_MID_MIN_STEPS) and down
+// (BMX_MID_MIN_STEPS_DN) (the routing, unknown here, may put all rows on a few experts; splits keep the workgroup count
+// up then, at the price of partial sums the epilogue adds). Measured (layer us; 8 / 16 / 32 steps for down): 16 tokens
+// on ~10 experts of H 4096, I 2048: 103.7 / 104.4 / 106.6; GLM-shaped 8 tokens: 218 / 214 / 214; DeepSeek-shaped 16
+// tokens: 298 / 292 / 295. Gate / up at 8 or 32 steps: 5-7 % slower than 16 on the first.
+static int mid_split(int ksteps, bool down)
 {
-    const char* v = getenv("BMX_MID_MIN_STEPS");
+    const char* v = getenv(down ? "BMX_MID_MIN_STEPS_DN" : "BMX_MID_MIN_STEPS");
     const int min_steps = (v && *v) ? atoi(v) : 16;
     for (int d = ksteps; d > 1; --d)
         if (ksteps % d == 0 && ksteps / d >= min_steps) return d;
@@ -732,8 +738,8 @@ static MidPlan mid_plan(const MoeShape& m)
     p.NBH = m.H / 128;
     p.G_max = groups_max(m.T, m.topk, m.E, m.shared, MID_M);
     p.R_max = m.T * m.topk + (m.shared ? m.T : 0);
-    p.KS_gu = mid_split(m.H / 64);
-    p.KS_dn = mid_split(m.I / 64);
+    p.KS_gu = mid_split(m.H / 64, false);
+    p.KS_dn = mid_split(m.I / 64, true);
     p.xt_bytes = (size_t)2 * p.R_max * m.H * 2;
     p.part_gu_bytes = (size_t)p.KS_gu * p.R_max * p.NB * 256 * 4;
     p.act_bytes = (size_t)p.R_max * m.I * 2;

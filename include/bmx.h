@@ -49,9 +49,9 @@ enum bmx_act { BMX_ACT_SILU = 0, BMX_ACT_GELU = 1, BMX_ACT_RELU2 = 2, BMX_ACT_SI
  * prefill call, engine/tiers.py:673-700), MID = grouped GEMMs on MFMA in groups of 32 rows with k-splits (decode batches
  * of several tokens per expert), SPLIT = the DECODE or the MID kernels chosen on the device from the dispatch: every
  * expert on the MID kernels when the call has at least BMX_SPLIT_RATIO rows per unique expert (default 2.5), else on the
- * DECODE GEMVs except experts with at least BMX_SPLIT_MIN_ROWS rows (default 32). AUTO picks PREFILL from
- * BMX_PREFILL_MIN_ROWS routed rows (T * topk; default 512), MID from BMX_MID_MIN_ROWS, SPLIT from BMX_SPLIT_MIN_TOKENS
- * tokens (default 16; environment variables), DECODE below. */
+ * DECODE GEMVs except experts with at least BMX_SPLIT_MIN_ROWS rows (default off). AUTO picks PREFILL from
+ * BMX_PREFILL_MIN_ROWS routed rows (T * topk; default 512), MID from BMX_MID_MIN_TOKENS tokens (default 8; environment
+ * variables), DECODE below; never SPLIT. */
 enum bmx_path { BMX_PATH_AUTO = 0, BMX_PATH_DECODE = 1, BMX_PATH_PREFILL = 2, BMX_PATH_MID = 3, BMX_PATH_SPLIT = 4 };
 
 /* One expert: three EXL3 linears (gate [H->I], up [H->I], down [I->H]). Device-resident array, one entry per expert.
@@ -196,7 +196,8 @@ int bmx_moe_layer_scratch(const bmx_moe_desc* desc, const bmx_router_desc* route
 
 /* Expert products only, on given routes (from bmx_dispatch with rows_per_group = bmx_rows_per_group(T, topk, path)):
  * y_rows fp32 [R, H] (expert output of each dispatch row), act_rows fp16 [R, I] (the rotated down input) or NULL.
- * bmx_resolve_path: the path (DECODE or PREFILL) that `path` selects for T tokens of topk picks, -1 if invalid. */
+ * bmx_resolve_path: the path (DECODE, PREFILL, MID or SPLIT) that `path` selects for T tokens of topk picks, -1 if
+ * invalid. */
 int bmx_rows_per_group(int T, int topk, int path);
 int bmx_resolve_path(int T, int topk, int path);
 size_t bmx_experts_workspace(const bmx_moe_desc* desc, int T, int path);

@@ -114,10 +114,12 @@ def test_split_layer_against_oracle(cuda, oracle, monkeypatch, thr, ratio):
     assert err < MAX_ABS and rel < REL_RMS
 
 
-def test_split_path_with_slot_table_stages(cuda, monkeypatch):
-    """A slot-table layer call of 16 tokens (AUTO: the split path) computes the resident experts' gate / up first and the
-    admitted ones after their copies, on both kernels (the per-expert rule at 4 rows: experts 3 and 7 and the ones
-    that happen to reach 4 rows on the mid-size kernel): outputs bit-identical to the same layer fully resident."""
+@pytest.mark.parametrize("path_name", ["split", "auto"])
+def test_split_path_with_slot_table_stages(cuda, monkeypatch, path_name):
+    """A slot-table layer call of 16 tokens computes the resident experts' gate / up first and the admitted ones after
+    their copies: on the split path on both kernels (the per-expert rule at 4 rows: experts 3 and 7 and the ones that
+    happen to reach 4 rows on the mid-size kernel), on AUTO (the mid-size path at 16 tokens) on the MFMA kernels alone;
+    outputs bit-identical to the same layer fully resident."""
     import bmx
     from bmx import synth
     from test_gpu_slots import small_layers
@@ -128,9 +130,11 @@ def test_split_path_with_slot_table_stages(cuda, monkeypatch):
     kw = dict(score=bmx.SCORE_SIGMOID, renorm=True, scale=1.0)
     st = [bmx.MoELayer(host_layers[li], topk, slots=slots, li=li, **kw) for li in range(2)]
     rf = [bmx.MoELayer(dev_layers[li], topk, **kw) for li in range(2)]
-    assert bmx.lib().bmx_resolve_path(T, topk, bmx.PATH_AUTO) == bmx.PATH_SPLIT
     monkeypatch.setenv("BMX_SPLIT_MIN_ROWS", "4")
     monkeypatch.setenv("BMX_SPLIT_RATIO", "1000")
+    path = bmx.PATH_SPLIT if path_name == "split" else bmx.PATH_AUTO
+    if path_name == "auto":
+        assert bmx.lib().bmx_resolve_path(T, topk, path) == bmx.PATH_MID
     for step in range(6):
         li = step % 2
         x = torch.from_numpy(np.random.default_rng(90 + step).standard_normal((T, H)).astype(np.float16)).cuda()
@@ -138,8 +142,8 @@ def test_split_path_with_slot_table_stages(cuda, monkeypatch):
         w = torch.from_numpy((np.random.default_rng(99 + step).random((T, topk)) + 0.2).astype(np.float16)).cuda()
         m = st[li]
         sg, wg, _ = m.layer(li, sel, w, x, T)
-        out = m.run_bszN(x, sg, wg)
-        want = rf[li].run_bszN(x, sel, w)
+        out = m.run_bszN(x, sg, wg, path)
+        want = rf[li].run_bszN(x, sel, w, path)
         torch.cuda.synchronize()
-        say("split slot-table step", step, "layer", li, "max diff", float((out - want).abs().max()))
+        say(path_name, "slot-table step", step, "layer", li, "max diff", float((out - want).abs().max()))
         assert torch.equal(out.view(torch.int32), want.view(torch.int32)), step
