@@ -116,15 +116,16 @@ static bool route_in_gemv_allowed()
 // Measured on MI355X (layer us, GEMV / mid-size): GLM-shaped (H 4096, I 1536) T 4 135 / 146, T 6 196 / 190, T 8 234 /
 // 219, T 16 354 / 316, T 32 533 / 432; DeepSeek-shaped (H 4096, I 2048, Zipf routing) T 6 165 / 168, T 8 201 / 193,
 // T 32 524 / 450; 16 tokens on ~10 experts 180 / 107; the 64-expert H 2048 layer crosses over later (T 8 72 / 83, T 16
-// 98 / 94). The split path (BMX_PATH_SPLIT) is never chosen here: the mid-size path alone is faster wherever the split
-// path would send a call to the MFMA kernels.
+// 98 / 94). Mid-size / prefill (128-row groups): DeepSeek-shaped T 86 (516 rows) 819 / 917, T 256 1426 / 1519, T 512
+// 1911 / 1883, T 2048 3546 / 2627; GLM-shaped T 64 554 / 661, T 128 680 / 771. The split path (BMX_PATH_SPLIT) is never
+// chosen here: the mid-size path alone is faster wherever the split path would send a call to the MFMA kernels.
 static int resolve_path(int path, int T, int topk)
 {
     if (path == BMX_PATH_DECODE || path == BMX_PATH_PREFILL || path == BMX_PATH_MID || path == BMX_PATH_SPLIT)
         return path;
     if (path != BMX_PATH_AUTO) return -1;
     const long rows = (long)T * topk;
-    if (rows >= env_rows("BMX_PREFILL_MIN_ROWS", 512)) return BMX_PATH_PREFILL;
+    if (rows >= env_rows("BMX_PREFILL_MIN_ROWS", 2048)) return BMX_PATH_PREFILL;
     if (T >= env_rows("BMX_MID_MIN_TOKENS", 8)) return BMX_PATH_MID;
     return BMX_PATH_DECODE;
 }

@@ -50,7 +50,7 @@ enum bmx_act { BMX_ACT_SILU = 0, BMX_ACT_GELU = 1, BMX_ACT_RELU2 = 2, BMX_ACT_SI
  * of several tokens per expert), SPLIT = the DECODE or the MID kernels chosen on the device from the dispatch: every
  * expert on the MID kernels when the call has at least BMX_SPLIT_RATIO rows per unique expert (default 2.5), else on the
  * DECODE GEMVs except experts with at least BMX_SPLIT_MIN_ROWS rows (default off). AUTO picks PREFILL from
- * BMX_PREFILL_MIN_ROWS routed rows (T * topk; default 512), MID from BMX_MID_MIN_TOKENS tokens (default 8; environment
+ * BMX_PREFILL_MIN_ROWS routed rows (T * topk; default 2048), MID from BMX_MID_MIN_TOKENS tokens (default 8; environment
  * variables), DECODE below; never SPLIT. */
 enum bmx_path { BMX_PATH_AUTO = 0, BMX_PATH_DECODE = 1, BMX_PATH_PREFILL = 2, BMX_PATH_MID = 3, BMX_PATH_SPLIT = 4 };
 

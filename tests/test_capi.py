@@ -46,8 +46,8 @@ def test_host_side_checks():
     assert L.bmx_moe_forward(ctypes.byref(d), None, 1, None, None, None, None, 0, 0, None) == bmx._lib.BMX_ERR_ARG
     assert b"multiples of 128" in L.bmx_last_error()
     assert L.bmx_rows_per_group(1, 8, 0) == 1 and L.bmx_rows_per_group(3, 8, 0) == 4 and L.bmx_rows_per_group(60, 8, 0) == 32
-    assert L.bmx_rows_per_group(64, 8, 0) == 128 and L.bmx_rows_per_group(64, 8, 1) == 8 and L.bmx_rows_per_group(1, 8, 2) == 128
-    assert L.bmx_resolve_path(63, 8, 0) == 3 and L.bmx_resolve_path(64, 8, 0) == 2 and L.bmx_resolve_path(1, 8, 2) == 2
+    assert L.bmx_rows_per_group(256, 8, 0) == 128 and L.bmx_rows_per_group(64, 8, 0) == 32 and L.bmx_rows_per_group(64, 8, 1) == 8 and L.bmx_rows_per_group(1, 8, 2) == 128
+    assert L.bmx_resolve_path(255, 8, 0) == 3 and L.bmx_resolve_path(256, 8, 0) == 2 and L.bmx_resolve_path(1, 8, 2) == 2
     # AUTO below the prefill rows: the mid-size path from 8 tokens, the GEMV path below; explicit paths kept
     assert L.bmx_resolve_path(15, 8, 0) == 3 and L.bmx_resolve_path(8, 8, 0) == 3 and L.bmx_resolve_path(16, 6, 0) == 3
     assert L.bmx_resolve_path(7, 8, 0) == 1 and L.bmx_resolve_path(1, 8, 0) == 1 and L.bmx_resolve_path(85, 6, 0) == 3

@@ -54,6 +54,9 @@ PF_LAYERS = [
     ("c1 T8 K4", "c1", 64, 8, None, None, None),
     ("c5 T16 K2/K2.5", "c5", 384, 16, None, None, [0, 7, 15]),
     ("odd blocks H384 I256", "c2", 8, 24, 384, 256, [0, 11, 23]),
+    # AUTO's path up to 2,048 routed rows: many 32-row groups per expert
+    ("c3 shape E64 T300", "c3", 64, 300, None, None, [0, 150, 299]),
+    ("c2 shared E48 T200", "c2", 48, 200, None, None, [0, 99, 199]),
 ]
 
 
@@ -162,6 +165,8 @@ def test_mid_layer_parity(cuda, oracle, name, cfgname, E, T, H, I, rows):
     fused = layer.forward(x, lg, path=MID).cpu().numpy()
     assert np.array_equal(fused, out)
     assert bmx.lib().bmx_rows_per_group(T, layer.num_experts_per_tok, MID) == 32
+    if T >= 8:
+        assert bmx.lib().bmx_resolve_path(T, layer.num_experts_per_tok, 0) == MID
     rows = list(range(T)) if rows is None else rows
     want = oracle_layer(oracle, tab, x.cpu().numpy(), sel.cpu().numpy(), w.cpu().numpy(), rows)
     got = out[rows]
