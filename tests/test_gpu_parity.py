@@ -408,14 +408,17 @@ def test_full_size_properties_c2_t8(cuda):
     s2[:, 3] = tab.E
     w2 = w.clone()
     w2[:, 3] = 0
-    # on the GEMV path every row is computed on its own: a dropped pick and a weight-0 pick give the same bits. AUTO takes
-    # the split path here, where a row's kernel follows its expert's row count, which the weight-0 pick still adds to:
-    # the other rows of that expert may move to the MFMA kernel, within the layer tolerance
-    a = bmx.ops.moe_forward(d, x, s2, w, bmx.PATH_DECODE)
-    b = bmx.ops.moe_forward(d, x, sel, w2, bmx.PATH_DECODE)
-    assert torch.equal(a, b) and not torch.equal(a, bmx.ops.moe_forward(d, x, sel, w, bmx.PATH_DECODE))
-    a2 = bmx.ops.moe_forward(d, x, s2, w)
-    b2 = bmx.ops.moe_forward(d, x, sel, w2)
+    # on the GEMV path and on the mid-size MFMA path (AUTO at 8 tokens) every row is computed on its own (an MFMA output
+    # row depends on its own input row only, in a fixed k order): a dropped pick and a weight-0 pick give the same bits.
+    # On the split path a row's kernel follows its expert's row count, which the weight-0 pick still adds to, so the other
+    # rows of that expert may move to the other kernel: within the layer tolerance there
+    assert bmx.lib().bmx_resolve_path(8, 8, bmx.PATH_AUTO) == bmx.PATH_MID
+    for path in (bmx.PATH_DECODE, bmx.PATH_AUTO):
+        a = bmx.ops.moe_forward(d, x, s2, w, path)
+        b = bmx.ops.moe_forward(d, x, sel, w2, path)
+        assert torch.equal(a, b) and not torch.equal(a, bmx.ops.moe_forward(d, x, sel, w, path)), path
+    a2 = bmx.ops.moe_forward(d, x, s2, w, bmx.PATH_SPLIT)
+    b2 = bmx.ops.moe_forward(d, x, sel, w2, bmx.PATH_SPLIT)
     assert float((a2 - b2).abs().max()) < 1e-2 and float((a2 - a).abs().max()) < 1e-2
     full = bmx.ops.moe_forward(tab.desc(8), x, sel, w)
     only_shared = bmx.ops.moe_forward(tab.desc(8), x, sel, torch.zeros_like(w))
