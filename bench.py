@@ -609,6 +609,7 @@ LEGS = {
     "c5": ("c5", 16, 16, 1),
     "prefill_staged": None,       # bench_staged: the c3 layer stack with its experts in pinned host memory
     "c4": None,                   # bench_c4: the 43-layer decode stack with the expert-slot table
+    "c4_cpu_lane": None,          # the same stack with the planner putting misses on a 12-thread CPU lane
 }
 HEADLINE_LEGS = ("decode", "prefill")
 
@@ -926,9 +927,12 @@ def main():
     results = []
     for leg in legs:
         name = leg[0]
-        if name == "c4":
-            r = bench_c4(args)
-            r = dict(r, leg="c4", ms=r["ms_per_step"], T=1)
+        if name in ("c4", "c4_cpu_lane"):
+            a4 = argparse.Namespace(**vars(args))
+            if name == "c4_cpu_lane" and not a4.cpu_lane:
+                a4.cpu_lane = 12
+            r = bench_c4(a4)
+            r = dict(r, leg=name, ms=r["ms_per_step"], T=1)
         elif name == "prefill_staged":
             pf = next((x for x in results if x["leg"] == "prefill"), None)
             cpu = None
