@@ -947,29 +947,41 @@ def main():
         results.append(r)
         torch.cuda.empty_cache()
     head = results[0]
-    res = {
-        "metric": METRIC,
-        "value": head["value"],
-        "unit": head["unit"],
-        "n_gpus": 1,
-        "steps": head["steps"],
-        "warmup": head["warmup"],
-        "ms_per_step": round(head["ms"], 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic: random EXL3 trellis codes, suh ~ U(0.5,1.5), svh ~ U(0.5,1.5)/sqrt(k), x ~ N(0,1) fp16 "
-                "(c5: 1 % of channels x20), router logits ~ N(0,1) fp16 (c3 / c5: Zipf(1.1) log-popularity + Gumbel "
-                "noise), bias ~ N(0,0.1); seeded; decode steps rotate over input batches (and c1 over layer tables) "
-                "so the experts read change every step (cold weights)",
-        "config": {"workload": head["workload"], "tokens": head["T"], "path": head["path"], "rotation": head["rotation"],
-                   "step": "router + dispatch + gate/up + down + combine (one bmx_moe_layer call)"},
-        "timing": "min of eager launches and HIP-graph replay of the same sequence of bmx_moe_layer calls",
-    }
-    for k in ("us_per_layer", "us_per_token", "us_per_layer_eager", "us_per_layer_graph", "quantized_bytes_per_layer",
-              "layer_hbm_gbps", "stage_us", "roofline", "cpu_baseline"):
-        res[k] = head[k]
+    if head["leg"] in ("c4", "c4_cpu_lane"):
+        # The stack leg's result is already a whole line of its own.
+        res = {k: v for k, v in head.items() if k not in ("leg", "ms", "T")}
+    else:
+        layer_call = "us_per_layer_graph" in head
+        res = {
+            "metric": METRIC,
+            "value": head["value"],
+            "unit": head["unit"],
+            "n_gpus": 1,
+            "steps": head["steps"],
+            "warmup": head["warmup"],
+            "ms_per_step": round(head["ms"], 6),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "fp16",
+            "data": "synthetic: random EXL3 trellis codes, suh ~ U(0.5,1.5), svh ~ U(0.5,1.5)/sqrt(k), x ~ N(0,1) fp16 "
+                    "(c5: 1 % of channels x20), router logits ~ N(0,1) fp16 (c3 / c5: Zipf(1.1) log-popularity + Gumbel "
+                    "noise), bias ~ N(0,0.1); seeded; decode steps rotate over input batches (and c1 over layer tables) "
+                    "so the experts read change every step (cold weights)",
+            "config": {"workload": head["workload"], "tokens": head["T"], "path": head["path"]},
+        }
+        if layer_call:
+            res["config"].update(rotation=head["rotation"],
+                                 step="router + dispatch + gate/up + down + combine (one bmx_moe_layer call)")
+            res["timing"] = "min of eager launches and HIP-graph replay of the same sequence of bmx_moe_layer calls"
+        else:
+            res["config"].update(layers=head["layers"], step="one chunk of tokens through every layer of the stack, "
+                                                             "experts staged from host memory one layer ahead")
+        for k in ("us_per_layer", "us_per_token", "us_per_layer_eager", "us_per_layer_graph", "quantized_bytes_per_layer",
+                  "layer_hbm_gbps", "stage_us", "ms_per_chunk", "staged_experts_per_layer", "staged_bytes_per_layer",
+                  "roofline", "cpu_baseline"):
+            if k in head:
+                res[k] = head[k]
     for r in results[1:]:
         r = dict(r)
         del r["ms"]
