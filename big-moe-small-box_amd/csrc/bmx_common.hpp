@@ -206,6 +206,42 @@ __device__ __forceinline__ void had128_wave(float& v0, float& v1)
     v1 = __builtin_fmaf(s32, v1, xor32_f(v1));
 }
 
+// had128_x8: the 16-lane form. Spans 1, 2, 4 inside the lane as above; at spans 8, 16, 32, 64 both lanes of a pair
+// compute fma(partner, s, own), s = +1 on the lower lane and -1 on the upper one, with the partner read through DPP in
+// the same instruction (v_fmac_f32_dpp): a + b on the lower lane, b - a on the upper, where the reference has a - b.
+// RN(b - a) = -RN(a - b) exactly, and a sign carried into a later stage is common to both lanes of its pair (they differ
+// only in that stage's bit), so it factors out: every output is the reference's value times had128_x8_sign(), which
+// is (-1)^popcount(j & 15) for lane j. Callers fold that sign into their next multiply (sign flips are exact, so the
+// products carry the reference's bits).
+__device__ __forceinline__ float had128_x8_sign()
+{
+    return (__builtin_popcount(threadIdx.x & 15) & 1) ? -1.0f : 1.0f;
+}
+
+// v[e] = fma(v[e] of the DPP partner, s, v[e]) for the 8 values, one v_fmac_f32_dpp each (the compiler keeps the DPP
+// move apart from a multiply-accumulate). The leading s_nop gives the two wait states a DPP read needs after a VALU write
+// of its source; inside the block each instruction reads a register no earlier one in it wrote.
+template <int K>   // 0: quad_perm [1,0,3,2], 1: quad_perm [2,3,0,1], 2: row_ror:8
+__device__ __forceinline__ void fmac_dpp_x8(float (&v)[8], float s)
+{
+#define BMX_FMAC8(D)                                                                                                    \
+    asm("s_nop 1\n\t"                                                                                                  \
+        "v_fmac_f32_dpp %0, %0, %8 " D "\n\t"                                                                          \
+        "v_fmac_f32_dpp %1, %1, %8 " D "\n\t"                                                                          \
+        "v_fmac_f32_dpp %2, %2, %8 " D "\n\t"                                                                          \
+        "v_fmac_f32_dpp %3, %3, %8 " D "\n\t"                                                                          \
+        "v_fmac_f32_dpp %4, %4, %8 " D "\n\t"                                                                          \
+        "v_fmac_f32_dpp %5, %5, %8 " D "\n\t"                                                                          \
+        "v_fmac_f32_dpp %6, %6, %8 " D "\n\t"                                                                          \
+        "v_fmac_f32_dpp %7, %7, %8 " D                                                                                 \
+        : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])                \
+        : "v"(s))
+    if (K == 0) BMX_FMAC8("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf");
+    else if (K == 1) BMX_FMAC8("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf");
+    else BMX_FMAC8("row_ror:8 row_mask:0xf bank_mask:0xf");
+#undef BMX_FMAC8
+}
+
 __device__ __forceinline__ void had128_x8(float (&v)[8])
 {
 #pragma unroll
@@ -221,14 +257,11 @@ __device__ __forceinline__ void had128_x8(float (&v)[8])
     const int lane = threadIdx.x & 63;
     const float s1 = (lane & 1) ? -1.0f : 1.0f, s2 = (lane & 2) ? -1.0f : 1.0f;
     const float s4 = (lane & 4) ? -1.0f : 1.0f, s8 = (lane & 8) ? -1.0f : 1.0f;
+    fmac_dpp_x8<0>(v, s1);                                                              // quad_perm [1,0,3,2]
+    fmac_dpp_x8<1>(v, s2);                                                              // quad_perm [2,3,0,1]
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s1, v[e], dpp_f<0xB1>(v[e]));   // quad_perm [1,0,3,2]
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s2, v[e], dpp_f<0x4E>(v[e]));   // quad_perm [2,3,0,1]
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s4, v[e], dpp_xor4(v[e]));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s8, v[e], dpp_f<0x128>(v[e]));  // row_ror:8
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(dpp_xor4(v[e]), s4, v[e]);
+    fmac_dpp_x8<2>(v, s8);                                                              // row_ror:8
 }
 
 // 16-byte global loads / stores and 8 fp16 <-> 16 bytes

@@ -397,6 +397,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
     }
     had128_x8(g);
     had128_x8(v);
+    const float rs = R_SCALE * had128_x8_sign();      // the transforms' lane sign folded into the scale
     float svg[8], svu[8], sud[8];
     unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[0]) + col), svg);
     unpack8(ldg4(reinterpret_cast<const uint16_t*>(ex.svh[1]) + col), svu);
@@ -405,13 +406,13 @@ __global__ __launch_bounds__(GV_THREADS) void k_gu_epi(GvArgs a)
 #pragma unroll
     for (int i = 0; i < 8; ++i)
     {
-        const float gi = (g[i] * R_SCALE) * svg[i], ui = (v[i] * R_SCALE) * svu[i];
+        const float gi = (g[i] * rs) * svg[i], ui = (v[i] * rs) * svu[i];
         act[i] = (a.fast_act ? act_gate_fast(a.act, a.gated, gi, ui, a.limit) : act_gate(a.act, a.gated, gi, ui, a.limit)) *
                  sud[i];
     }
     had128_x8(act);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) act[i] = act[i] * R_SCALE;
+    for (int i = 0; i < 8; ++i) act[i] = act[i] * rs;
     *reinterpret_cast<u32x4*>(a.act_rows + (size_t)r * a.I + col) = pack8_r(act);
 }
 
@@ -460,6 +461,7 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
     }
     had128_x8(g);
     had128_x8(v);
+    const float rs = R_SCALE * had128_x8_sign();      // the transforms' lane sign folded into the scale
     float svg[8], svu[8], sud[8];
     unpack8(svg4, svg);
     unpack8(svu4, svu);
@@ -468,12 +470,12 @@ __device__ __forceinline__ void gu_epi_wave(const GvArgs& a, int r, int cb, uint
 #pragma unroll
     for (int i = 0; i < 8; ++i)
     {
-        const float gi = (g[i] * R_SCALE) * svg[i], ui = (v[i] * R_SCALE) * svu[i];
+        const float gi = (g[i] * rs) * svg[i], ui = (v[i] * rs) * svu[i];
         act[i] = act_gate(a.act, a.gated, gi, ui, a.limit) * sud[i];
     }
     had128_x8(act);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) act[i] = act[i] * R_SCALE;
+    for (int i = 0; i < 8; ++i) act[i] = act[i] * rs;
     if (q == 0) *reinterpret_cast<u32x4*>(dst + 8 * j) = pack8_r(act);
 }
 
@@ -510,10 +512,11 @@ __device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float 
         sv4 = ldg4(svp);
     }
     had128_x8(y);
+    const float rs = R_SCALE * had128_x8_sign();
     float sv[8];
     unpack8(sv4, sv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = (y[i] * R_SCALE) * sv[i];
+    for (int i = 0; i < 8; ++i) y[i] = (y[i] * rs) * sv[i];
 }
 
 __device__ __forceinline__ void store8f(float* p, const float (&y)[8])

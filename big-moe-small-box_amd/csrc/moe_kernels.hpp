@@ -122,7 +122,7 @@ __device__ __forceinline__ void prep_unit(const GvArgs& a, long u)
         for (int q = 0; q < 8; ++q) v[q] = v[q] * s[q];
         had128_x8(v);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = v[q] * R_SCALE;
+        for (int q = 0; q < 8; ++q) v[q] = v[q] * (R_SCALE * had128_x8_sign());
         *reinterpret_cast<u32x4*>(dst + 128 * b) = pack8_r(v);
     }
 }
