@@ -9,6 +9,7 @@ the layer's expert products wait for those copies only in their staged part (MoE
 admits a later layer's guessed experts ahead of its step (the reference's layer-ahead routing guess, engine/nv2.py:
 450-487) with copies on the same side stream. No host synchronisation anywhere."""
 import ctypes
+import os
 import weakref
 
 import torch
@@ -70,9 +71,11 @@ class ExpertSlots:
         # staged prefill (stage_prefill): calls of at least stage_min picks admit nothing; each layer's experts that are
         # not resident are copied into one of two staging arenas one layer ahead on a copy stream
         self.stage_min = 8192                 # picks (the reference's EC_STAGE_MIN default, engine/tiers.py:673)
-        self.cstream = None
+        # copy streams the staging copies alternate over: a copy's set-up overlaps the transfer before it
+        self.stage_streams = int(os.environ.get("BMX_STAGE_STREAMS", "2"))
+        self.cstreams = []
         self.st_buf = [None, None]            # staging arenas, uint8 [n * rec] each
-        self.st_ready = [None, None]          # event: the arena's last staging copies done
+        self.st_ready = [[], []]              # events: the arena's last staging copies done (one per copy stream)
         self.st_open = False
         self.st_last = None                   # layer of the last staged call of the open forward
         self.st_layers = {}                   # li -> (experts np.int32, experts on the device, copy runs)
@@ -354,7 +357,8 @@ class ExpertSlots:
         if li not in self.st_sub:
             self._stage_submit(li)
         b = li % 2
-        cur.wait_event(self.st_ready[b])
+        for ev in self.st_ready[b]:
+            cur.wait_event(ev)
         ex, idx, runs = self.st_layers[li]
         if len(ex):
             L.check(L.lib().bmx_slot_stage_rows(ctypes.byref(self.struct), li, ctypes.c_void_p(idx.data_ptr()),
@@ -384,7 +388,7 @@ class ExpertSlots:
     def stage_release(self):
         """Close a staged forward and free the staging arenas."""
         self.stage_end()
-        self.st_buf, self.st_ready = [None, None], [None, None]
+        self.st_buf, self.st_ready = [None, None], [[], []]
 
     def _stage_begin(self, li0):
         """A staged forward from layer li0: wait for every copy in flight, snapshot residency, plan each later layer's
@@ -422,36 +426,42 @@ class ExpertSlots:
             self.st_layers[lj] = (ex, torch.from_numpy(ex).to(dev), runs)
             nmax = max(nmax, len(ex))
         need = nmax * self.layers[0].rec
-        if self.cstream is None:
-            self.cstream = torch.cuda.Stream(device=dev)
+        while len(self.cstreams) < max(1, self.stage_streams):
+            self.cstreams.append(torch.cuda.Stream(device=dev))
         for b in range(2):
             if self.st_buf[b] is None or self.st_buf[b].numel() < need:
                 self.st_buf[b] = None
                 buf = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
-                buf.record_stream(self.cstream)
+                for cs in self.cstreams:
+                    buf.record_stream(cs)
                 self.st_buf[b] = buf
         self.st_open = True
         self.st_stats["forwards"] += 1
 
     def _stage_submit(self, lj):
-        """Enqueue layer lj's staging copies into arena lj % 2 on the copy stream, behind everything the current stream
-        has enqueued so far (the products of the layer that last read that arena, and its restore)."""
+        """Enqueue layer lj's staging copies into arena lj % 2 on the copy streams (run i on stream i % streams),
+        behind everything the current stream has enqueued so far (the products of the layer that last read that arena,
+        and its restore)."""
         b = lj % 2
         _, _, runs = self.st_layers[lj]
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream())
-        self.cstream.wait_event(ev)
-        if runs:
-            base = self.st_buf[b].data_ptr()
-            n = len(runs)
-            src = (ctypes.c_void_p * n)(*[r[0] for r in runs])
-            dst = (ctypes.c_void_p * n)(*[base + r[1] for r in runs])
-            nb = (ctypes.c_size_t * n)(*[r[2] for r in runs])
-            L.check(L.lib().bmx_slot_stage_async(src, dst, nb, n, ctypes.c_void_p(self.cstream.cuda_stream)),
-                    "bmx_slot_stage_async")
-            self.st_stats["bytes"] += sum(r[2] for r in runs)
-        ready = torch.cuda.Event()
-        ready.record(self.cstream)
+        base = self.st_buf[b].data_ptr()
+        ready = []
+        for k, cs in enumerate(self.cstreams):
+            cs.wait_event(ev)
+            part = runs[k::len(self.cstreams)]
+            if part:
+                n = len(part)
+                src = (ctypes.c_void_p * n)(*[r[0] for r in part])
+                dst = (ctypes.c_void_p * n)(*[base + r[1] for r in part])
+                nb = (ctypes.c_size_t * n)(*[r[2] for r in part])
+                L.check(L.lib().bmx_slot_stage_async(src, dst, nb, n, ctypes.c_void_p(cs.cuda_stream)),
+                        "bmx_slot_stage_async")
+            done = torch.cuda.Event()
+            done.record(cs)
+            ready.append(done)
+        self.st_stats["bytes"] += sum(r[2] for r in runs)
         self.st_ready[b] = ready
         self.st_sub.add(lj)
 
