@@ -69,7 +69,7 @@ class ExpertSlots:
         self.cpu_ready = False                # dma: the agent has a CPU lane (cpu_lane())
         self.last_seq = 0                     # dma: the last sequence number the agent was given
         # staged prefill (stage_prefill): calls of at least stage_min picks admit nothing; each layer's experts that are
-        # not resident are copied into one of two staging arenas one layer ahead on a copy stream
+        # not resident are copied into one of two staging arenas one layer ahead on copy streams
         self.stage_min = 8192                 # picks (the reference's EC_STAGE_MIN default, engine/tiers.py:673)
         # copy streams the staging copies alternate over: a copy's set-up overlaps the transfer before it
         self.stage_streams = int(os.environ.get("BMX_STAGE_STREAMS", "2"))
@@ -341,7 +341,7 @@ class ExpertSlots:
         engine/tiers.py:406-463): returns False (and ends an open staged forward) when sel holds fewer than stage_min
         picks. Otherwise marks the hits only (a step that admits nothing, the reference's _ec_hits), and makes layer
         li's table point at a staging arena that holds every expert of the layer not resident in a slot: the copies
-        home -> arena (li % 2) run on a copy stream, enqueued one layer ahead (layer li + 1's go into the other arena
+        home -> arena (li % 2) run on copy streams (BMX_STAGE_STREAMS, 2), enqueued one layer ahead (layer li + 1's go into the other arena
         while layer li computes), and the current stream waits for layer li's. Residency is snapshotted when a forward
         starts (its first staged call, or a call to a layer at or before the last one; this synchronises), and stays as
         it is because staged calls admit nothing. After the layer's expert products, stage_restore(li) points the
