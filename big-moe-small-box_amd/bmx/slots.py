@@ -341,8 +341,8 @@ class ExpertSlots:
         engine/tiers.py:406-463): returns False (and ends an open staged forward) when sel holds fewer than stage_min
         picks. Otherwise marks the hits only (a step that admits nothing, the reference's _ec_hits), and makes layer
         li's table point at a staging arena that holds every expert of the layer not resident in a slot: the copies
-        home -> arena (li % 2) run on copy streams (BMX_STAGE_STREAMS, 2), enqueued one layer ahead (layer li + 1's go into the other arena
-        while layer li computes), and the current stream waits for layer li's. Residency is snapshotted when a forward
+        home -> arena (li % 2) run on copy streams (BMX_STAGE_STREAMS, 2), enqueued one layer ahead (layer li + 1's go
+        into the other arena while layer li computes), and the current stream waits for layer li's. Residency is snapshotted when a forward
         starts (its first staged call, or a call to a layer at or before the last one; this synchronises), and stays as
         it is because staged calls admit nothing. After the layer's expert products, stage_restore(li) points the
         entries back. The shared expert is not in the slot table and is read where it lives."""
