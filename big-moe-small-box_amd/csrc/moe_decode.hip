@@ -217,9 +217,10 @@ __device__ __forceinline__ void gemv_unit(const GvArgs& a, int ks, int cb, int e
 }
 
 // the 4- and 8-row kernels (the product loop's staged input and accumulators grow with the rows) capped at 128 and 168
-// VGPRs: 4 and 3 waves per SIMD instead of 3 and 2
+// VGPRs: 4 and 3 waves per SIMD instead of 3 and 2; the one-row down GEMV at 5 waves per SIMD (96 VGPRs instead of 116:
+// C2's 1,152 one-token down workgroups start in one round; down 15.2 -> 14.6 us, the layer 54.6 -> 54.2 us)
 template <int MX, int NM>
-__global__ __launch_bounds__(GV_THREADS, (MX == 4 ? 4 : MX == 8 ? 3 : 1)) void k_gemv_part(GvArgs a)
+__global__ __launch_bounds__(GV_THREADS, (MX == 4 ? 4 : MX == 8 ? 3 : MX == 1 && NM == 1 ? 5 : 1)) void k_gemv_part(GvArgs a)
 {
     if (NM == 2 && a.split_min > a.T && a.filter != 2 && split_callwide(a))
     {
