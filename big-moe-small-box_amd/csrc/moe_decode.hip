@@ -542,6 +542,69 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_epi(GvArgs a)
 // ---- down epilogue + combine -----------------------------------------------------------------------------------------
 // out[t] = sum over k ascending of w[t, k] * y(inv[t, k]) (picks with inv < 0 or w = 0 skipped), then + y(shared row)
 // (engine/kernels/x16/x16_dev.cu:354-384). Large launches: 16 lanes per (token, 128-column block), the slots in turn.
+// With one k-split for every row (the prefill path): CB_BATCH slots at a time, every load of the batch (the slot's
+// partial row, its expert's scale vector) issued before the first slot's transform, the same operations in the same
+// order afterwards (so the same bits).
+constexpr int CB_BATCH = 3;
+__device__ __forceinline__ void combine_batched(const GvArgs& a, int t, int cb, float (&o)[8])
+{
+    const int j = threadIdx.x & 15;
+    const float rs = R_SCALE * had128_x8_sign();
+    for (int k0 = 0; k0 < a.topk; k0 += CB_BATCH)
+    {
+        int r[CB_BATCH];
+        float wk[CB_BATCH];
+        f32x4 q[CB_BATCH][2];
+        u32x4 sv4[CB_BATCH];
+#pragma unroll
+        for (int b = 0; b < CB_BATCH; ++b)
+        {
+            const int k = k0 + b;
+            r[b] = -1;
+            wk[b] = 0.0f;
+            if (k < a.topk)
+            {
+                r[b] = a.inv[t * a.topk + k];
+                wk[b] = h2f(a.w[t * a.topk + k]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < CB_BATCH; ++b)
+            if (r[b] >= 0 && wk[b] != 0.0f)
+            {
+                const float* pp = a.part_dn + ((size_t)r[b] * a.NBH + cb) * 128 + 8 * j;
+                q[b][0] = ldg4f(pp);
+                q[b][1] = ldg4f(pp + 4);
+                const int e = a.row_expert[r[b]];
+                const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
+                sv4[b] = ldg4(reinterpret_cast<const uint16_t*>(ex.svh[2]) + cb * 128 + 8 * j);
+            }
+#pragma unroll
+        for (int b = 0; b < CB_BATCH; ++b)
+        {
+            if (r[b] < 0 || wk[b] == 0.0f) continue;
+            float y[8], sv[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                y[i] = 0.0f + q[b][0][i];
+                y[4 + i] = 0.0f + q[b][1][i];
+            }
+            had128_x8(y);
+            unpack8(sv4[b], sv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = (y[i] * rs) * sv[i];
+            if (a.y_rows) store8f(a.y_rows + (size_t)r[b] * a.H + cb * 128 + 8 * j, y);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+            {
+                const float p = wk[b] * y[i];
+                o[i] = o[i] + p;
+            }
+        }
+    }
+}
+
 __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
 {
     const int u = ep_unit<4>(), j = threadIdx.x & 15;
@@ -550,6 +613,8 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
     float o[8], y[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = 0.0f;
+    if (a.KS_dn == 1 && !a.split_min) combine_batched(a, t, cb, o);
+    else
     for (int k = 0; k < a.topk; ++k)
     {
         const int r = a.inv[t * a.topk + k];
