@@ -542,10 +542,10 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_epi(GvArgs a)
 // ---- down epilogue + combine -----------------------------------------------------------------------------------------
 // out[t] = sum over k ascending of w[t, k] * y(inv[t, k]) (picks with inv < 0 or w = 0 skipped), then + y(shared row)
 // (engine/kernels/x16/x16_dev.cu:354-384). Large launches: 16 lanes per (token, 128-column block), the slots in turn.
-// With one k-split for every row (the prefill path): CB_BATCH slots at a time, every load of the batch (the slot's
-// partial row, its expert's scale vector) issued before the first slot's transform, the same operations in the same
-// order afterwards (so the same bits).
-constexpr int CB_BATCH = 3;
+// With one k-split for every row (the prefill path): CB_BATCH slots at a time (2: 217 us at C3, 3: 219, 6: 245; one
+// slot at a time: 256), every load of the batch (the slots' partial rows, their experts' scale vectors) issued before
+// the first slot's transform, the same operations in the same order afterwards (so the same bits).
+constexpr int CB_BATCH = 2;
 __device__ __forceinline__ void combine_batched(const GvArgs& a, int t, int cb, float (&o)[8])
 {
     const int j = threadIdx.x & 15;
