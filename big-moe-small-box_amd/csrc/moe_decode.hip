@@ -520,6 +520,14 @@ __device__ __forceinline__ void down_out8(const GvArgs& a, int r, int cb, float 
     for (int i = 0; i < 8; ++i) y[i] = (y[i] * rs) * sv[i];
 }
 
+// the same with non-temporal stores: outputs written once and read by the next layer, not by this call's kernels
+__device__ __forceinline__ void store8f_nt(float* p, const float (&y)[8])
+{
+    const f32x4 a = {y[0], y[1], y[2], y[3]}, b = {y[4], y[5], y[6], y[7]};
+    __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(p));
+    __builtin_nontemporal_store(b, reinterpret_cast<f32x4*>(p + 4));
+}
+
 __device__ __forceinline__ void store8f(float* p, const float (&y)[8])
 {
     *reinterpret_cast<float4*>(p) = make_float4(y[0], y[1], y[2], y[3]);
@@ -648,7 +656,7 @@ __global__ __launch_bounds__(GV_THREADS) void k_dn_combine(GvArgs a)
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = o[i] + y[i];
     }
-    store8f(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
+    store8f_nt(a.out + (size_t)t * a.H + cb * 128 + 8 * j, o);
 }
 
 // The combine of token t's 128-column block cb by one workgroup: 16-lane group k computes slot k (the shared expert's

@@ -123,7 +123,7 @@ __device__ __forceinline__ void prep_unit(const GvArgs& a, long u)
         had128_x8(v);
 #pragma unroll
         for (int q = 0; q < 8; ++q) v[q] = v[q] * (R_SCALE * had128_x8_sign());
-        *reinterpret_cast<u32x4*>(dst + 128 * b) = pack8_r(v);
+        __builtin_nontemporal_store(pack8_r(v), reinterpret_cast<u32x4*>(dst + 128 * b));   // streamed (C3: 265 -> 252 us)
     }
 }
 
