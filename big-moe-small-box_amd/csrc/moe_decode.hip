@@ -61,6 +61,10 @@ __device__ __forceinline__ void strip(const uint32_t (&own)[Fmt<F>::TB / 16], co
     }
 }
 
+template <int F, int MR>
+__device__ __forceinline__ void gemv_wave_from(const uint8_t* p, size_t row_bytes, uint32_t (&wa)[Fmt<F>::TB / 16],
+                                               int ntr, const uint32_t* xb, int xstride, float (&acc)[4][MR]);
+
 // A wave's GEMV over tile-rows [tr0, tr0 + ntr) (ntr even; the two half-waves take alternate rows) of the 128-column
 // block cb of a matrix with tn tiles per row. xs: LDS input rows, dword (tr - xtr0) * 8 of each token row. Two register
 // sets alternate so the next strip's words are in flight while the current one is decoded.
@@ -72,9 +76,18 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ mat, int t
     const int lane = threadIdx.x & 63, h = lane >> 5, t = (lane >> 2) & 7, s = lane & 3;
     const size_t row_bytes = (size_t)tn * TB;
     const uint8_t* p = mat + (size_t)(tr0 + h) * row_bytes + (size_t)(cb * 8 + t) * TB + s * (TB / 4);
-    const uint32_t* xb = xs + (tr0 + h - xtr0) * 8;
-    uint32_t wa[NW], wb[NW];
+    uint32_t wa[NW];
     load_words(wa, p);
+    gemv_wave_from<F, MR>(p, row_bytes, wa, ntr, xs + (tr0 + h - xtr0) * 8, xstride, acc);
+}
+
+// The loop of gemv_wave from the lane's first words wa (already requested, at p)
+template <int F, int MR>
+__device__ __forceinline__ void gemv_wave_from(const uint8_t* p, size_t row_bytes, uint32_t (&wa)[Fmt<F>::TB / 16],
+                                               int ntr, const uint32_t* xb, int xstride, float (&acc)[4][MR])
+{
+    constexpr int NW = Fmt<F>::TB / 16;
+    uint32_t wb[NW];
     int it = 0;
     for (; it + 4 <= ntr; it += 4)
     {
@@ -137,6 +150,49 @@ __device__ __forceinline__ void gemv_rows(const GvArgs& a, const bmx_expert& ex,
             for (int m = 0; m < MR; ++m) red[(wave * MX + m) * 128 + lane_col(lane, c)] = acc[c][m];
 }
 
+// The one-row down GEMV's staging and products (k_gemv_part<1, 1>, input rows from act_rows): the loads of the row's
+// k-range are issued first, then each lane's first trellis words (they need the expert record only), and only then is
+// the row stored to LDS, so the words' latency runs beside the staging's instead of after the barrier (C2 one-token
+// layer 53.02 -> 52.91 us, paired runs). Same products, same order as staging then gemv_rows<1, 1, 1>. XW <= 4 *
+// GV_THREADS (checked by the caller).
+template <int F>
+__device__ __forceinline__ void down1_rows(const GvArgs& a, const bmx_expert& ex, int cb, int k0, int KR, int r0,
+                                           uint32_t* xs, float* red)
+{
+    constexpr int TB = Fmt<F>::TB, NW = TB / 16;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, XW = KR / 2;
+    uint32_t xv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int d = threadIdx.x + i * GV_THREADS;
+        xv[i] = d < XW ? ldg(a.act_rows + (size_t)r0 * a.I + k0 + 2 * d, 0) : 0u;
+    }
+    const int TRW = KR / 16 / GV_WAVES, tr0 = k0 / 16 + wave * TRW;
+    const int h = lane >> 5, t = (lane >> 2) & 7, s = lane & 3;
+    const size_t row_bytes = (size_t)(a.H / 16) * TB;
+    const uint8_t* p = reinterpret_cast<const uint8_t*>(ex.tr[2]) + (size_t)(tr0 + h) * row_bytes +
+                       (size_t)(cb * 8 + t) * TB + s * (TB / 4);
+    uint32_t wa[NW];
+    load_words(wa, p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int d = threadIdx.x + i * GV_THREADS;
+        if (d < XW) xs[d] = xv[i];
+    }
+    lds_barrier();
+    float acc[4][1];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c][0] = 0.0f;
+    gemv_wave_from<F, 1>(p, row_bytes, wa, TRW, xs + (tr0 + h - k0 / 16) * 8, XW, acc);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c][0] = acc[c][0] + xor32_f(acc[c][0]);
+    if (lane < 32)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) red[wave * 128 + lane_col(lane, c)] = acc[c][0];
+}
+
 // One work unit (k-split ks, column block cb of a group: expert e, rows r0 .. r0 + nr - 1) of the split-K GEMV. tok1 >= 0:
 // the rows' token (a one-token call whose dispatch is being written by another workgroup), else from row_token.
 template <int MX, int NM>
@@ -151,6 +207,7 @@ __device__ __forceinline__ void gemv_unit(const GvArgs& a, int ks, int cb, int e
     uint32_t* xs = smem;                                           // [NM][MX][KR / 2] fp16 pairs
     float* red = reinterpret_cast<float*>(smem + NM * MX * XW);    // [GV_WAVES][MX][128] (gate / up: waves 0-1 gate)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    bool pre = false;                  // the one-row down GEMV ran its staging and products itself (down1_rows)
 
     if (NM == 2)
     {
@@ -181,6 +238,20 @@ __device__ __forceinline__ void gemv_unit(const GvArgs& a, int ks, int cb, int e
             gu_epi_wave<2>(a, r0 + u / nblk, k0 / 128 + u % nblk,     // two splits in flight: the GEMV's registers
                         reinterpret_cast<uint16_t*>(xs + (u / nblk) * XW + (u % nblk) * 64));
     }
+    else if (MX == 1 && XW <= 4 * GV_THREADS)
+    {
+        if constexpr (NM == 1 && MX == 1)
+        {
+            switch (ex.fmt[2])
+            {
+                case BMX_TF_K2: down1_rows<BMX_TF_K2>(a, ex, cb, k0, KR, r0, xs, red); break;
+                case BMX_TF_K25: down1_rows<BMX_TF_K25>(a, ex, cb, k0, KR, r0, xs, red); break;
+                case BMX_TF_K3: down1_rows<BMX_TF_K3>(a, ex, cb, k0, KR, r0, xs, red); break;
+                default: down1_rows<BMX_TF_K4>(a, ex, cb, k0, KR, r0, xs, red); break;
+            }
+            pre = true;
+        }
+    }
     else
     {
         for (int i = threadIdx.x; i < nr * XW; i += GV_THREADS)
@@ -196,11 +267,14 @@ __device__ __forceinline__ void gemv_unit(const GvArgs& a, int ks, int cb, int e
         const int mat = i / ((mr - nr) * XW), rem = i % ((mr - nr) * XW);
         xs[(mat * MX + nr) * XW + rem] = 0u;
     }
-    lds_barrier();
-    if (mr == 1) gemv_rows<1, MX, NM>(a, ex, cb, k0, KR, N, xs, red);
-    else if (mr == 2) { if constexpr (MX >= 2) gemv_rows<2, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
-    else if (mr == 4) { if constexpr (MX >= 4) gemv_rows<4, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
-    else { if constexpr (MX >= 8) gemv_rows<8, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
+    if (!pre)
+    {
+        lds_barrier();
+        if (mr == 1) gemv_rows<1, MX, NM>(a, ex, cb, k0, KR, N, xs, red);
+        else if (mr == 2) { if constexpr (MX >= 2) gemv_rows<2, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
+        else if (mr == 4) { if constexpr (MX >= 4) gemv_rows<4, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
+        else { if constexpr (MX >= 8) gemv_rows<8, MX, NM>(a, ex, cb, k0, KR, N, xs, red); }
+    }
     lds_barrier();
     // the waves of a matrix in order, then one partial per (split, row, block)
     float* part = (NM == 2 ? a.part_gu : a.part_dn) + (((size_t)ks * a.R_max + r0) * NB + cb) * (NM * 128);
