@@ -339,6 +339,17 @@ __global__ __launch_bounds__(GV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8
     extern __shared__ uint32_t smem[];
     RouteLds<J>& L = *reinterpret_cast<RouteLds<J>*>(smem);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, topk = f.ra.topk;
+    int bid = blockIdx.x;
+    const int ks = bid % a.KS_gu;
+    bid /= a.KS_gu;
+    const int cb = bid % a.NB, g = bid / a.NB;
+    if (g >= topk + (a.has_shared ? 1 : 0)) return;
+    if (g == topk && blockIdx.x != 0)
+    {
+        // the shared expert's row (topk) needs nothing from the router: these workgroups decode while the others route
+        gemv_unit<1, 2>(a, ks, cb, a.E, g, 1, 0);
+        return;
+    }
     if (wave == 0)
     {
         RouterArgs ra = f.ra;
@@ -355,11 +366,6 @@ __global__ __launch_bounds__(GV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8
         if (blockIdx.x == 0) dispatch_wave<J + 1>(L.pe, topk, f.ra.E, 1, topk, f.sd, L.cnt, L.off, L.mask);
     }
     __syncthreads();
-    int bid = blockIdx.x;
-    const int ks = bid % a.KS_gu;
-    bid /= a.KS_gu;
-    const int cb = bid % a.NB, g = bid / a.NB;
-    if (g >= topk + (a.has_shared ? 1 : 0)) return;
     const int e = g < topk ? L.gex[g] : a.E;
     __syncthreads();                      // every wave has read the routing LDS before the GEMV reuses it
     gemv_unit<1, 2>(a, ks, cb, e, g, 1, 0);
