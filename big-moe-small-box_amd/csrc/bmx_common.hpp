@@ -133,6 +133,84 @@ __device__ __forceinline__ void cb_oct(const uint32_t (&st)[8], uint32_t (&w)[4]
           "v"((KBIAS_BITS << 16) | KBIAS_BITS));
 }
 
+// cb_oct on states held in the high halves of st[0 .. 7] (op_sel on the two multiplies; the rest is cb_oct's).
+__device__ __forceinline__ void cb_oct_hi(const uint32_t (&st)[8], uint32_t (&w)[4])
+{
+    uint32_t t[8];
+    asm("v_pk_mul_lo_u16 %4, %12, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %5, %13, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %6, %14, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %7, %15, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %8, %16, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %9, %17, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %10, %18, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %11, %19, %20 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_mad_u32_u16 %4, %12, %21, %4 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %5, %13, %21, %5 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %6, %14, %21, %6 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %7, %15, %21, %7 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %8, %16, %21, %8 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %9, %17, %21, %9 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %10, %18, %21, %10 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %11, %19, %21, %11 op_sel:[1,0,0,0]\n\t"
+        "v_sad_u8 %0, %4, 0, %22\n\t"
+        "v_sad_u8 %1, %6, 0, %22\n\t"
+        "v_sad_u8 %2, %8, 0, %22\n\t"
+        "v_sad_u8 %3, %10, 0, %22\n\t"
+        "v_sad_hi_u8 %0, %5, 0, %0\n\t"
+        "v_sad_hi_u8 %1, %7, 0, %1\n\t"
+        "v_sad_hi_u8 %2, %9, 0, %2\n\t"
+        "v_sad_hi_u8 %3, %11, 0, %3\n\t"
+        "v_pk_fma_f16 %0, %0, %23, %24\n\t"
+        "v_pk_fma_f16 %1, %1, %23, %24\n\t"
+        "v_pk_fma_f16 %2, %2, %23, %24\n\t"
+        "v_pk_fma_f16 %3, %3, %23, %24"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]),
+          "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+        : "v"(st[0]), "v"(st[1]), "v"(st[2]), "v"(st[3]), "v"(st[4]), "v"(st[5]), "v"(st[6]), "v"(st[7]),
+          "s"(MUL1_HI_SHL16), "s"(MUL1_LO), "s"((F16_1024 << 16) | F16_1024), "s"((KINV_BITS << 16) | KINV_BITS),
+          "v"((KBIAS_BITS << 16) | KBIAS_BITS));
+}
+
+// cb_oct on eight states held in four registers: state q < 4 in the high half of v[q], state q + 4 in its low half.
+__device__ __forceinline__ void cb_oct_k4(const uint32_t (&v)[4], uint32_t (&w)[4])
+{
+    uint32_t t[8];
+    asm("v_pk_mul_lo_u16 %4, %12, %16 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %5, %13, %16 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %6, %14, %16 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %7, %15, %16 op_sel:[1,0] op_sel_hi:[1,1]\n\t"
+        "v_pk_mul_lo_u16 %8, %12, %16 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %9, %13, %16 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %10, %14, %16 op_sel_hi:[0,1]\n\t"
+        "v_pk_mul_lo_u16 %11, %15, %16 op_sel_hi:[0,1]\n\t"
+        "v_mad_u32_u16 %4, %12, %17, %4 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %5, %13, %17, %5 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %6, %14, %17, %6 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %7, %15, %17, %7 op_sel:[1,0,0,0]\n\t"
+        "v_mad_u32_u16 %8, %12, %17, %8\n\t"
+        "v_mad_u32_u16 %9, %13, %17, %9\n\t"
+        "v_mad_u32_u16 %10, %14, %17, %10\n\t"
+        "v_mad_u32_u16 %11, %15, %17, %11\n\t"
+        "v_sad_u8 %0, %4, 0, %18\n\t"
+        "v_sad_u8 %1, %6, 0, %18\n\t"
+        "v_sad_u8 %2, %8, 0, %18\n\t"
+        "v_sad_u8 %3, %10, 0, %18\n\t"
+        "v_sad_hi_u8 %0, %5, 0, %0\n\t"
+        "v_sad_hi_u8 %1, %7, 0, %1\n\t"
+        "v_sad_hi_u8 %2, %9, 0, %2\n\t"
+        "v_sad_hi_u8 %3, %11, 0, %3\n\t"
+        "v_pk_fma_f16 %0, %0, %19, %20\n\t"
+        "v_pk_fma_f16 %1, %1, %19, %20\n\t"
+        "v_pk_fma_f16 %2, %2, %19, %20\n\t"
+        "v_pk_fma_f16 %3, %3, %19, %20"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]),
+          "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+        : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]),
+          "s"(MUL1_HI_SHL16), "s"(MUL1_LO), "s"((F16_1024 << 16) | F16_1024), "s"((KINV_BITS << 16) | KINV_BITS),
+          "v"((KBIAS_BITS << 16) | KBIAS_BITS));
+}
+
 // Workgroup barrier that orders LDS only: waits for the wave's LDS operations, not for its global loads and stores
 // (__syncthreads waits for those too). For barriers whose data is exchanged through LDS alone.
 __device__ __forceinline__ void lds_barrier()

@@ -34,7 +34,6 @@ __device__ __forceinline__ void strip(const uint32_t (&own)[Fmt<F>::TB / 16], co
                                       float (&acc)[4][MR])
 {
     constexpr int NW = Fmt<F>::TB / 16;
-    constexpr RingTab<F> tab;
     // previous lane's last word (quad_perm [3,0,1,2]: lane 0 of the tile takes lane 3's, the ring wraps)
     const uint32_t prev = __builtin_amdgcn_mov_dpp(own[NW - 1], 0x93, 0xf, 0xf, false);
     uint32_t X[MR][8];
@@ -45,10 +44,8 @@ __device__ __forceinline__ void strip(const uint32_t (&own)[Fmt<F>::TB / 16], co
 #pragma unroll
     for (int j8 = 0; j8 < 64; j8 += 8)
     {
-        uint32_t st[8], w[4];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) st[q] = win_state(prev, own, tab.q[j8 + q]);
-        cb_oct(st, w);
+        uint32_t w[4];
+        oct_weights<F>(prev, own, j8, w);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
         {

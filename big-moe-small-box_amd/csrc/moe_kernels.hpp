@@ -156,6 +156,61 @@ __device__ __forceinline__ uint32_t win_state(uint32_t prev, const uint32_t (&ow
     return __builtin_amdgcn_alignbit(hi, own[d], 48 - o);
 }
 
+// Window bits [q - 16, q + 16) as one 32-bit value: the state at bit q in its low half, the one at q - 16 in its high
+// half (q >= 16)
+template <int NW>
+__device__ __forceinline__ uint32_t win_pair(uint32_t prev, const uint32_t (&own)[NW], int q)
+{
+    const int p = q - 16, d = p >> 5, o = p & 31;
+    const uint32_t w0 = d == 0 ? prev : own[d - 1];
+    if (o == 0) return w0;
+    return __builtin_amdgcn_alignbit(w0, own[d], 32 - o);
+}
+
+// states that start 16 bits apart in the ring: stream positions i and i + 16 / K for every i of a 64-position strip
+template <int F> __host__ __device__ constexpr bool ring_pairs16(int step)
+{
+    for (int i = 0; i + step < 64; ++i)
+        if (ring_end<F>(i + step) - ring_end<F>(i) != 16) return false;
+    return true;
+}
+
+// Codebook weights of stream positions j8 .. j8 + 7 of a lane's strip (j8 a multiple of 8, a constant after unrolling),
+// packed as cb_oct's. K 2 and K 4: the state 16 ring bits before another (8 positions back at K 2, 4 at K 4) is the high
+// half of the same 32-bit window, so one funnel shift gives two states and the hash reads the high half by op_sel
+// (K 2: half a shift per state; the two octs of a 16-position block share their shifts, which the compiler computes
+// once). K 2.5 and K 3 have no such partner: a shift per state.
+template <int F, int NW>
+__device__ __forceinline__ void oct_weights(uint32_t prev, const uint32_t (&own)[NW], int j8, uint32_t (&w)[4])
+{
+    constexpr RingTab<F> tab;
+    if constexpr (F == BMX_TF_K2)
+    {
+        static_assert(ring_pairs16<F>(8), "K 2: positions 8 apart start 16 bits apart");
+        const int j16 = j8 & ~15;
+        uint32_t v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = win_pair(prev, own, tab.q[j16 + 8 + q]);
+        if (j8 & 8) cb_oct(v, w);
+        else cb_oct_hi(v, w);
+    }
+    else if constexpr (F == BMX_TF_K4)
+    {
+        static_assert(ring_pairs16<F>(4), "K 4: positions 4 apart start 16 bits apart");
+        uint32_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = win_pair(prev, own, tab.q[j8 + 4 + q]);
+        cb_oct_k4(v, w);
+    }
+    else
+    {
+        uint32_t st[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st[q] = win_state(prev, own, tab.q[j8 + q]);
+        cb_oct(st, w);
+    }
+}
+
 // NT: non-temporal loads. The prefill GEMM reads with the default policy instead, since a row group decoded again by
 // another workgroup then finds its words in the caches (C3's layer 2 % faster); the decode GEMV (5 % slower without)
 // and the mid-size GEMM (1 %) keep the non-temporal loads.

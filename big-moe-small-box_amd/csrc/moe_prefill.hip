@@ -92,7 +92,6 @@ __device__ __forceinline__ void decode_half(const uint32_t (&own)[Fmt<F>::TB / 1
                                             int col0, int lane)
 {
     constexpr int NW = Fmt<F>::TB / 16;
-    constexpr RingTab<F> tab;
     // every word of the window is consumed here (a half strip reads only some of them): keeps the prefetched registers
     // allocated until now instead of reused while their load is in flight, which would force a wait on it
 #pragma unroll
@@ -102,10 +101,8 @@ __device__ __forceinline__ void decode_half(const uint32_t (&own)[Fmt<F>::TB / 1
 #pragma unroll
     for (int j8 = 32 * HALF; j8 < 32 * HALF + 32; j8 += 8)
     {
-        uint32_t st[8], w[4];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) st[q] = win_state(prev, own, tab.q[j8 + q]);
-        cb_oct(st, w);
+        uint32_t w[4];
+        oct_weights<F>(prev, own, j8, w);
 #pragma unroll
         for (int q = 0; q < 4; ++q) fr[strip_cidx(j8 + 2 * q) >> 1][strip_dw(j8 + 2 * q)] = w[q];
     }
@@ -127,7 +124,6 @@ __device__ __forceinline__ void decode_quarter(const uint32_t (&own)[Fmt<F>::TB 
                                                int col0)
 {
     constexpr int NW = Fmt<F>::TB / 16;
-    constexpr RingTab<F> tab;
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int k = 0; k < NW; ++k) asm volatile("" :: "v"(own[k]));
@@ -136,10 +132,8 @@ __device__ __forceinline__ void decode_quarter(const uint32_t (&own)[Fmt<F>::TB 
 #pragma unroll
     for (int j8 = 32 * HALF + 16 * SUB; j8 < 32 * HALF + 16 * SUB + 16; j8 += 8)
     {
-        uint32_t st[8], w[4];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) st[q] = win_state(prev, own, tab.q[j8 + q]);
-        cb_oct(st, w);
+        uint32_t w[4];
+        oct_weights<F>(prev, own, j8, w);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
         {
