@@ -8,7 +8,7 @@
 // (columns), run the MFMAs of that step with A fragments read from global memory. fp32 accumulation; each output
 // element is one fixed sum (k ascending in MFMA blocks), independent of scheduling.
 //
-//   k_pf_prep     : rotated gate / up inputs of every dispatch row, xt = RN16(H128(x * suh) * R)
+//   k_pf_prep_tok : rotated gate / up inputs of every dispatch row, xt = RN16(H128(x * suh) * R), token-major
 //   k_pf_gemm<false> : gate or up products of one 256-column block -> fp32 [row][128-block][gate | up][128]
 //   (k_gu_epi)    : fp16 gate / up -> epilogue -> fp16 down-input rows (shared with the decode path)
 //   k_pf_gemm<true>  : down products of one 256-column block -> fp32 [row][128-block][128]
@@ -42,6 +42,80 @@ __global__ __launch_bounds__(256) void k_pf_prep(GvArgs a)
 static dim3 prep_grid(int R_max, int H)
 {
     return dim3((unsigned)(((long)2 * R_max * ((H / 128 + PREP_BPU - 1) / PREP_BPU) + 15) / 16));
+}
+
+// ---- rotated inputs, token-major (the prefill path) --------------------------------------------------------------------
+// Unit u = (token, run of PREP_BPU 128-blocks) by a 16-lane group: the token's inputs are loaded once and rotated into
+// the rows of all its picks and its shared-expert row, gate and up (the same values as prep_unit, which reads the
+// token's inputs once per row and matrix, 12 times at top-6: 441 MB of HBM reads for C3's 805 MB of rows, 205 MB
+// here). Lane j first fetches slot k0 + j's row and its expert's suh addresses, so the dependent index loads run once
+// per 16 slots, side by side; the slot loop takes them by shuffles within the group.
+__device__ __forceinline__ void prep_tok_unit(const GvArgs& a, long u)
+{
+    const int nblk = a.H / 128, nrun = (nblk + PREP_BPU - 1) / PREP_BPU;
+    const int j = threadIdx.x & 15, run = (int)(u % nrun);
+    const long t = u / nrun;
+    if (t >= a.T) return;                 // the whole 16-lane group: the shuffles below stay inside it
+    float xv[PREP_BPU][8];
+    const uint16_t* xr = a.x + (size_t)t * a.H + 8 * j;
+#pragma unroll
+    for (int i = 0; i < PREP_BPU; ++i)
+        if (run * PREP_BPU + i < nblk) unpack8(ldg4(xr + 128 * (run * PREP_BPU + i)), xv[i]);
+    const int ns = a.topk + (a.has_shared ? 1 : 0);
+    for (int k0 = 0; k0 < ns; k0 += 16)
+    {
+        const int kj = k0 + j;
+        int rj = -1;
+        if (kj < a.topk) rj = a.inv[t * a.topk + kj];
+        else if (kj < ns) rj = a.offsets[a.E] + (int)t;
+        uint64_t su0 = 0, su1 = 0;
+        if (rj >= 0)
+        {
+            const int e = a.row_expert[rj];
+            const bmx_expert& ex = e == a.E ? *a.shared : a.experts[e];
+            su0 = reinterpret_cast<uint64_t>(ex.suh[0]);
+            su1 = reinterpret_cast<uint64_t>(ex.suh[1]);
+        }
+        const int kn = ns - k0 < 16 ? ns - k0 : 16;
+        for (int k = 0; k < kn; ++k)
+        {
+            const int r = __shfl(rj, k, 16);
+            if (r < 0) continue;              // a dropped pick: no row
+#pragma unroll
+            for (int mat = 0; mat < 2; ++mat)
+            {
+                const uint64_t sa = mat ? su1 : su0;
+                const uint32_t lo = __shfl((uint32_t)sa, k, 16), hi = __shfl((uint32_t)(sa >> 32), k, 16);
+                const uint16_t* su = reinterpret_cast<const uint16_t*>(((uint64_t)hi << 32) | lo) + 8 * j;
+                uint16_t* dst = a.xt + ((size_t)mat * a.R_max + r) * a.H + 8 * j;
+#pragma unroll
+                for (int i = 0; i < PREP_BPU; ++i)
+                {
+                    const int b = run * PREP_BPU + i;
+                    if (b >= nblk) break;
+                    float v[8], s[8];
+                    unpack8(ldg4(su + 128 * b), s);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) v[q] = xv[i][q] * s[q];
+                    had128_x8(v);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) v[q] = v[q] * (R_SCALE * had128_x8_sign());
+                    __builtin_nontemporal_store(pack8_r(v), reinterpret_cast<u32x4*>(dst + 128 * b));
+                }
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_pf_prep_tok(GvArgs a)
+{
+    prep_tok_unit(a, (long)blockIdx.x * 16 + (threadIdx.x >> 4));
+}
+
+static dim3 prep_tok_grid(int T, int H)
+{
+    const long units = (long)T * ((H / 128 + PREP_BPU - 1) / PREP_BPU);
+    return dim3((unsigned)std::max(1L, (units + 15) / 16));
 }
 
 // ---- LDS stages ------------------------------------------------------------------------------------------------------
@@ -874,7 +948,7 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
     a.fast_act = prefill_fast_act() ? 1 : 0;
     int rc = BMX_OK;
     if (stages & (1 << BMX_STAGE_PREP))
-        hipLaunchKernelGGL(k_pf_prep, prep_grid(p.R_max, m.H), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_pf_prep_tok, prep_tok_grid(m.T, m.H), dim3(256), 0, s, a);
     for (int f = 0; f < 3; ++f)
     {
         const int st = f == 0 ? BMX_STAGE_GATE_UP : f == 1 ? BMX_STAGE_GATE_UP_RESIDENT : BMX_STAGE_GATE_UP_STAGED;
