@@ -245,3 +245,32 @@ def test_prefill_pairs(cuda, oracle, name, H, I, fmts, shared, T, topk, E, plan)
     err_abs, err_rel = float(np.abs(got - want).max()), rel_rms(got, want)
     say("pairs", name, "oracle rows", rows, "max_abs", err_abs, "rel_rms", err_rel)
     assert err_abs < MAX_ABS and err_rel < REL_RMS
+
+
+def test_prefill_wide_topk_dropped_picks(cuda, oracle):
+    """The prefill path's token-major rotation takes a token's slots 16 at a time: 16 picks plus the shared expert need
+    a second pass, and picks with ids outside the layer's experts have no row (their slots are skipped). Every token
+    against the oracle."""
+    import bmx
+    H, I, E, T, topk = 512, 256, 40, 24, 16
+    tab = bmx.ExpertTable.random(H, I, E, (0, 3, 2), shared=True, seed=41, device=cuda)
+    layer = bmx.MoELayer(tab, topk, score=bmx.SCORE_SIGMOID, renorm=True, scale=1.5)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(42)
+    x = torch.randn((T, H), generator=g, device=cuda).half()
+    lg = torch.randn((T, E), generator=g, device=cuda).half()
+    sel, w = layer.routing_fn(T, None, x, {"logits": lg})
+    sel = sel.clone()
+    for t, k in ((0, 3), (5, 0), (5, 15), (11, 7), (23, 15)):
+        sel[t, k] = E + 3 if (t + k) % 2 else -2
+    say("wide topk: run")
+    out = layer.run_bszN(x, sel, w, path=PREFILL).cpu().numpy()
+    sel_np, w_np = sel.cpu().numpy(), w.cpu().numpy()
+    want = oracle_layer(oracle, tab, x.cpu().numpy(), sel_np, w_np, list(range(T)))
+    err_abs, err_rel = float(np.abs(out - want).max()), rel_rms(out, want)
+    say("wide topk: max_abs", err_abs, "rel_rms", err_rel)
+    assert err_abs < MAX_ABS and err_rel < REL_RMS
+    # the dropped picks matter: the oracle without them differs
+    kept = sel_np.copy()
+    kept[0, 3] = (kept[0, 3] + 1) % E
+    assert rel_rms(oracle_layer(oracle, tab, x.cpu().numpy(), kept, w_np, [0]), want[:1]) > 10 * REL_RMS
