@@ -240,7 +240,7 @@ def bench_c4(args):
     host memory, a VRAM cache of 30 % of them warmed with each layer's most popular experts, Zipf(1.1) routing with a
     per-layer permutation over a cycle of synthetic tokens. A step is one token through the 43 layers: router, slot step
     (copies of admissions on a side stream), dispatch, gate / up of resident experts, gate / up of staged experts after
-    their copies, epilogue, down, combine."""
+    their copies, epilogue, down of resident experts, down of staged experts after their copies, combine."""
     import numpy as np
     import torch
     import bmx
@@ -321,8 +321,8 @@ def bench_c4(args):
     seq, pseq, seqs = ctypes.c_int64(), ctypes.c_int64(), [0] * NL
 
     # timeline phases of a layer call (the reference's per-layer split, engine/nv2.py:836-901): an event before each
-    PHASES = ("route", "step", "dispatch", "moe_resident", "copy_wait_gate_up", "moe_staged", "copy_wait_down",
-              "down_combine", "cpu_add")
+    PHASES = ("route", "step", "dispatch", "moe_resident", "copy_wait_gate_up", "moe_staged_act_down_resident",
+              "copy_wait_down", "down_staged_combine", "cpu_add")
 
     def token(tok, evs=None):
         s = torch.cuda.current_stream()
@@ -378,8 +378,9 @@ def bench_c4(args):
             d = ctypes.byref(descs[li])
             o = ctypes.c_void_p(out.data_ptr() + li * H * 4)
             for k, st in enumerate((bmx._lib.STAGE_GATE_UP_RESIDENT, "gu", bmx._lib.STAGE_GATE_UP_STAGED,
-                                    bmx._lib.STAGE_ACT, "dn", bmx._lib.STAGE_DOWN, bmx._lib.STAGE_COMBINE)):
-                ph = (3, 4, 5, None, 6, 7, None)[k]
+                                    bmx._lib.STAGE_ACT, bmx._lib.STAGE_DOWN_RESIDENT, "dn", bmx._lib.STAGE_DOWN_STAGED,
+                                    bmx._lib.STAGE_COMBINE)):
+                ph = (3, 4, 5, None, None, 6, 7, None)[k]
                 if ph is not None:
                     mark(li, ph)
                 if isinstance(st, str):
@@ -467,7 +468,7 @@ def bench_c4(args):
                                                                "on a side stream") + ") + "
                            + (f"guess of layer li + {AH} (router on noisy logits) + slot prefetch of up to {PF} + "
                               if PF else "")
-                           + "dispatch + gate/up (resident, then staged) + down + combine"},
+                           + "dispatch + gate/up (resident, then staged) + down (resident, then staged) + combine"},
         "us_per_token": round(ms * 1e3, 3), "us_per_layer": round(ms * 1e3 / NL, 3),
         "slot_stats_per_token": {"hits": d[0] / args.steps, "misses": d[1] / args.steps, "admitted": d[2] / args.steps,
                                  "no_victim": d[3] / args.steps, "evictions": d[4] / args.steps,

@@ -14,6 +14,7 @@ PATH_AUTO, PATH_DECODE, PATH_PREFILL, PATH_MID, PATH_SPLIT = 0, 1, 2, 3, 4
 STAGE_GATE_UP, STAGE_ACT, STAGE_DOWN, STAGE_COMBINE, STAGE_DOWN_OUT, STAGE_PREP = 0, 1, 2, 3, 4, 5
 STAGE_GATE_UP_RESIDENT, STAGE_GATE_UP_STAGED = 6, 7
 STAGE_ROUTE = 8
+STAGE_DOWN_RESIDENT, STAGE_DOWN_STAGED = 9, 10
 LANE_VRAM, LANE_ADMIT, LANE_HOME, LANE_CPU = 0, 1, 2, 3
 PLAN_MAXP, PLAN_MAXT = 64, 8
 

@@ -125,7 +125,9 @@ class MoELayer:
 
     def _run_slots(self, x, sel, rw, path):
         """Expert products with the slot table: gate / up of the experts resident before this layer's step, then (after
-        the side stream's copies of the experts it admitted) the admitted ones, then the rest of the layer."""
+        the copies of the gate / up parts of the experts it admitted) the admitted ones and the activation, the down
+        products of the resident experts while the admitted experts' down parts are still being copied, then theirs and
+        the combine."""
         T, lib = x.shape[0], L.lib()
         desc = self.slot_desc
         routes = ops.dispatch(sel, self.num_local_experts, self.routing_first, self.table.has_shared,
@@ -146,8 +148,9 @@ class MoELayer:
         self.slots.wait_copies(self.li, part="gate_up")
         stage(L.STAGE_GATE_UP_STAGED)
         stage(L.STAGE_ACT)
+        stage(L.STAGE_DOWN_RESIDENT)
         self.slots.wait_copies(self.li, part="down")
-        stage(L.STAGE_DOWN)
+        stage(L.STAGE_DOWN_STAGED)
         stage(L.STAGE_COMBINE)
         self._routes = routes
         return out

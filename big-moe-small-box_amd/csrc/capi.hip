@@ -315,10 +315,11 @@ int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T
     if (rc) return rc;
     const int p = resolve_path(path, T, desc->topk);
     if (p < 0 || T < 0) return set_error(BMX_ERR_ARG, "bmx_moe_stage: bad path or T");
-    if (stage < BMX_STAGE_GATE_UP || stage > BMX_STAGE_GATE_UP_STAGED)
+    if (stage < BMX_STAGE_GATE_UP || stage > BMX_STAGE_DOWN_STAGED || stage == BMX_STAGE_ROUTE)
         return set_error(BMX_ERR_ARG, "bmx_moe_stage: unknown stage %d", stage);
-    if ((stage == BMX_STAGE_GATE_UP_RESIDENT || stage == BMX_STAGE_GATE_UP_STAGED) && !desc->fresh)
-        return set_error(BMX_ERR_ARG, "bmx_moe_stage: split gate / up stages need desc->fresh");
+    if ((stage == BMX_STAGE_GATE_UP_RESIDENT || stage == BMX_STAGE_GATE_UP_STAGED || stage == BMX_STAGE_DOWN_RESIDENT ||
+         stage == BMX_STAGE_DOWN_STAGED) && !desc->fresh)
+        return set_error(BMX_ERR_ARG, "bmx_moe_stage: split gate / up and down stages need desc->fresh");
     if (T == 0) return BMX_OK;
     if (!routes || !workspace) return set_error(BMX_ERR_ARG, "bmx_moe_stage: null pointer");
     if ((stage == BMX_STAGE_GATE_UP || stage == BMX_STAGE_PREP || stage == BMX_STAGE_GATE_UP_RESIDENT ||

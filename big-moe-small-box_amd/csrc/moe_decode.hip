@@ -307,7 +307,7 @@ __global__ __launch_bounds__(GV_THREADS, (MX == 4 ? 4 : MX == 8 ? 3 : MX == 1 &&
     const int cb = bid % NB, g = bid / NB;
     if (g >= *a.ngroups) return;
     const int e = a.groups[3 * g], r0 = a.groups[3 * g + 1], nr = a.groups[3 * g + 2];
-    if (NM == 2 && group_skipped(a, e)) return;
+    if (group_skipped(a, e)) return;
     if (split_heavy(a, e)) return;          // split path: the mid-size kernel takes this expert's rows
     gemv_unit<MX, NM>(a, ks, cb, e, r0, nr, -1);
 }
@@ -980,8 +980,14 @@ static void launch_mr(const GvArgs& a, const DecodePlan& p, int stages, hipStrea
                                b);
     }
     if ((stages & (1 << BMX_STAGE_ACT)) && !a.act_in_down) launch_epilogue(a, BMX_STAGE_ACT, s);
-    if (stages & (1 << BMX_STAGE_DOWN))
-        hipLaunchKernelGGL((k_gemv_part<MR, 1>), dim3((unsigned)(p.G_max * p.NBH * p.KS_dn)), dim3(GV_THREADS), lds_dn, s, a);
+    for (int f = 0; f < 3; ++f)
+    {
+        const int st = f == 0 ? BMX_STAGE_DOWN : f == 1 ? BMX_STAGE_DOWN_RESIDENT : BMX_STAGE_DOWN_STAGED;
+        if (!(stages & (1 << st))) continue;
+        GvArgs b = a;
+        b.filter = f;
+        hipLaunchKernelGGL((k_gemv_part<MR, 1>), dim3((unsigned)(p.G_max * p.NBH * p.KS_dn)), dim3(GV_THREADS), lds_dn, s, b);
+    }
     if (stages & (1 << BMX_STAGE_COMBINE)) launch_epilogue(a, BMX_STAGE_COMBINE, s);
     if (stages & (1 << BMX_STAGE_DOWN_OUT)) launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
 }
@@ -1186,10 +1192,14 @@ int launch_split_experts(const MoeShape& m, const void* x, const bmx_routes* r, 
         launch_split_mid(bf, st, nu_max, s);
     }
     if (stages & (1 << BMX_STAGE_ACT)) launch_epilogue(a, BMX_STAGE_ACT, s);
-    if (stages & (1 << BMX_STAGE_DOWN))
+    for (int f = 0; f < 3; ++f)
     {
-        gemv(1 << BMX_STAGE_DOWN);
-        launch_split_mid(b, BMX_STAGE_DOWN, nu_max, s);
+        const int st = f == 0 ? BMX_STAGE_DOWN : f == 1 ? BMX_STAGE_DOWN_RESIDENT : BMX_STAGE_DOWN_STAGED;
+        if (!(stages & (1 << st))) continue;
+        gemv(1 << st);
+        GvArgs bf = b;
+        bf.filter = f;
+        launch_split_mid(bf, st, nu_max, s);
     }
     if (stages & (1 << BMX_STAGE_COMBINE)) launch_epilogue(a, BMX_STAGE_COMBINE, s);
     if (stages & (1 << BMX_STAGE_DOWN_OUT)) launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);

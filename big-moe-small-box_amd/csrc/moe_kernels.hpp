@@ -30,7 +30,7 @@ struct GvArgs {
     int T, topk, has_shared;
     uint16_t* xt;              // prefill: rotated gate / up input rows [2][R_max][H]
     const int32_t* fresh;      // [E] admitted-this-step flags of the expert-slot table, or null
-    int filter;                // gate / up groups: 0 all, 1 experts not fresh, 2 fresh experts only
+    int filter;                // gate / up or down groups: 0 all, 1 experts not fresh, 2 fresh experts only
     int act_in_down;           // the down GEMV computes its input rows from the gate / up partials (one-row groups)
     int gu_half;               // part_gu holds one split as fp16 [row][128-column block][matrix][128], each value the
                                // epilogue's own rounding of that split's sum (RN of 0.0f + product): same bits downstream
@@ -127,7 +127,7 @@ __device__ __forceinline__ void prep_unit(const GvArgs& a, long u)
     }
 }
 
-// group filter of the split gate / up stages (the shared expert, index E, is never fresh)
+// group filter of the split gate / up and down stages (the shared expert, index E, is never fresh)
 __device__ __forceinline__ bool group_skipped(const GvArgs& a, int e)
 {
     if (!a.filter) return false;

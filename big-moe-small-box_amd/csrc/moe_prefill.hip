@@ -508,7 +508,7 @@ __global__ __launch_bounds__(PF_WAVES * 64) void k_pf_gemm(GvArgs a)
     else { jb.g = lid / (2 * NB2); jb.mat = (lid / NB2) & 1; jb.cb = lid % NB2; }
     if (jb.g >= *a.ngroups) return;
     jb.e = a.groups[3 * jb.g];
-    if (!DOWN && group_skipped(a, jb.e)) return;
+    if (group_skipped(a, jb.e)) return;
     jb.r0 = a.groups[3 * jb.g + 1];
     jb.nr = a.groups[3 * jb.g + 2];
     jb.pair = 0;
@@ -677,7 +677,7 @@ __device__ __forceinline__ void mid_unit(const GvArgs& a, int lid)
         jb.e = a.uexp[u];
         const int c = a.counts[jb.e];
         if (MID_M * q >= c || !split_heavy(a, jb.e)) return;
-        if (!DOWN && group_skipped(a, jb.e)) return;
+        if (group_skipped(a, jb.e)) return;
         jb.r0 = a.offsets[jb.e] + MID_M * q;
         jb.nr = min(MID_M, c - MID_M * q);
     }
@@ -685,7 +685,7 @@ __device__ __forceinline__ void mid_unit(const GvArgs& a, int lid)
     {
         if (jb.g >= *a.ngroups) return;
         jb.e = a.groups[3 * jb.g];
-        if (!DOWN && group_skipped(a, jb.e)) return;
+        if (group_skipped(a, jb.e)) return;
         jb.r0 = a.groups[3 * jb.g + 1];
         jb.nr = a.groups[3 * jb.g + 2];
     }
@@ -869,9 +869,15 @@ int launch_mid_experts(const MoeShape& m, const void* x, const bmx_routes* r, fl
                            dim3(MID_WAVES * 64), 0, s, b);
     }
     if (stages & (1 << BMX_STAGE_ACT)) rc = launch_epilogue(a, BMX_STAGE_ACT, s);
-    if (!rc && (stages & (1 << BMX_STAGE_DOWN)))
+    for (int f = 0; f < 3 && !rc; ++f)
+    {
+        const int st = f == 0 ? BMX_STAGE_DOWN : f == 1 ? BMX_STAGE_DOWN_RESIDENT : BMX_STAGE_DOWN_STAGED;
+        if (!(stages & (1 << st))) continue;
+        GvArgs b = a;
+        b.filter = f;
         hipLaunchKernelGGL(k_mid_gemm<true>, dim3((unsigned)(p.G_max * ((p.NBH + 1) / 2) * p.KS_dn)),
-                           dim3(MID_WAVES * 64), 0, s, a);
+                           dim3(MID_WAVES * 64), 0, s, b);
+    }
     if (!rc && (stages & (1 << BMX_STAGE_COMBINE))) rc = launch_epilogue(a, BMX_STAGE_COMBINE, s);
     if (!rc && (stages & (1 << BMX_STAGE_DOWN_OUT))) rc = launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
     if (rc) return rc;
@@ -895,7 +901,7 @@ void launch_split_mid(const GvArgs& a, int stage, int nu_max, hipStream_t s)
     const long units = (long)nu_max * a.split_chunks;
     if (stage == BMX_STAGE_PREP)
         hipLaunchKernelGGL(k_pf_prep, prep_grid(a.R_max, a.H), dim3(256), 0, s, a);
-    else if (stage == BMX_STAGE_DOWN)
+    else if (stage == BMX_STAGE_DOWN || stage == BMX_STAGE_DOWN_RESIDENT || stage == BMX_STAGE_DOWN_STAGED)
         hipLaunchKernelGGL(k_mid_gemm<true>, dim3((unsigned)std::min(MID_SPLIT_WGS, units * ((a.NBH + 1) / 2) * a.KS_dn)),
                            dim3(MID_WAVES * 64), 0, s, a);
     else
@@ -958,8 +964,14 @@ int launch_prefill_experts(const MoeShape& m, const void* x, const bmx_routes* r
         hipLaunchKernelGGL(k_pf_gemm<false>, dim3((unsigned)(p.G_max * 2 * ((p.NB + 1) / 2))), dim3(PF_WAVES * 64), 0, s, b);
     }
     if (stages & (1 << BMX_STAGE_ACT)) rc = launch_epilogue(a, BMX_STAGE_ACT, s);
-    if (!rc && (stages & (1 << BMX_STAGE_DOWN)))
-        hipLaunchKernelGGL(k_pf_gemm<true>, dim3((unsigned)(p.G_max * ((p.NBH + 1) / 2))), dim3(PF_WAVES * 64), 0, s, a);
+    for (int f = 0; f < 3 && !rc; ++f)
+    {
+        const int st = f == 0 ? BMX_STAGE_DOWN : f == 1 ? BMX_STAGE_DOWN_RESIDENT : BMX_STAGE_DOWN_STAGED;
+        if (!(stages & (1 << st))) continue;
+        GvArgs b = a;
+        b.filter = f;
+        hipLaunchKernelGGL(k_pf_gemm<true>, dim3((unsigned)(p.G_max * ((p.NBH + 1) / 2))), dim3(PF_WAVES * 64), 0, s, b);
+    }
     if (!rc && (stages & (1 << BMX_STAGE_COMBINE))) rc = launch_epilogue(a, BMX_STAGE_COMBINE, s);
     if (!rc && (stages & (1 << BMX_STAGE_DOWN_OUT))) rc = launch_epilogue(a, BMX_STAGE_DOWN_OUT, s);
     if (rc) return rc;

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define BMX_ABI_VERSION 5
+#define BMX_ABI_VERSION 6
 
 typedef void* bmx_stream_t; /* hipStream_t */
 
@@ -220,7 +220,10 @@ enum bmx_stage {
     BMX_STAGE_GATE_UP_RESIDENT = 6, BMX_STAGE_GATE_UP_STAGED = 7,
     /* bmx_moe_layer_stages only: the router projection (when no logits are given), then the router and the dispatch
      * (these two are BMX_STAGE_GATE_UP's work instead where the one-token gate / up GEMV routes the token itself) */
-    BMX_STAGE_ROUTE = 8
+    BMX_STAGE_ROUTE = 8,
+    /* BMX_STAGE_DOWN split the same way (desc->fresh): the resident experts' down products can run while the admitted
+     * experts' down parts are still being copied. Together they equal BMX_STAGE_DOWN. (ABI 6) */
+    BMX_STAGE_DOWN_RESIDENT = 9, BMX_STAGE_DOWN_STAGED = 10
 };
 int bmx_moe_stage(const bmx_moe_desc* desc, int stage, const void* x_fp16, int T, const bmx_routes* routes,
                   void* act_rows_fp16, float* y_rows, const void* w_fp16, float* out, void* workspace,

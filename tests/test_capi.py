@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_host_side_checks():
     import bmx
     L = bmx.lib()
-    assert L.bmx_abi_version() == 5
+    assert L.bmx_abi_version() == 6
     assert [L.bmx_tile_bytes(f) for f in range(4)] == [64, 80, 96, 128] and L.bmx_tile_bytes(9) == -1
     assert L.bmx_exl3_dequant(None, 7, 16, 16, None, None) == bmx._lib.BMX_ERR_ARG
     assert b"format" in L.bmx_last_error()
@@ -91,3 +91,23 @@ def test_layer_stages_mask_checks():
     ok = (1 << B.STAGE_ROUTE) | (1 << B.STAGE_GATE_UP)
     assert L.bmx_moe_layer_stages(ctypes.byref(d), ctypes.byref(r), None, None, 0, None, None, None, None, 0, 0, ok,
                                   None) == 0
+
+
+def test_moe_stage_checks():
+    """bmx_moe_stage refuses unknown stages (and BMX_STAGE_ROUTE, which only bmx_moe_layer_stages runs) and the split
+    gate / up and down stages without desc->fresh, before any device work; a zero-token call of a known stage does
+    nothing."""
+    import bmx
+    B = bmx._lib
+    L = bmx.lib()
+    d = B.MoeDesc(4096, 1536, 288, 8, 0, 0, 1, 0.0, ctypes.c_void_p(1), ctypes.c_void_p(2))
+    args = (None, 0, None, None, None, None, None, None, 0, 1, None)
+    for st in (-1, B.STAGE_ROUTE, B.STAGE_DOWN_STAGED + 1):
+        assert L.bmx_moe_stage(ctypes.byref(d), st, *args) == B.BMX_ERR_ARG
+        assert b"unknown stage" in L.bmx_last_error()
+    for st in (B.STAGE_GATE_UP_RESIDENT, B.STAGE_GATE_UP_STAGED, B.STAGE_DOWN_RESIDENT, B.STAGE_DOWN_STAGED):
+        assert L.bmx_moe_stage(ctypes.byref(d), st, *args) == B.BMX_ERR_ARG
+        assert b"desc->fresh" in L.bmx_last_error()
+    d.fresh = ctypes.c_void_p(3)
+    for st in (B.STAGE_GATE_UP, B.STAGE_DOWN, B.STAGE_DOWN_RESIDENT, B.STAGE_DOWN_STAGED, B.STAGE_COMBINE):
+        assert L.bmx_moe_stage(ctypes.byref(d), st, *args) == 0
