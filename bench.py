@@ -282,6 +282,7 @@ def bench_c4(args):
     slots = bmx.ExpertSlots(layers, S, maxj=16, copies=args.copies)
     DMA = args.copies == "dma"
     CPUL = args.cpu_lane > 0 and DMA
+    FUSED = not CPUL and not args.separate_route_step     # routing + slot step in one launch (bmx_route_slot_step)
     if CPUL:
         # planned steps: the agent's planner puts misses on the CPU lane (fast mode, args.cpu_lane worker threads, reading
         # its own huge-page copy of the homes) when its estimated finish is no later than the GPU's; the GPU costs are
@@ -331,10 +332,28 @@ def bench_c4(args):
         for li in range(NL):
             mark(li, 0)
             lgp = ctypes.c_void_p(lg_all.data_ptr() + (li * NTOK + tok) * E * 2)
-            bmx._lib.check(L.bmx_router_topk(lgp, P(biases[li]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0, P(sel),
-                                             P(w), sp), "router")
-            mark(li, 1)
-            if CPUL:
+            if FUSED:
+                # the routing and the step in one launch: the route phase holds both, the step phase reads ~0
+                bmx._lib.check(L.bmx_route_slot_step(tstruct, slots.agent if DMA else None, li, lgp, P(biases[li]), E,
+                                                     topk, 1, 1, c["score"], 1, c["scale"], 0, 1, P(sel), P(w),
+                                                     ctypes.byref(seq), sp), "route + slot step")
+                mark(li, 1)
+                if DMA:
+                    seqs[li] = seq.value
+            else:
+                bmx._lib.check(L.bmx_router_topk(lgp, P(biases[li]), 1, E, topk, 1, 1, c["score"], 1, c["scale"], 0,
+                                                 P(sel), P(w), sp), "router")
+                mark(li, 1)
+            if FUSED and DMA:
+                pass
+            elif FUSED:
+                stepped[li].record(s)
+                side.wait_event(stepped[li])
+                bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 3, ctypes.c_void_p(side.cuda_stream)), "slot copy")
+                copied_gu[li].record(side)
+                bmx._lib.check(L.bmx_slot_copy_mats(tstruct, li, 4, ctypes.c_void_p(side.cuda_stream)), "slot copy")
+                copied_dn[li].record(side)
+            elif CPUL:
                 bmx._lib.check(L.bmx_slot_step_planned(tstruct, slots.agent, li, P(sel), P(w), 1, topk, 0, 1, P(x),
                                                        P(sel_g), P(w_g), None, ctypes.byref(seq), sp), "planned step")
                 seqs[li] = seq.value
@@ -431,7 +450,8 @@ def bench_c4(args):
                 "timing": "timing-only events (no system-scope release) on the compute stream before each phase of every "
                           "layer call, in a separate loop of the same tokens; copy_wait_* is the time the stream spends "
                           "in the one-lane kernel waiting for the copies of the layer's admissions (the part of the copy "
-                          "no compute hides)"}
+                          "no compute hides)" + ("; the router and the slot step are one launch, timed as route (step "
+                                                 "reads the events' own cost)" if FUSED else "")}
     log(f"bench c4: timeline {timeline['parts_us_mean']}")
     h2d = measure_h2d()
     link = staged / (ms * 1e-3 * args.steps) / 1e9
@@ -464,8 +484,8 @@ def bench_c4(args):
         "config": {"workload": f"c4 decode stack: {NL} layers of {E} routed experts top-{topk} sigmoid+bias + 1 shared (in "
                                f"VRAM), H {H}, I {I}, EXL3 3 bpw; expert-slot table of {S} VRAM slots (30 %) warmed with each "
                                f"layer's top {per} experts by popularity", "tokens": 1, "layers": NL, "path": "decode",
-                   "step": "per layer: router + slot step (copies " + ("by the copy agent on the DMA engines" if DMA else
-                                                               "on a side stream") + ") + "
+                   "step": "per layer: router + slot step" + (" (one launch)" if FUSED else "") + " (copies "
+                           + ("by the copy agent on the DMA engines" if DMA else "on a side stream") + ") + "
                            + (f"guess of layer li + {AH} (router on noisy logits) + slot prefetch of up to {PF} + "
                               if PF else "")
                            + "dispatch + gate/up (resident, then staged) + down (resident, then staged) + combine"},
@@ -887,6 +907,8 @@ def main():
     ap.add_argument("--cpu-lane", type=int, default=0, metavar="THREADS",
                     help="c4: planned steps with the CPU lane (fast mode) on THREADS worker threads (0: off)")
     ap.add_argument("--cpu-max", type=int, default=2, help="c4 --cpu-lane: most misses a layer call puts on the CPU")
+    ap.add_argument("--separate-route-step", action="store_true",
+                    help="c4: the router and the slot step as two launches (default: one, bmx_route_slot_step)")
     ap.add_argument("--cpu-expert-us", type=float, default=125.0,
                     help="c4 --cpu-lane: the planner's CPU cost of one expert until the lane's first job is timed")
     ap.add_argument("--timeline-steps", type=int, default=10, help="c4: tokens of the per-layer timeline loop")

@@ -101,6 +101,8 @@ SIGNATURES = {
     "bmx_copy_agent_status": (_I, [_P, _P]),
     "bmx_copy_agent_control": (_I, [_P, _I, _I64]),
     "bmx_slot_step_agent": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _I, _I64, _I, ctypes.POINTER(_I64), _P]),
+    "bmx_route_slot_step": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, ctypes.c_float, _I64,
+                                 _I, _P, _P, ctypes.POINTER(_I64), _P]),
     "bmx_slot_prefetch_agent": (_I, [ctypes.POINTER(SlotTable), _P, _I, _P, _I, _I64, _I, ctypes.POINTER(_I64), _P]),
     "bmx_copy_wait": (_I, [_P, _I64, _I, _P]),
     "bmx_copy_wait_layer": (_I, [_P, _I, _I, _P]),

@@ -144,6 +144,10 @@ class ExpertSlots:
             cur.wait_event(self.last_copied)
         L.check(L.lib().bmx_slot_step(ctypes.byref(self.struct), li, ctypes.c_void_p(sel.data_ptr()), sel.numel(),
                                       int(first), int(admit), ctypes.c_void_p(cur.cuda_stream)), "bmx_slot_step")
+        return self._copy_after_step(li, cur)
+
+    def _copy_after_step(self, li, cur):
+        """The copies of a plain step's admissions on the side stream, after the step on stream cur."""
         stepped = torch.cuda.Event()
         stepped.record(cur)
         self.side.wait_event(stepped)
@@ -157,6 +161,35 @@ class ExpertSlots:
         self.copied[li] = tuple(evs)
         self.last_copied = evs[1]
         return evs[1]
+
+    def route_step(self, li, logits, topk, bias=None, n_group=1, topk_group=1, score=L.SCORE_SIGMOID, renorm=True,
+                   scale=1.0, admit=True, *, first=None):
+        """One token's routing and the step of layer li in one launch (bmx_route_slot_step): the same picks, weights
+        and table state as ops.router_topk followed by step(li, sel, admit). logits fp16 [1, E] or [E] (device).
+        Returns (sel int64 [1, topk], w fp16 [1, topk])."""
+        if logits.dtype != torch.float16 or not logits.is_contiguous():
+            logits = logits.half().contiguous()
+        E = logits.numel()
+        if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous()):
+            bias = bias.float().contiguous()
+        first = self.first if first is None else int(first)
+        sel = torch.empty((1, topk), dtype=torch.int64, device=logits.device)
+        w = torch.empty((1, topk), dtype=torch.float16, device=logits.device)
+        cur = torch.cuda.current_stream()
+        P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+        if self.agent is None and self.last_copied is not None:   # the previous step's copies read the job buffer
+            cur.wait_event(self.last_copied)
+        q = ctypes.c_int64()
+        L.check(L.lib().bmx_route_slot_step(ctypes.byref(self.struct), self.agent, li, P(logits), P(bias), E, topk,
+                                            n_group, topk_group, score, int(renorm), float(scale), first, int(admit),
+                                            P(sel), P(w), ctypes.byref(q), ctypes.c_void_p(cur.cuda_stream)),
+                "bmx_route_slot_step")
+        if self.agent is not None:
+            self.seq[li] = q.value
+            self.last_seq = max(self.last_seq, q.value)
+            return sel, w
+        self._copy_after_step(li, cur)
+        return sel, w
 
     def prefetch(self, li, guess, limit=None, *, first=None):
         """Layer-ahead prefetch into layer li's slots: the first `limit` (default maxj) distinct guesses (int64 device

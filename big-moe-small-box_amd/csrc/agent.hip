@@ -692,6 +692,27 @@ int bmx_slot_step_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, cons
     return BMX_OK;
 }
 
+int bmx_route_slot_step(const bmx_slot_table* t, bmx_copy_agent* a, int li, const void* logits_fp16, const float* bias,
+                        int E, int topk, int n_group, int topk_group, int score_fn, int renorm, float scale, int64_t first,
+                        int admit, int64_t* sel, void* w_fp16, int64_t* seq, bmx_stream_t stream)
+{
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!a)
+        return launch_route_slot_step(t, li, logits_fp16, bias, E, topk, n_group, topk_group, score_fn, renorm, scale,
+                                      first, sel, w_fp16, admit, s, nullptr, 0, nullptr, 0);
+    if (!seq) return set_error(BMX_ERR_ARG, "bmx_route_slot_step: null seq with an agent");
+    if (li < 0 || li >= a->t.L) return set_error(BMX_ERR_ARG, "bmx_route_slot_step: bad layer %d", li);
+    const int64_t q = a->next_seq + 1;
+    int rc = agent_failure(a, "bmx_route_slot_step");
+    if (rc) return rc;
+    rc = launch_route_slot_step(t, li, logits_fp16, bias, E, topk, n_group, topk_group, score_fn, renorm, scale, first,
+                                sel, w_fp16, admit, s, a->sh_dev, q, a->need, a->wait_ticks);
+    if (rc) return rc;
+    a->next_seq = q;
+    *seq = q;
+    return BMX_OK;
+}
+
 int bmx_slot_prefetch_agent(const bmx_slot_table* t, bmx_copy_agent* a, int li, const int64_t* sel, int n,
                             int64_t first, int limit, int64_t* seq, bmx_stream_t stream)
 {

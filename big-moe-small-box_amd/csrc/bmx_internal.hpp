@@ -126,6 +126,14 @@ struct PlanArgs {
     uint16_t* w_gpu;
     int32_t* lanes;
 };
+// router argument checks (bmx_router_topk's), for the entries that route inside other kernels
+int check_router(int T, int E, int topk, int n_group, int topk_group, int score_fn, const void* logits, const void* sel,
+                 const void* w);
+// one token's routing and the slot-table step of layer li in one launch (sh: the copy agent's ring, or null)
+int launch_route_slot_step(const bmx_slot_table* t, int li, const void* logits, const float* bias, int E, int topk,
+                           int n_group, int topk_group, int score_fn, int renorm, float scale, int64_t first, int64_t* sel,
+                           void* w, int admit, hipStream_t s, AgentShared* sh, int64_t seq, int64_t* need,
+                           int64_t wait_limit);
 // Publishing (sh != null): the step writes ring[seq % AG_RING] once the agent has consumed record seq - AG_RING, waiting
 // at most wait_limit wall-clock ticks (then it sets flags[3]). need (steps only): need[li] = the last record layer li's
 // next products depend on (seq when the step admitted experts, seq - 1 when it did not: its prefetched hits came with

@@ -143,7 +143,7 @@ __global__ __launch_bounds__(RT_THREADS) void k_route_dispatch_small(RouterArgs 
     }
 }
 
-static int check_router(int T, int E, int topk, int n_group, int topk_group, int score_fn, const void* logits,
+int check_router(int T, int E, int topk, int n_group, int topk_group, int score_fn, const void* logits,
                         const void* sel, const void* w)
 {
     if (T < 0 || E <= 0 || E > RT_MAXE || topk <= 0 || topk > RT_MAXK || topk > E)

@@ -6,6 +6,7 @@
 
 #include "bmx_common.hpp"
 #include "bmx_internal.hpp"
+#include "router_wave.hpp"
 
 namespace bmx {
 
@@ -197,7 +198,8 @@ __device__ int plan_step(const SlotArgs& a, const uint32_t* mark, const int32_t*
     return ok;
 }
 
-__global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
+// The step of one workgroup of SL_THREADS threads (k_slot_step, and k_route_slot_step after its routing wave).
+__device__ __forceinline__ void slot_step_body(const SlotArgs& a)
 {
     __shared__ int32_t pin[SL_MAXS];
     __shared__ int32_t refb[SL_MAXS];
@@ -205,7 +207,7 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
     __shared__ int32_t miss[512];
     __shared__ int32_t first_at[512];
     __shared__ int wave_cnt[SL_THREADS / 64];
-    __shared__ int n_hit, n_pfused, n_missall, s_ok;
+    __shared__ int n_hit, n_pfused, n_missall, s_ok, ring_ok;
     __shared__ int32_t ecnt[512];        // planned step: picks per expert
     __shared__ int32_t elane[512];       // planned step: lane per expert
     __shared__ int32_t uq[512];          // planned step: the picked experts, ascending
@@ -226,6 +228,9 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
         elane[tid] = BMX_LANE_VRAM;
     }
     if (tid == 0) n_hit = n_pfused = n_missall = 0;
+    // the ring slot check of a publishing step (a round trip to the agent's count in host memory, and a bounded wait if
+    // the agent is a ring behind) by the last wave, beside the other waves' work; read after the barriers below
+    if (a.sh && !a.plan && tid == SL_THREADS - 64) ring_ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
     __syncthreads();
     int32_t* slotof = t.slotof + (size_t)a.li * E;
     int nmiss;
@@ -304,7 +309,7 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
             // this step sees runs from its home, and publish nothing
             int ok = 0;
             if (a.plan) ok = s_ok;           // the planned step has waited for its ring slot and its reply
-            else if (lane == 0) ok = ring_slot_free(a.sh, a.seq, a.wait_limit) ? 1 : 0;
+            else ok = ring_ok;
             if (__shfl(ok, 0)) pub = &a.sh->ring[ring_index(a.seq)];
             else admit = 0;
         }
@@ -415,6 +420,22 @@ __global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
         t.pin[s] = pin[s];
         t.refb[s] = refb[s];
     }
+}
+
+__global__ __launch_bounds__(SL_THREADS) void k_slot_step(SlotArgs a)
+{
+    slot_step_body(a);
+}
+
+// A one-token layer call's routing and its step in one launch: wave 0 routes the token (writes sel / w, the picks the
+// step reads after its first barrier) while the other waves load the slot state into LDS; then the step. The same
+// picks, weights and table state as k_router followed by k_slot_step.
+template <int J>
+__global__ __launch_bounds__(SL_THREADS) void k_route_slot_step(RouterArgs ra, SlotArgs a)
+{
+    __shared__ TopkLds tl;
+    if ((threadIdx.x >> 6) == 0) route_token_wave<J>(ra, 0, tl);
+    slot_step_body(a);
 }
 
 // copies of the last step's admissions (buf < 0) or of prefetch buffer buf: blockIdx.y = job; the matrices in `mats`
@@ -537,6 +558,52 @@ int launch_slot_step(const bmx_slot_table* t, int li, const int64_t* sel, int n,
     }
     hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(SL_THREADS), 0, s, a);
     return check_launch(plan ? "bmx_slot_step_planned" : "bmx_slot_step");
+}
+
+int launch_route_slot_step(const bmx_slot_table* t, int li, const void* logits, const float* bias, int E, int topk,
+                           int n_group, int topk_group, int score_fn, int renorm, float scale, int64_t first, int64_t* sel,
+                           void* w, int admit, hipStream_t s, AgentShared* sh, int64_t seq, int64_t* need,
+                           int64_t wait_limit)
+{
+    int rc = check_table(t, "bmx_route_slot_step");
+    if (rc) return rc;
+    if (li < 0 || li >= t->L) return set_error(BMX_ERR_ARG, "bmx_route_slot_step: bad layer %d", li);
+    if (E != t->E || E > SL_THREADS)
+        return set_error(BMX_ERR_ARG, "bmx_route_slot_step: the router's %d experts are not the table's %d", E, t->E);
+    rc = check_router(1, E, topk, n_group, topk_group, score_fn, logits, sel, w);
+    if (rc) return rc;
+    RouterArgs ra;
+    ra.logits = static_cast<const uint16_t*>(logits); ra.bias = bias; ra.T = 1; ra.E = E; ra.topk = topk;
+    ra.G = n_group; ra.TG = topk_group; ra.score_fn = score_fn; ra.renorm = renorm; ra.scale = scale; ra.first = first;
+    ra.sel = sel; ra.w = static_cast<uint16_t*>(w);
+    SlotArgs a;
+    a.t = *t;
+    a.sel = ra.sel;
+    a.first = ra.first;
+    a.li = li;
+    a.n = ra.topk;
+    a.admit = admit ? 1 : 0;
+    a.pf = 0;
+    a.limit = 0;
+    a.buf = 0;
+    a.sh = sh;
+    a.seq = seq;
+    a.need = need;
+    a.wait_limit = wait_limit;
+    a.plan = 0;
+    a.pl = PlanArgs{};
+    const dim3 g(1), b(SL_THREADS);
+    switch ((ra.E + 63) / 64)
+    {
+        case 1: hipLaunchKernelGGL(k_route_slot_step<1>, g, b, 0, s, ra, a); break;
+        case 2: hipLaunchKernelGGL(k_route_slot_step<2>, g, b, 0, s, ra, a); break;
+        case 3: hipLaunchKernelGGL(k_route_slot_step<3>, g, b, 0, s, ra, a); break;
+        case 4: hipLaunchKernelGGL(k_route_slot_step<4>, g, b, 0, s, ra, a); break;
+        case 5: hipLaunchKernelGGL(k_route_slot_step<5>, g, b, 0, s, ra, a); break;
+        case 6: hipLaunchKernelGGL(k_route_slot_step<6>, g, b, 0, s, ra, a); break;
+        default: hipLaunchKernelGGL(k_route_slot_step<8>, g, b, 0, s, ra, a); break;
+    }
+    return check_launch("bmx_route_slot_step");
 }
 
 int launch_slot_prefetch(const bmx_slot_table* t, int li, const int64_t* sel, int n, int64_t first, int limit, int buf,

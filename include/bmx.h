@@ -329,6 +329,15 @@ int bmx_slot_step_agent(const bmx_slot_table* t, bmx_copy_agent* agent, int li, 
                         int64_t first, int admit, int64_t* seq, bmx_stream_t stream);
 int bmx_slot_prefetch_agent(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const int64_t* sel, int n,
                             int64_t first, int limit, int64_t* seq, bmx_stream_t stream);
+/* A one-token layer call's routing (bmx_router_topk with T = 1; E = the table's experts) and its slot-table step
+ * (bmx_slot_step_agent with the token's topk picks, or bmx_slot_step when agent is NULL; seq is then not written) in
+ * one launch: the reference's routing_fn followed by the step of Nv2.layer (engine/nv2.py:470-487, then
+ * engine/kernels/nv2/nv2_dev.cu:221-367 nv_step_k), whose two kernels this replaces for one token. The step's loads of
+ * the slot state run beside the routing. Picks, weights and table state are those of the two calls. (ABI 6) */
+int bmx_route_slot_step(const bmx_slot_table* t, bmx_copy_agent* agent, int li, const void* logits_fp16,
+                        const float* bias, int E, int topk, int n_group, int topk_group, int score_fn, int renorm,
+                        float scale, int64_t first, int admit, int64_t* sel, void* w_fp16, int64_t* seq,
+                        bmx_stream_t stream);
 int bmx_copy_wait(bmx_copy_agent* agent, int64_t seq, int part, bmx_stream_t stream);
 /* Orders a stream after what layer li's products need from the copies (part 0 gate / up, 1 down): its last step's
  * record when that step admitted experts, else the records before it (the prefetches its hits came from); the step

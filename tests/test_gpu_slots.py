@@ -321,3 +321,41 @@ def test_agent_failure_is_reported(cuda):
         slots.wait_copies(0)
     bmx._lib.check(lib.bmx_copy_agent_control(slots.agent, 0, 0), "bmx_copy_agent_control")
     slots.close()
+
+
+@pytest.mark.parametrize("E,copies", [(40, "kernel"), (288, "dma")])
+def test_route_slot_step_matches_separate(cuda, E, copies):
+    """bmx_route_slot_step (one token's routing and the step in one launch) against bmx_router_topk followed by the step
+    on a twin table: the same picks and weights, and the same slot state, fresh flags, counters and jobs after every
+    call; the admitted experts' slots then hold their homes' bytes."""
+    import bmx
+    Lyr, S, topk = 3, 20, 8
+    a_layers = small_layers(Lyr, E, 256, 128, 60, "host")
+    b_layers = small_layers(Lyr, E, 256, 128, 60, "host")
+    sa = bmx.ExpertSlots(a_layers, S, maxj=4, copies=copies)
+    sb = bmx.ExpertSlots(b_layers, S, maxj=4, copies=copies)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(61)
+    bias = (torch.randn(E, generator=g, device=cuda) * 0.1).float()
+    rng = np.random.default_rng(62)
+    for step in range(24):
+        li = int(rng.integers(0, Lyr))
+        admit = bool(rng.random() < 0.85)
+        lg = torch.randn((1, E), generator=g, device=cuda).half()
+        say("route step", step, "layer", li, "admit", admit)
+        sel, w = bmx.ops.router_topk(lg, topk, bias, 1, 1, bmx.SCORE_SIGMOID, True, 2.5)
+        sa.step(li, sel.view(-1), admit)
+        sel_b, w_b = sb.route_step(li, lg, topk, bias, 1, 1, bmx.SCORE_SIGMOID, True, 2.5, admit)
+        torch.cuda.synchronize()
+        assert torch.equal(sel, sel_b) and torch.equal(w, w_b), step
+        for name in ("slotof", "owner", "refb", "pin", "ctl", "stats_t", "fresh", "pfl"):
+            assert torch.equal(getattr(sa, name), getattr(sb, name)), (step, name)
+        nj = int(sa.ctl[2].item())
+        assert torch.equal(sa.jobs[:2 * nj], sb.jobs[:2 * nj]), step
+    for li in range(Lyr):
+        sa.wait_copies(li)
+        sb.wait_copies(li)
+    torch.cuda.synchronize()
+    assert resident_bytes_match(sb, b_layers) == resident_bytes_match(sa, a_layers) > 0
+    sa.close()
+    sb.close()
