@@ -111,3 +111,26 @@ def test_moe_stage_checks():
     d.fresh = ctypes.c_void_p(3)
     for st in (B.STAGE_GATE_UP, B.STAGE_DOWN, B.STAGE_DOWN_RESIDENT, B.STAGE_DOWN_STAGED, B.STAGE_COMBINE):
         assert L.bmx_moe_stage(ctypes.byref(d), st, *args) == 0
+
+
+def test_route_slot_step_checks():
+    """bmx_route_slot_step refuses, on the host and before any launch: a table that fails the step's checks, a bad
+    layer, a router over another expert count than the table's, and the router's own unsupported sizes."""
+    import bmx
+    B = bmx._lib
+    L = bmx.lib()
+    dummy = [ctypes.c_void_p(16 * (i + 1)) for i in range(13)]
+    t = B.SlotTable(2, 40, 8, 4, 256, 128, 49152, 16384, 32768, *dummy)
+    lg, sel, w = ctypes.c_void_p(16), ctypes.c_void_p(32), ctypes.c_void_p(48)
+    seq = ctypes.c_int64()
+
+    def call(tab, li=0, E=40, topk=8, n_group=1, topk_group=1):
+        return L.bmx_route_slot_step(ctypes.byref(tab), None, li, lg, None, E, topk, n_group, topk_group,
+                                     bmx.SCORE_SIGMOID, 1, 1.0, 0, 1, sel, w, ctypes.byref(seq), None)
+
+    bad = B.SlotTable(2, 40, 8, 4, 256, 128, 49152, 16384, 32768, *([None] * 13))
+    assert call(bad) == B.BMX_ERR_ARG and b"null table array" in L.bmx_last_error()
+    assert call(t, li=2) == B.BMX_ERR_ARG and b"bad layer" in L.bmx_last_error()
+    assert call(t, E=48) == B.BMX_ERR_ARG and b"not the table's" in L.bmx_last_error()
+    assert call(t, topk=41) == B.BMX_ERR_ARG and b"unsupported sizes" in L.bmx_last_error()
+    assert call(t, n_group=3) == B.BMX_ERR_ARG and b"bad groups" in L.bmx_last_error()
