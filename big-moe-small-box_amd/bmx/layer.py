@@ -94,6 +94,25 @@ class MoELayer:
         self.slots.step(li, sel, True, first=self.routing_first)
         return sel, w, False
 
+    def route_layer(self, li, z, bsz, params=None):
+        """routing_fn followed by layer() (the reference's routing hook, then the step of Nv2.layer): for a one-token
+        call on a slot table that is not planned, both in one launch (ExpertSlots.route_step, bmx_route_slot_step: the
+        same picks, weights and table state); other calls run the two hooks. Returns (sel, w, cpu_job) as layer()."""
+        if self.slots is None or bsz != 1 or getattr(self.slots, "planned", False):
+            sel, w = self.routing_fn(bsz, None, z, params)
+            return self.layer(li, sel, w, z, bsz)
+        logits = params.get("logits") if params else None
+        if logits is None:
+            logits = self.router_logits(z)
+        self._cpu_seq = None
+        self._staged = None
+        if getattr(self.slots, "st_open", False):
+            self.slots.stage_end()          # a one-token call ends a staged forward, as in layer()
+        sel, w = self.slots.route_step(li, logits.reshape(-1), self.num_experts_per_tok, self.bias, self.n_group,
+                                       self.topk_group, self.score, self.renorm, self.scale, True,
+                                       first=self.routing_first)
+        return sel, w, False
+
     # ---- experts + combine ----
     def run_bszN(self, z, sel, rw, path=L.PATH_AUTO):
         x = z.view(-1, self.hidden_size)

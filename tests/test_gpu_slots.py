@@ -207,7 +207,7 @@ def test_layer_with_staged_experts_matches_resident(cuda, copies):
     """The same layers computed with every expert resident in device memory and with homes in pinned host memory staged
     through a small slot table (hits, admissions copied on the side stream by a kernel or by the copy agent on the DMA
     engines, and misses left at home when maxj runs out): identical outputs, bit for bit, on the GEMV, mid-size and
-    prefill paths."""
+    prefill paths. One-token calls route and step in one launch (MoELayer.route_layer)."""
     import bmx
     from bmx import synth
     Lyr, E, H, I, topk = 3, 24, 512, 256, 4
@@ -226,8 +226,11 @@ def test_layer_with_staged_experts_matches_resident(cuda, copies):
         for path in (bmx.PATH_DECODE, bmx.PATH_MID, bmx.PATH_PREFILL):
             sel, w = ref_layers[li].routing_fn(T, None, x, {"logits": lg})
             want = ref_layers[li].run_bszN(x, sel, w, path)
-            sel2, w2 = st_layers[li].routing_fn(T, None, x, {"logits": lg})
-            st_layers[li].layer(li, sel2, w2, x, T)
+            if T == 1:      # the routing and the step in one launch
+                sel2, w2, _ = st_layers[li].route_layer(li, x, T, {"logits": lg})
+            else:
+                sel2, w2 = st_layers[li].routing_fn(T, None, x, {"logits": lg})
+                st_layers[li].layer(li, sel2, w2, x, T)
             got = st_layers[li].run_bszN(x, sel2, w2, path)
             torch.cuda.synchronize()
             say("staged layer step", step, "layer", li, "T", T, "path", path, "stats", slots.stats())
